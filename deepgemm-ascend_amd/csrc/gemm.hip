@@ -1,0 +1,243 @@
+// Host side of the GEMM family: argument checks, tile-shape heuristic, launch.
+//
+// Replaces the reference's launch_fp8_gemm / launch_fp4_gemm / launch_fp8_dequant_gemm /
+// launch_bf16_gemm (csrc/jit_kernels/fp8_gemm.hpp:11-151, fp8_dequant_gemm.hpp:24-95,
+// bf16_gemm.hpp:16-78) and its select_gemm_config cost model
+// (csrc/jit_kernels/heuristics.hpp:592-755).  Kernels are compiled ahead of time for a
+// fixed menu of tile shapes; the heuristic scores each shape with a gfx950 model
+// (256 CUs, waves-of-tiles quantisation, LDS-read efficiency of the wave tile) and memoises
+// the choice per problem signature.
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "gemm_tiles.hpp"
+#include "../../include/deep_gemm_amd.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+}  // namespace
+
+extern "C" int dg_set_error(const char* msg) {
+    g_last_error = msg;
+    return DG_EINVAL;
+}
+
+extern "C" const char* dg_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" const char* dg_version(void) { return "deep_gemm_amd 0.1.0 (gfx950)"; }
+
+extern "C" int dg_device_num_cus(int32_t device) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
+        dg_set_error("hipDeviceGetAttribute(MultiprocessorCount) failed");
+        return DG_ELAUNCH;
+    }
+    return n;
+}
+
+namespace dg {
+
+KernelFn lookup_kernel(int kind, int bm, int bn) {
+    switch (kind) {
+        case kFP8FP8: return lookup_kernel_fp8fp8(bm, bn);
+        case kFP8FP4: return lookup_kernel_fp8fp4(bm, bn);
+        case kFP4FP4: return lookup_kernel_fp4fp4(bm, bn);
+        case kBF16: return lookup_kernel_bf16(bm, bn);
+        default: return nullptr;
+    }
+}
+
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// Relative efficiency of a wave tile: LDS bytes read per MFMA flop falls with the wave
+// tile's (WM * WN) / (WM + WN); 128 x 128 wave tiles keep LDS below the MFMA rate.
+double tile_efficiency(int bm, int bn) {
+    const double wm = bm / 2.0, wn = bn / 2.0;
+    const double ratio = (wm * wn) / (wm + wn) / 64.0;
+    return ratio >= 1.0 ? 1.0 : ratio;
+}
+
+bool tile_allowed(const dg_gemm_args& a, int bm, int bn) {
+    if (a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) {
+        if (a.alignment % bm != 0) return false;
+    }
+    (void)bn;
+    return true;
+}
+
+TileCfg select_tile(const dg_gemm_args& a, int cus) {
+    const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
+    double best = 1e300;
+    TileCfg pick = {0, 0};
+    for (int i = 0; i < kNumTiles; ++i) {
+        const int bm = kTiles[i].bm, bn = kTiles[i].bn;
+        if (!tile_allowed(a, bm, bn)) continue;
+        const int64_t tiles = (int64_t)ceil_div(a.m, bm) * ceil_div(a.n, bn) * groups;
+        const int64_t rounds = ceil_div64(tiles, cus);
+        // compute term: padded tile flops at the tile's efficiency
+        const double t_mma = (double)rounds * bm * bn / tile_efficiency(bm, bn);
+        // memory term: operand bytes streamed per round per CU (L2-level), weighted lightly
+        const double t_mem = (double)rounds * (bm + bn) * 40.0;
+        const double t = t_mma + t_mem;
+        if (t < best * 0.999) {
+            best = t;
+            pick = kTiles[i];
+        }
+    }
+    return pick;
+}
+
+struct MemoKey {
+    int kind, type, m, n, k, g, cus, align;
+    bool operator==(const MemoKey& o) const { return memcmp(this, &o, sizeof(*this)) == 0; }
+};
+struct MemoHash {
+    size_t operator()(const MemoKey& k) const {
+        size_t h = 1469598103934665603ull;
+        const unsigned char* p = reinterpret_cast<const unsigned char*>(&k);
+        for (size_t i = 0; i < sizeof(k); ++i) h = (h ^ p[i]) * 1099511628211ull;
+        return h;
+    }
+};
+
+std::mutex g_memo_mu;
+std::unordered_map<MemoKey, TileCfg, MemoHash> g_memo;
+
+TileCfg choose(const dg_gemm_args& a, int cus) {
+    if (a.block_m > 0 && a.block_n > 0) return {a.block_m, a.block_n};
+    MemoKey key;
+    memset(&key, 0, sizeof(key));
+    key.kind = a.kind; key.type = a.gemm_type; key.m = a.m; key.n = a.n; key.k = a.k;
+    key.g = a.num_groups; key.cus = cus; key.align = a.alignment;
+    std::lock_guard<std::mutex> lk(g_memo_mu);
+    auto it = g_memo.find(key);
+    if (it != g_memo.end()) return it->second;
+    const TileCfg c = select_tile(a, cus);
+    g_memo.emplace(key, c);
+    return c;
+}
+
+int elem_bytes_times2(int kind, bool is_a) {
+    // storage bytes per 2 logical K elements
+    switch (kind) {
+        case kFP8FP8: return 2;
+        case kFP8FP4: return is_a ? 2 : 1;
+        case kFP4FP4: return 1;
+        case kBF16: return 4;
+    }
+    return 0;
+}
+
+}  // namespace dg
+
+extern "C" int dg_select_config(const dg_gemm_args* args, int32_t* block_m, int32_t* block_n) {
+    if (args == nullptr) return dg_set_error("dg_select_config: null args");
+    const int cus = args->num_cus > 0 ? args->num_cus : dg::device_cus();
+    const dg::TileCfg c = dg::choose(*args, cus);
+    if (c.bm == 0) return dg_set_error("no tile shape fits this problem (M-grouped alignment must be a multiple of 32)");
+    if (block_m) *block_m = c.bm;
+    if (block_n) *block_n = c.bn;
+    return DG_OK;
+}
+
+extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
+    using namespace dg;
+    if (args == nullptr) return dg_set_error("dg_gemm: null args");
+    const dg_gemm_args& a = *args;
+    if (a.kind < kFP8FP8 || a.kind > kBF16) return dg_set_error("dg_gemm: unknown kind");
+    if (a.gemm_type < kNormal || a.gemm_type > kMasked) return dg_set_error("dg_gemm: unknown gemm_type");
+    if (a.m < 0 || a.n < 0 || a.k < 0) return dg_set_error("dg_gemm: negative size");
+    if (a.d_dtype != DG_DTYPE_BF16 && a.d_dtype != DG_DTYPE_F32) return dg_set_error("dg_gemm: D must be bf16 or fp32");
+    if (a.m == 0 || a.n == 0) return DG_OK;
+    const bool bf16 = a.kind == kBF16;
+    if (a.a == nullptr || a.b == nullptr || a.d == nullptr) return dg_set_error("dg_gemm: null operand");
+    if (!bf16 && (a.sfa == nullptr || a.sfb == nullptr)) return dg_set_error("dg_gemm: scale factors required");
+    const bool grouped = a.gemm_type != kNormal;
+    if ((a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx || a.gemm_type == kMasked) &&
+        a.grouped_layout == nullptr)
+        return dg_set_error("dg_gemm: grouped_layout required");
+    if (grouped && a.num_groups < 1) return dg_set_error("dg_gemm: num_groups must be >= 1");
+    if (grouped && a.accumulate && a.gemm_type != kBatched)
+        return dg_set_error("dg_gemm: grouped GEMMs do not accumulate");
+    // storage bytes of one K row
+    const int64_t kbytes_a = (int64_t)a.k * elem_bytes_times2(a.kind, true) / 2;
+    const int64_t kbytes_b = (int64_t)a.k * elem_bytes_times2(a.kind, false) / 2;
+    const int64_t esz_a = bf16 ? 2 : 1, esz_b = bf16 ? 2 : 1;
+    const int64_t lda_b = a.lda * esz_a, ldb_b = a.ldb * esz_b;
+    if ((a.kind == kFP4FP4 && a.k % 2) || (a.kind == kFP8FP4 && a.k % 2))
+        return dg_set_error("dg_gemm: packed FP4 operands need an even K");
+    if (kbytes_a % 16 || kbytes_b % 16 || lda_b % 16 || ldb_b % 16 ||
+        (reinterpret_cast<uintptr_t>(a.a) & 15) || (reinterpret_cast<uintptr_t>(a.b) & 15))
+        return dg_set_error("dg_gemm: K rows and strides must be 16-byte aligned (host pads otherwise)");
+    if (lda_b < kbytes_a || ldb_b < kbytes_b || a.ldd < a.n)
+        return dg_set_error("dg_gemm: leading dimension smaller than the row");
+    if ((int64_t)256 * lda_b > 0x7fffffffLL || (int64_t)256 * ldb_b > 0x7fffffffLL)
+        return dg_set_error("dg_gemm: row stride too large for 32-bit tile offsets");
+    if (a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) {
+        if (a.alignment < 32 || a.alignment % 32 != 0) return dg_set_error("dg_gemm: alignment must be a multiple of 32");
+    }
+
+    const int cus = a.num_cus > 0 ? a.num_cus : device_cus();
+    const TileCfg cfg = choose(a, cus);
+    if (cfg.bm == 0) return dg_set_error("dg_gemm: no tile shape fits this problem");
+    if (!tile_allowed(a, cfg.bm, cfg.bn)) return dg_set_error("dg_gemm: block_m must divide the M-grouped alignment");
+    KernelFn fn = lookup_kernel(a.kind, cfg.bm, cfg.bn);
+    if (fn == nullptr) {
+        char buf[160];
+        snprintf(buf, sizeof(buf), "dg_gemm: no compiled kernel for kind=%d block=%dx%d", a.kind, cfg.bm, cfg.bn);
+        dg_set_error(buf);
+        return DG_ENOKERNEL;
+    }
+
+    KParams p;
+    memset(&p, 0, sizeof(p));
+    p.a = reinterpret_cast<const uint8_t*>(a.a);
+    p.b = reinterpret_cast<const uint8_t*>(a.b);
+    p.d = reinterpret_cast<uint8_t*>(a.d);
+    p.sfa = reinterpret_cast<const uint16_t*>(a.sfa);
+    p.sfb = reinterpret_cast<const uint16_t*>(a.sfb);
+    p.bias = reinterpret_cast<const uint8_t*>(a.bias);
+    p.layout = a.grouped_layout;
+    p.m = a.m; p.n = a.n; p.k = a.k; p.num_groups = a.num_groups;
+    p.lda = lda_b; p.ldb = ldb_b; p.ldd = a.ldd;
+    p.bsa = a.batch_stride_a * esz_a; p.bsb = a.batch_stride_b * esz_b; p.bsd = a.batch_stride_d;
+    p.sfa_ld = a.sfa_ld; p.sfb_ld = a.sfb_ld; p.sfa_bs = a.sfa_batch_stride; p.sfb_bs = a.sfb_batch_stride;
+    p.gemm_type = a.gemm_type; p.out_f32 = a.d_dtype == DG_DTYPE_F32; p.accumulate = a.accumulate != 0;
+    p.has_bias = a.bias != nullptr; p.alignment = a.alignment > 0 ? a.alignment : 256;
+    p.alpha = a.alpha;
+    const int out_esz = p.out_f32 ? 4 : 2;
+    p.vec_store = (a.ldd % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.d) % (4 * out_esz)) == 0) &&
+                  (a.gemm_type != kBatched && a.gemm_type != kMasked ? true : (a.batch_stride_d % 4 == 0));
+    p.num_m_blocks = ceil_div(a.m, cfg.bm);
+    p.num_n_blocks = ceil_div(a.n, cfg.bn);
+    p.kbytes_a = (int)kbytes_a; p.kbytes_b = (int)kbytes_b;
+    p.group_m = 4;
+    const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
+    const int64_t grid = (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
+    if (grid <= 0) return DG_OK;
+    if (grid > 0x7fffffffLL) return dg_set_error("dg_gemm: too many tiles");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), 0, st, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        dg_set_error(hipGetErrorString(e));
+        return DG_ELAUNCH;
+    }
+    return DG_OK;
+}

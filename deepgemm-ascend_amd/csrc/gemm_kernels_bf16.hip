@@ -1,0 +1,6 @@
+// Instantiates the GEMM kernel for every tile shape of the menu (kBF16 operands).
+#include "gemm_tiles.hpp"
+
+namespace dg {
+KernelFn lookup_kernel_bf16(int bm, int bn) { DG_TILE_TABLE(kBF16) }
+}  // namespace dg

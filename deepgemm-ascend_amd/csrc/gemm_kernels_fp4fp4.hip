@@ -1,0 +1,6 @@
+// Instantiates the GEMM kernel for every tile shape of the menu (kFP4FP4 operands).
+#include "gemm_tiles.hpp"
+
+namespace dg {
+KernelFn lookup_kernel_fp4fp4(int bm, int bn) { DG_TILE_TABLE(kFP4FP4) }
+}  // namespace dg

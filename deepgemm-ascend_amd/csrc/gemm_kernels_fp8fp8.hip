@@ -1,0 +1,6 @@
+// Instantiates the GEMM kernel for every tile shape of the menu (kFP8FP8 operands).
+#include "gemm_tiles.hpp"
+
+namespace dg {
+KernelFn lookup_kernel_fp8fp8(int bm, int bn) { DG_TILE_TABLE(kFP8FP8) }
+}  // namespace dg

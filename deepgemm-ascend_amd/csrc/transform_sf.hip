@@ -1,0 +1,127 @@
+// Scale-factor layout transform (HBM-bound byte work).
+//
+// Behaviour of the reference's transform_sf kernel
+// (deep_gemm/include/deep_gemm/transform_sf.hpp:447-639, host side
+// csrc/jit_kernels/transform_sf.hpp:15-105): fp32 power-of-two SF -> UE8M0 exponent byte,
+// two K-adjacent bytes per int16 (even block low), MN-major output, each SF row repeated
+// gran_mn times, M-grouped psum padding rows zeroed, invalid fp32 SF flagged.
+//
+// One thread produces one output int16; consecutive threads walk the contiguous MN axis so
+// the stores are fully coalesced (the output is the larger side of the transform).
+#include "dg_common.hpp"
+#include "../../include/deep_gemm_amd.h"
+
+namespace dg {
+
+struct SfParams {
+    const uint8_t* src;
+    int64_t stride_b, stride_mn, stride_k;   // elements of the source type
+    int num_batches, sf_mn, sf_k, mn, k64, k32, gran_mn, gran_k;
+    const int* psum;
+    int num_groups, alignment;
+    int16_t* dst;
+    int64_t dst_stride_b;
+    int* err;
+};
+
+// Is SF row `i` (rows [i*gran, (i+1)*gran) of the operand) padding of an M-grouped layout?
+__device__ __forceinline__ bool sf_row_is_padding(const SfParams& p, int i) {
+    const int row = i * p.gran_mn;
+    int lo = 0, hi = p.num_groups;   // first g with align(psum[g]) > row
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (align_up(p.psum[mid], p.alignment) > row) hi = mid;
+        else lo = mid + 1;
+    }
+    if (lo == p.num_groups) return false;   // beyond the last group: untouched
+    return i >= ceil_div(p.psum[lo], p.gran_mn);
+}
+
+template <bool kFloat>
+__global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
+    const int64_t per_batch = (int64_t)p.k64 * p.mn;
+    const int64_t total = per_batch * p.num_batches;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+        const int b = (int)(e / per_batch);
+        const int64_t rem = e - (int64_t)b * per_batch;
+        const int k64 = (int)(rem / p.mn);
+        const int mn = (int)(rem - (int64_t)k64 * p.mn);
+        const int i = mn / p.gran_mn;
+        uint16_t out = 0;
+        if (i < p.sf_mn && !(p.psum != nullptr && sf_row_is_padding(p, i))) {
+            const int64_t row_off = (int64_t)b * p.stride_b + (int64_t)i * p.stride_mn;
+            if constexpr (kFloat) {
+                const uint32_t* s = reinterpret_cast<const uint32_t*>(p.src);
+                uint32_t bytes[2] = {0, 0};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int blk = 2 * k64 + h;                       // 32-wide K block
+                    if (blk < p.k32) {
+                        const int j = p.gran_k == 128 ? blk >> 2 : blk;
+                        if (j < p.sf_k) {
+                            const uint32_t bits = s[row_off + (int64_t)j * p.stride_k];
+                            if ((bits & 0x807fffffu) != 0 && p.err != nullptr) *p.err = 1;
+                            bytes[h] = (bits >> 23) & 0xffu;
+                        }
+                    }
+                }
+                out = (uint16_t)(bytes[0] | (bytes[1] << 8));
+            } else {
+                const uint16_t* s = reinterpret_cast<const uint16_t*>(p.src);
+                if (k64 < p.sf_k) out = s[row_off + (int64_t)k64 * p.stride_k];
+            }
+        }
+        p.dst[(int64_t)b * p.dst_stride_b + (int64_t)k64 * p.mn + mn] = (int16_t)out;
+    }
+}
+
+}  // namespace dg
+
+extern "C" int dg_set_error(const char* msg);
+
+extern "C" int dg_transform_sf(const void* src, int32_t src_kind, int64_t stride_b, int64_t stride_mn,
+                               int64_t stride_k, int32_t num_batches, int32_t sf_mn, int32_t sf_k,
+                               int32_t mn, int32_t k, int32_t gran_mn, int32_t gran_k,
+                               const int32_t* psum, int32_t num_groups, int32_t alignment,
+                               int16_t* dst, int64_t dst_stride_b, int32_t* err_flag, void* stream) {
+    using namespace dg;
+    if (src == nullptr || dst == nullptr) return dg_set_error("dg_transform_sf: null pointer");
+    if (num_batches < 1 || mn < 0 || k < 0 || sf_mn < 0 || sf_k < 0)
+        return dg_set_error("dg_transform_sf: negative size");
+    if (gran_mn < 1 || gran_mn > 128 || (gran_mn & (gran_mn - 1)) != 0)
+        return dg_set_error("gran_mn only support a power of two in [1, 128]");
+    if (src_kind == DG_SF_F32) {
+        if (gran_k != 32 && gran_k != 128) return dg_set_error("gran_k must be 32 or 128 for fp32 SF");
+        if (sf_k != ceil_div(k, gran_k)) return dg_set_error("dg_transform_sf: sf_k != ceil(K / gran_k)");
+    } else if (src_kind == DG_SF_I16) {
+        if (gran_k != 32) return dg_set_error("gran_k must be 32");
+        if (sf_k != ceil_div(k, 64)) return dg_set_error("dg_transform_sf: sf_k != ceil(K / 64)");
+    } else {
+        return dg_set_error("dg_transform_sf: unknown src_kind");
+    }
+    if (sf_mn != ceil_div(mn, gran_mn)) return dg_set_error("dg_transform_sf: sf_mn != ceil(MN / gran_mn)");
+    if (psum != nullptr && (num_groups < 1 || alignment < 1 || alignment % gran_mn != 0))
+        return dg_set_error("dg_transform_sf: psum needs num_groups >= 1 and alignment % gran_mn == 0");
+    SfParams p;
+    p.src = reinterpret_cast<const uint8_t*>(src);
+    p.stride_b = stride_b; p.stride_mn = stride_mn; p.stride_k = stride_k;
+    p.num_batches = num_batches; p.sf_mn = sf_mn; p.sf_k = sf_k; p.mn = mn;
+    p.k64 = ceil_div(k, 64); p.k32 = ceil_div(k, 32); p.gran_mn = gran_mn; p.gran_k = gran_k;
+    p.psum = psum; p.num_groups = num_groups; p.alignment = alignment;
+    p.dst = dst; p.dst_stride_b = dst_stride_b; p.err = err_flag;
+    const int64_t total = (int64_t)p.k64 * mn * num_batches;
+    if (total == 0) return DG_OK;
+    int64_t blocks = ceil_div64(total, 256);
+    if (blocks > 8192) blocks = 8192;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (src_kind == DG_SF_F32)
+        hipLaunchKernelGGL(transform_sf_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL(transform_sf_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        dg_set_error(hipGetErrorString(e));
+        return DG_ELAUNCH;
+    }
+    return DG_OK;
+}

@@ -1,0 +1,88 @@
+"""ctypes binding of libdeep_gemm_amd.so (the C ABI declared in include/deep_gemm_amd.h).
+
+The library is loaded lazily on the first kernel call, so ``import deep_gemm`` touches
+neither the HIP runtime nor the GPU (the reference keeps import fork-safe the same way,
+csrc/apis/runtime.hpp:41-44).  There is no CPU fallback: a missing library raises.
+"""
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+_LIB_NAME = 'libdeep_gemm_amd.so'
+_lock = threading.Lock()
+_lib = None
+
+DG_KIND_FP8_FP8, DG_KIND_FP8_FP4, DG_KIND_FP4_FP4, DG_KIND_BF16 = 0, 1, 2, 3
+DG_GEMM_NORMAL, DG_GEMM_BATCHED, DG_GEMM_MGROUPED_PSUM, DG_GEMM_MGROUPED_IDX, DG_GEMM_MASKED = 0, 1, 2, 3, 4
+DG_DTYPE_BF16, DG_DTYPE_F32 = 0, 1
+DG_SF_F32, DG_SF_I16 = 0, 1
+
+# Every symbol include/deep_gemm_amd.h declares.
+EXPORTED_SYMBOLS = ('dg_gemm', 'dg_transform_sf', 'dg_device_num_cus', 'dg_select_config',
+                    'dg_last_error', 'dg_version')
+
+
+class GemmArgs(ctypes.Structure):
+    """Mirror of ``dg_gemm_args`` (include/deep_gemm_amd.h)."""
+    _fields_ = [
+        ('kind', ctypes.c_int32), ('gemm_type', ctypes.c_int32),
+        ('a', ctypes.c_void_p), ('b', ctypes.c_void_p), ('d', ctypes.c_void_p),
+        ('sfa', ctypes.c_void_p), ('sfb', ctypes.c_void_p),
+        ('bias', ctypes.c_void_p), ('grouped_layout', ctypes.c_void_p),
+        ('m', ctypes.c_int32), ('n', ctypes.c_int32), ('k', ctypes.c_int32), ('num_groups', ctypes.c_int32),
+        ('lda', ctypes.c_int64), ('ldb', ctypes.c_int64), ('ldd', ctypes.c_int64),
+        ('batch_stride_a', ctypes.c_int64), ('batch_stride_b', ctypes.c_int64), ('batch_stride_d', ctypes.c_int64),
+        ('sfa_ld', ctypes.c_int64), ('sfb_ld', ctypes.c_int64),
+        ('sfa_batch_stride', ctypes.c_int64), ('sfb_batch_stride', ctypes.c_int64),
+        ('d_dtype', ctypes.c_int32), ('accumulate', ctypes.c_int32), ('alpha', ctypes.c_float),
+        ('alignment', ctypes.c_int32), ('block_m', ctypes.c_int32), ('block_n', ctypes.c_int32),
+        ('num_cus', ctypes.c_int32),
+    ]
+
+
+def library_path() -> Path:
+    override = os.environ.get('DG_LIBRARY_PATH')
+    if override:
+        return Path(override)
+    return Path(__file__).resolve().parent / _LIB_NAME
+
+
+def load(path=None) -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raises if it has not been built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = Path(path) if path is not None else library_path()
+        if not p.exists():
+            raise RuntimeError(f'deep_gemm HIP library not found at {p}; build it with '
+                               f'`python deepgemm-ascend_amd/build.py` (there is no CPU fallback)')
+        lib = ctypes.CDLL(str(p))
+        lib.dg_gemm.argtypes = [ctypes.POINTER(GemmArgs), ctypes.c_void_p]
+        lib.dg_gemm.restype = ctypes.c_int
+        lib.dg_transform_sf.argtypes = [
+            ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+            ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+        lib.dg_transform_sf.restype = ctypes.c_int
+        lib.dg_device_num_cus.argtypes = [ctypes.c_int32]
+        lib.dg_device_num_cus.restype = ctypes.c_int
+        lib.dg_select_config.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(ctypes.c_int32),
+                                         ctypes.POINTER(ctypes.c_int32)]
+        lib.dg_select_config.restype = ctypes.c_int
+        lib.dg_last_error.restype = ctypes.c_char_p
+        lib.dg_version.restype = ctypes.c_char_p
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def check(rc: int, lib=None) -> None:
+    if rc != 0:
+        lib = lib or load()
+        msg = lib.dg_last_error().decode(errors='replace')
+        raise RuntimeError(msg or f'deep_gemm error {rc}')

@@ -1,0 +1,405 @@
+"""GEMM API: validation, descriptor building and dispatch onto the HIP library.
+
+Mirrors the reference's csrc/apis/gemm.hpp (get_gemm_desc :60-197, fp8_fp4_gemm :225-256,
+m_grouped_fp8_fp4_gemm_contiguous :289-324, bf16_gemm :424-453, bindings :552-678) and
+csrc/utils/layout.hpp (major detection :37-52, gemm_early_return :54-86, shape specs
+:141-219): same names, argument order, defaults and error messages.  Every launch goes
+through ``dg_gemm`` of libdeep_gemm_amd.so on the current HIP stream.
+
+The kernels read K-major operands with 16-byte-aligned rows.  Operands given MN-major, or
+with a K extent / stride that is not 16-byte aligned, are first copied into that layout on
+the device (a layout conversion, not a change of the arithmetic).
+"""
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from . import epilogue as _epi
+from .layout import transform_sf_into_required_layout, get_recipe, operand_recipes, _assert
+from .runtime import get_num_sms, get_mk_alignment_for_contiguous_layout, get_dry_run
+
+PACKED_FP4 = torch.int8   # the reference's kPackedFP4 (csrc/utils/dtype.hpp:9)
+_FP4_TYPES = (torch.int8, getattr(torch, 'float4_e2m1fn_x2', torch.int8))
+
+
+def _is_fp4(t: torch.Tensor) -> bool:
+    return t.dtype in _FP4_TYPES
+
+
+def _as_int8(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.int8 else t.view(torch.int8)
+
+
+def _major_is_k(t: torch.Tensor) -> bool:
+    """csrc/utils/layout.hpp:37-47."""
+    if t.stride(-2) == 1 and t.stride(-1) == 1 and t.size(-1) > 1 and t.size(-2) > 1:
+        raise RuntimeError(f'Ambiguous major axis, the tensor has both last two dimensions contiguous, '
+                           f'strides={list(t.stride())}')
+    if t.stride(-1) == 1:
+        return True
+    _assert(t.stride(-2) == 1)
+    return False
+
+
+def _logical_k(t: torch.Tensor, k_is_major: bool) -> int:
+    return t.size(-1) * (2 if _is_fp4(t) and k_is_major else 1)
+
+
+def _logical_mn(t: torch.Tensor, k_is_major: bool) -> int:
+    return t.size(-2) * (2 if _is_fp4(t) and not k_is_major else 1)
+
+
+def _to_kernel_operand(t: torch.Tensor, k: int) -> torch.Tensor:
+    """Return a [..., MN, K-storage] K-major tensor whose rows are 16-byte aligned."""
+    fp4 = _is_fp4(t)
+    k_major = _major_is_k(t)
+    if fp4:
+        t = _as_int8(t)
+        if not k_major:
+            # packed along MN -> unpack the nibble pairs, re-pack along K
+            u = t.transpose(-2, -1).contiguous().view(torch.uint8)          # [..., K, MN/2]
+            lo, hi = u & 0x0f, u >> 4
+            codes = torch.stack((lo, hi), dim=-1).reshape(*u.shape[:-1], u.shape[-1] * 2)  # [..., K, MN]
+            codes = codes.transpose(-2, -1).contiguous()                      # [..., MN, K]
+            packed = codes[..., 0::2] | (codes[..., 1::2] << 4)
+            t = packed.view(torch.int8)
+        kbytes, align_elems, esize = k // 2, 32, 1
+    else:
+        if not k_major:
+            t = t.contiguous()
+        esize = t.element_size()
+        kbytes, align_elems = k * esize, 16 // esize
+    row_stride_bytes = t.stride(-2) * (1 if fp4 else esize)
+    ok = (kbytes % 16 == 0 and row_stride_bytes % 16 == 0 and t.data_ptr() % 16 == 0 and t.stride(-1) == 1)
+    if t.dim() == 3:
+        ok = ok and (t.stride(0) * (1 if fp4 else esize)) % 16 == 0
+    if ok:
+        return t
+    kpad = (k + align_elems - 1) // align_elems * align_elems
+    store_k = kpad // 2 if fp4 else kpad
+    out = torch.zeros((*t.shape[:-1], store_k), dtype=t.dtype, device=t.device)
+    out[..., :t.size(-1)] = t
+    return out
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _kind(a: torch.Tensor, b: torch.Tensor) -> int:
+    """dispatch_fp8_fp4_gemm (csrc/apis/gemm.hpp:22-33)."""
+    fa, fb = _is_fp4(a), _is_fp4(b)
+    if a.dtype == torch.float8_e4m3fn and b.dtype == torch.float8_e4m3fn:
+        return _lib.DG_KIND_FP8_FP8
+    if fa and fb:
+        return _lib.DG_KIND_FP4_FP4
+    if a.dtype == torch.float8_e4m3fn and fb:
+        return _lib.DG_KIND_FP8_FP4
+    raise RuntimeError('Unsupported operand dtypes')
+
+
+def _launch(args: _lib.GemmArgs, stream: int) -> None:
+    if get_dry_run():
+        return
+    lib = _lib.load()
+    _lib.check(lib.dg_gemm(args, stream), lib)
+
+
+def _fill_common(args, d, k_kernel, alpha, kind):
+    args.kind = kind
+    args.d = d.data_ptr()
+    args.ldd = d.stride(-2)
+    args.d_dtype = _lib.DG_DTYPE_F32 if d.dtype == torch.float32 else _lib.DG_DTYPE_BF16
+    args.alpha = 1.0 if alpha is None else float(alpha)
+    args.k = k_kernel
+    args.num_cus = get_num_sms()
+    args.alignment = get_mk_alignment_for_contiguous_layout()
+
+
+def _early_return(m, n, k, d, c, is_cd_same, with_bias) -> bool:
+    """csrc/utils/layout.hpp:54-86."""
+    if m == 0 or n == 0:
+        return True
+    if is_cd_same:
+        _assert(c.shape == d.shape and c.stride() == d.stride())
+    _assert(d.dtype in (torch.bfloat16, torch.float32))
+    if c is not None:
+        _assert(c.stride(-1) == 1)
+        _assert(d.dtype == c.dtype)
+    if k == 0:
+        if not is_cd_same:
+            if c is not None and not with_bias:
+                d.copy_(c)
+            elif c is not None:
+                d.copy_(c.expand_as(d))
+            else:
+                d.zero_()
+        return True
+    return False
+
+
+def _dense_gemm(a, sfa, b, sfb, d, c, recipe, recipe_a, recipe_b, disable_ue8m0_cast, alpha, epilogue,
+                bf16: bool):
+    """fp8_fp4_gemm / bf16_gemm after the nt/nn/tn/tt transposes (csrc/apis/gemm.hpp:225-256, 424-453)."""
+    _assert(d.dtype in (torch.bfloat16, torch.float32))
+    if bf16:
+        _assert(a.dtype == torch.bfloat16)
+        _assert(b.dtype == torch.bfloat16)
+    epi = _epi.resolve(epilogue, c, d, alpha)
+    ka, kb = _major_is_k(a), _major_is_k(b)
+    m, k = _logical_mn(a, ka), _logical_k(a, ka)
+    n, k_b = _logical_mn(b, kb), _logical_k(b, kb)
+    if k != k_b:
+        raise RuntimeError(f"Conflicting shape dimension 'k': A gives {k}, B gives {k_b}")
+    _assert(d.dim() == 2 and d.size(0) == m and d.size(1) == n, f'D shape {tuple(d.shape)} != ({m}, {n})')
+    _assert(d.stride(-1) == 1)
+    is_cd_same = c is not None and c.data_ptr() == d.data_ptr() and d.numel() > 0
+    with_bias = c is not None and not is_cd_same
+    if c is not None:
+        _assert(c.dim() == 2 and c.size(0) == (1 if with_bias else m) and c.size(1) == n,
+                "C must match D's pointer and shape for accumulation, or be a separate [1, N] bias")
+        _assert(c.device == d.device, 'C and D must be on the same device')
+    if with_bias:
+        _assert(c.is_contiguous(), 'Bias must be contiguous')
+        _assert(not isinstance(epi, _epi.Alpha), 'alpha and bias cannot be used together')
+    if _early_return(m, n, k, d, c, is_cd_same, with_bias):
+        return
+    alpha_v = epi.alpha if isinstance(epi, _epi.Alpha) else None
+
+    args = _lib.GemmArgs()
+    if bf16:
+        kind = _lib.DG_KIND_BF16
+    else:
+        kind = _kind(a, b)
+        ra, rb = operand_recipes(recipe, recipe_a, recipe_b)
+        sfa_t = transform_sf_into_required_layout(sfa, m, k, ra, None, True, disable_ue8m0_cast)
+        sfb_t = transform_sf_into_required_layout(sfb, n, k, rb, None, False, disable_ue8m0_cast)
+        args.sfa, args.sfb = sfa_t.data_ptr(), sfb_t.data_ptr()
+        args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
+    a_k = _to_kernel_operand(a, k)
+    b_k = _to_kernel_operand(b, k)
+    k_kernel = a_k.size(-1) * (2 if _is_fp4(a_k) else 1)
+    k_kernel_b = b_k.size(-1) * (2 if _is_fp4(b_k) else 1)
+    k_kernel = max(k_kernel, k_kernel_b)
+    if k_kernel != a_k.size(-1) * (2 if _is_fp4(a_k) else 1) or k_kernel != k_kernel_b:
+        # keep both operands on the same padded K
+        a_k = _pad_k(a_k, k_kernel)
+        b_k = _pad_k(b_k, k_kernel)
+    _fill_common(args, d, k_kernel, alpha_v, kind)
+    args.gemm_type = _lib.DG_GEMM_NORMAL
+    args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
+    args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
+    args.m, args.n, args.num_groups = m, n, 1
+    args.accumulate = 1 if is_cd_same else 0
+    args.bias = c.data_ptr() if with_bias else None
+    _launch(args, _stream(d))
+
+
+def _pad_k(t: torch.Tensor, k: int) -> torch.Tensor:
+    store = k // 2 if _is_fp4(t) else k
+    if t.size(-1) == store:
+        return t
+    out = torch.zeros((*t.shape[:-1], store), dtype=t.dtype, device=t.device)
+    out[..., :t.size(-1)] = t
+    return out
+
+
+def _make_fp8_fp4_gemm(trans_a: bool, trans_b: bool, default_dims: str):
+    def fn(a: Tuple[torch.Tensor, torch.Tensor], b: Tuple[torch.Tensor, torch.Tensor], d: torch.Tensor,
+           c: Optional[torch.Tensor] = None, recipe=None, recipe_a=None, recipe_b=None,
+           compiled_dims: str = default_dims, disable_ue8m0_cast: bool = False,
+           alpha: Optional[float] = None, epilogue=None) -> None:
+        (a_, sfa), (b_, sfb) = a, b
+        if trans_a:
+            a_, sfa = a_.transpose(0, 1), sfa.transpose(0, 1)
+        if trans_b:
+            b_, sfb = b_.transpose(0, 1), sfb.transpose(0, 1)
+        _dense_gemm(a_, sfa, b_, sfb, d, c, recipe, recipe_a, recipe_b, disable_ue8m0_cast, alpha, epilogue,
+                    bf16=False)
+    return fn
+
+
+fp8_fp4_gemm_nt = _make_fp8_fp4_gemm(False, False, 'nk')
+fp8_fp4_gemm_nn = _make_fp8_fp4_gemm(False, True, 'nk')
+fp8_fp4_gemm_tn = _make_fp8_fp4_gemm(True, True, 'mn')
+fp8_fp4_gemm_tt = _make_fp8_fp4_gemm(True, False, 'mn')
+for _f, _name in ((fp8_fp4_gemm_nt, 'nt'), (fp8_fp4_gemm_nn, 'nn'), (fp8_fp4_gemm_tn, 'tn'), (fp8_fp4_gemm_tt, 'tt')):
+    _f.__name__ = f'fp8_fp4_gemm_{_name}'
+    _f.__doc__ = (f'D = A @ B^T (+ C) with the `{_name}` logical operand shapes; block-scaled e4m3/e2m1 '
+                  f'operands (csrc/apis/gemm.hpp:199-256).')
+
+
+def _make_bf16_gemm(trans_a: bool, trans_b: bool, default_dims: str):
+    def fn(a: torch.Tensor, b: torch.Tensor, d: torch.Tensor, c: Optional[torch.Tensor] = None,
+           compiled_dims: str = default_dims, alpha: Optional[float] = None, epilogue=None) -> None:
+        a_ = a.transpose(0, 1) if trans_a else a
+        b_ = b.transpose(0, 1) if trans_b else b
+        _dense_gemm(a_, None, b_, None, d, c, None, None, None, False, alpha, epilogue, bf16=True)
+    return fn
+
+
+bf16_gemm_nt = _make_bf16_gemm(False, False, 'nk')
+bf16_gemm_nn = _make_bf16_gemm(False, True, 'nk')
+bf16_gemm_tn = _make_bf16_gemm(True, True, 'mn')
+bf16_gemm_tt = _make_bf16_gemm(True, False, 'mn')
+for _f, _name in ((bf16_gemm_nt, 'nt'), (bf16_gemm_nn, 'nn'), (bf16_gemm_tn, 'tn'), (bf16_gemm_tt, 'tt')):
+    _f.__name__ = f'bf16_gemm_{_name}'
+
+
+def _grouped_contiguous(a, sfa, b, sfb, d, grouped_layout, recipe, recipe_a, recipe_b, disable_ue8m0_cast,
+                        use_psum_layout, epilogue, bf16: bool):
+    """m_grouped_fp8_fp4_gemm_contiguous / m_grouped_bf16_gemm_contiguous (csrc/apis/gemm.hpp:289-324, 470-499)."""
+    if bf16:
+        _assert(a.dtype == torch.bfloat16)
+        _assert(b.dtype == torch.bfloat16)
+    else:
+        _assert(a.dtype == torch.float8_e4m3fn or _is_fp4(a))
+        _assert(b.dtype == torch.float8_e4m3fn or _is_fp4(b))
+    _assert(d.dtype in (torch.bfloat16, torch.float32))
+    epi = _epi.resolve(epilogue, None, d)
+    _assert(isinstance(epi, _epi.Identity), 'grouped GEMMs only support the identity epilogue')
+    _assert(_major_is_k(a))
+    kb = _major_is_k(b)
+    m, k = _logical_mn(a, True), _logical_k(a, True)
+    _assert(b.dim() == 3, 'B must be [G, N, K]')
+    g = b.size(0)
+    n, k_b = _logical_mn(b, kb), _logical_k(b, kb)
+    _assert(k == k_b, f"Conflicting shape dimension 'k': A gives {k}, B gives {k_b}")
+    _assert(d.dim() == 2 and d.size(0) == m and d.size(1) == n and d.stride(-1) == 1)
+    _assert(grouped_layout.is_contiguous())
+    _assert(grouped_layout.dtype == torch.int32)
+    if use_psum_layout:
+        _assert(grouped_layout.numel() == g, f"Conflicting shape dimension 'g': {grouped_layout.numel()} vs {g}")
+    else:
+        _assert(grouped_layout.numel() == m, 'm_indices must have one entry per row of A')
+    if m == 0 or n == 0:
+        return
+    if k == 0:
+        d.zero_()
+        return
+    alignment = get_mk_alignment_for_contiguous_layout()
+    args = _lib.GemmArgs()
+    if bf16:
+        kind = _lib.DG_KIND_BF16
+    else:
+        kind = _kind(a, b)
+        ra, rb = operand_recipes(recipe, recipe_a, recipe_b)
+        sfa_t = transform_sf_into_required_layout(sfa, m, k, ra, None, True, disable_ue8m0_cast,
+                                                  grouped_layout if use_psum_layout else None)
+        sfb_t = transform_sf_into_required_layout(sfb, n, k, rb, g, False, disable_ue8m0_cast)
+        args.sfa, args.sfb = sfa_t.data_ptr(), sfb_t.data_ptr()
+        args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
+        args.sfb_batch_stride = sfb_t.stride(0)
+    a_k = _to_kernel_operand(a, k)
+    b_k = _to_kernel_operand(b, k)
+    k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
+    a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
+    _fill_common(args, d, k_kernel, None, kind)
+    args.alignment = alignment
+    args.gemm_type = _lib.DG_GEMM_MGROUPED_PSUM if use_psum_layout else _lib.DG_GEMM_MGROUPED_IDX
+    args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
+    args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
+    args.batch_stride_b = b_k.stride(0)
+    args.grouped_layout = grouped_layout.data_ptr()
+    args.m, args.n, args.num_groups = m, n, g
+    _launch(args, _stream(d))
+
+
+def _make_m_grouped_fp8_fp4(trans_b: bool):
+    def fn(a, b, d, grouped_layout, recipe=None, recipe_a=None, recipe_b=None, compiled_dims: str = 'nk',
+           disable_ue8m0_cast: bool = False, use_psum_layout: bool = True, ensure_zero_padding: bool = True,
+           expected_m_for_psum_layout: Optional[int] = None, epilogue=None) -> None:
+        (a_, sfa), (b_, sfb) = a, b
+        if trans_b:
+            b_, sfb = b_.transpose(1, 2), sfb.transpose(1, 2)
+        _grouped_contiguous(a_, sfa, b_, sfb, d, grouped_layout, recipe, recipe_a, recipe_b, disable_ue8m0_cast,
+                            use_psum_layout, epilogue, bf16=False)
+    return fn
+
+
+m_grouped_fp8_fp4_gemm_nt_contiguous = _make_m_grouped_fp8_fp4(False)
+m_grouped_fp8_fp4_gemm_nn_contiguous = _make_m_grouped_fp8_fp4(True)
+m_grouped_fp8_fp4_gemm_nt_contiguous.__name__ = 'm_grouped_fp8_fp4_gemm_nt_contiguous'
+m_grouped_fp8_fp4_gemm_nn_contiguous.__name__ = 'm_grouped_fp8_fp4_gemm_nn_contiguous'
+
+
+def _make_m_grouped_bf16(trans_b: bool):
+    def fn(a, b, d, grouped_layout, compiled_dims: str = 'nk', use_psum_layout: bool = True,
+           ensure_zero_padding: bool = True, expected_m_for_psum_layout: Optional[int] = None,
+           epilogue=None) -> None:
+        b_ = b.transpose(1, 2) if trans_b else b
+        _grouped_contiguous(a, None, b_, None, d, grouped_layout, None, None, None, False, use_psum_layout,
+                            epilogue, bf16=True)
+    return fn
+
+
+m_grouped_bf16_gemm_nt_contiguous = _make_m_grouped_bf16(False)
+m_grouped_bf16_gemm_nn_contiguous = _make_m_grouped_bf16(True)
+
+
+def _masked(a, sfa, b, sfb, d, masked_m, recipe, recipe_a, recipe_b, disable_ue8m0_cast, bf16: bool):
+    """Masked grouped GEMM, upstream DeepGEMM semantics: D[g, :masked_m[g]] = A[g, :masked_m[g]] @ B[g]^T.
+    The reference has no masked kernel (csrc/apis/gemm.hpp:606,630)."""
+    _assert(a.dim() == 3 and b.dim() == 3 and d.dim() == 3, 'masked GEMM takes A [G,M,K], B [G,N,K], D [G,M,N]')
+    _assert(d.dtype in (torch.bfloat16, torch.float32))
+    _assert(_major_is_k(a))
+    kb = _major_is_k(b)
+    g, m, k = a.size(0), _logical_mn(a, True), _logical_k(a, True)
+    n, k_b = _logical_mn(b, kb), _logical_k(b, kb)
+    _assert(k == k_b and b.size(0) == g and d.size(0) == g and d.size(1) == m and d.size(2) == n)
+    _assert(d.stride(-1) == 1)
+    _assert(masked_m.dtype == torch.int32 and masked_m.is_contiguous() and masked_m.numel() == g)
+    if m == 0 or n == 0 or k == 0:
+        if k == 0:
+            d.zero_()
+        return
+    args = _lib.GemmArgs()
+    if bf16:
+        kind = _lib.DG_KIND_BF16
+    else:
+        kind = _kind(a, b)
+        ra, rb = operand_recipes(recipe, recipe_a, recipe_b)
+        sfa_t = transform_sf_into_required_layout(sfa, m, k, ra, g, True, disable_ue8m0_cast)
+        sfb_t = transform_sf_into_required_layout(sfb, n, k, rb, g, False, disable_ue8m0_cast)
+        args.sfa, args.sfb = sfa_t.data_ptr(), sfb_t.data_ptr()
+        args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
+        args.sfa_batch_stride, args.sfb_batch_stride = sfa_t.stride(0), sfb_t.stride(0)
+    a_k = _to_kernel_operand(a, k)
+    b_k = _to_kernel_operand(b, k)
+    k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
+    a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
+    _fill_common(args, d, k_kernel, None, kind)
+    args.gemm_type = _lib.DG_GEMM_MASKED
+    args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
+    args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
+    args.batch_stride_a, args.batch_stride_b, args.batch_stride_d = a_k.stride(0), b_k.stride(0), d.stride(0)
+    args.grouped_layout = masked_m.data_ptr()
+    args.m, args.n, args.num_groups = m, n, g
+    _launch(args, _stream(d))
+
+
+def m_grouped_fp8_fp4_gemm_nt_masked(a, b, d, masked_m: torch.Tensor, expected_m: int, recipe=None,
+                                     recipe_a=None, recipe_b=None, compiled_dims: str = 'nk',
+                                     disable_ue8m0_cast: bool = False) -> None:
+    (a_, sfa), (b_, sfb) = a, b
+    _masked(a_, sfa, b_, sfb, d, masked_m, recipe, recipe_a, recipe_b, disable_ue8m0_cast, bf16=False)
+
+
+def m_grouped_bf16_gemm_nt_masked(a, b, d, masked_m: torch.Tensor, expected_m: int,
+                                  compiled_dims: str = 'nk') -> None:
+    _masked(a, None, b, None, d, masked_m, None, None, None, False, bf16=True)
+
+
+def select_config(m: int, n: int, k: int, kind: int = _lib.DG_KIND_FP8_FP8, gemm_type: int = _lib.DG_GEMM_NORMAL,
+                  num_groups: int = 1) -> Tuple[int, int]:
+    """Tile shape (block_m, block_n) the library heuristic picks (for DG_PRINT_CONFIGS-style inspection)."""
+    args = _lib.GemmArgs()
+    args.kind, args.gemm_type, args.m, args.n, args.k, args.num_groups = kind, gemm_type, m, n, k, num_groups
+    args.alignment = get_mk_alignment_for_contiguous_layout()
+    args.num_cus = get_num_sms()
+    import ctypes
+    bm, bn = ctypes.c_int32(), ctypes.c_int32()
+    lib = _lib.load()
+    _lib.check(lib.dg_select_config(args, ctypes.byref(bm), ctypes.byref(bn)), lib)
+    return bm.value, bn.value

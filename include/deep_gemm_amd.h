@@ -1,0 +1,122 @@
+/*
+ * deep_gemm_amd.h -- C ABI of the MI355X (gfx950) block-scaled GEMM library
+ * (libdeep_gemm_amd.so).  Plain pointers, sizes and strides only; no torch types.
+ *
+ * All device pointers are HIP device addresses; `stream` is a hipStream_t (NULL = the
+ * default stream).  Every entry point is asynchronous on `stream` and returns 0 on success
+ * or a negative DG_E* code; dg_last_error() then holds a message (thread-local).
+ *
+ * Scale factors (SF) consumed by the GEMM entry points are in the "required layout" that
+ * dg_transform_sf() produces, which is the layout the reference documents for
+ * transform_sf_into_required_layout (csrc/apis/layout.hpp:18-35): one UE8M0 exponent byte
+ * per 32 K-elements, two K-adjacent bytes per int16 (even block in the low byte), stored
+ * MN-major: element (mn, k64) at sf[k64 * sf_ld + mn].
+ */
+#ifndef DEEP_GEMM_AMD_H_
+#define DEEP_GEMM_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Operand format pairs (A x B). */
+#define DG_KIND_FP8_FP8   0   /* e4m3 x e4m3, per-32 UE8M0 scales on both operands          */
+#define DG_KIND_FP8_FP4   1   /* e4m3 x e2m1 (B packed two per byte, low nibble = even k)   */
+#define DG_KIND_FP4_FP4   2   /* e2m1 x e2m1                                                 */
+#define DG_KIND_BF16      3   /* bf16 x bf16, no scales                                      */
+
+/* Work decomposition. */
+#define DG_GEMM_NORMAL        0  /* D[M,N] = A[M,K] B[N,K]^T                                  */
+#define DG_GEMM_BATCHED       1  /* D[g] = A[g] B[g]^T for g < num_groups                     */
+#define DG_GEMM_MGROUPED_PSUM 2  /* grouped_layout = psum int32[G]; group g = rows
+                                    [align(psum[g-1], alignment), psum[g]) uses B[g]          */
+#define DG_GEMM_MGROUPED_IDX  3  /* grouped_layout = m_indices int32[M]; -1 marks padding rows */
+#define DG_GEMM_MASKED        4  /* A[G,M,K], D[G,M,N]; grouped_layout = masked_m int32[G]     */
+
+#define DG_DTYPE_BF16 0
+#define DG_DTYPE_F32  1
+
+#define DG_SF_F32 0   /* fp32 powers of two, one per gran_mn x gran_k block             */
+#define DG_SF_I16 1   /* packed UE8M0x2 int16, one per gran_mn x 64                       */
+
+#define DG_OK            0
+#define DG_EINVAL       -1   /* invalid argument / unsupported shape or layout           */
+#define DG_ELAUNCH      -2   /* HIP launch error                                           */
+#define DG_ENOKERNEL    -3   /* no compiled kernel for the requested configuration         */
+
+/*
+ * Problem description for dg_gemm().  Replaces the reference's GemmDesc
+ * (csrc/jit_kernels/gemm_config.hpp:39-95) as the argument of launch_fp8_gemm /
+ * launch_fp4_gemm / launch_fp8_dequant_gemm / launch_bf16_gemm
+ * (csrc/jit_kernels/fp8_gemm.hpp:11-151, fp8_dequant_gemm.hpp:24-95, bf16_gemm.hpp:16-78).
+ *
+ * A and B are K-major: A row i at a + i*lda, B row j at b + j*ldb (elements of the storage
+ * type: bytes for e4m3 and packed e2m1, bf16 elements for DG_KIND_BF16).  D is row-major
+ * with row stride ldd (elements of d_dtype).
+ */
+typedef struct dg_gemm_args {
+    int32_t kind;                 /* DG_KIND_*                                               */
+    int32_t gemm_type;            /* DG_GEMM_*                                               */
+    const void *a, *b;
+    void *d;
+    const int16_t *sfa, *sfb;     /* required-layout SF; NULL for DG_KIND_BF16              */
+    const void *bias;             /* [N] of d_dtype, or NULL                                 */
+    const int32_t *grouped_layout;/* psum / m_indices / masked_m (see DG_GEMM_*)             */
+    int32_t m, n, k;              /* logical sizes; for MASKED, m = rows per group           */
+    int32_t num_groups;           /* batches / groups                                        */
+    int64_t lda, ldb, ldd;
+    int64_t batch_stride_a, batch_stride_b, batch_stride_d;   /* elements                   */
+    int64_t sfa_ld, sfb_ld;       /* stride between k64 rows of SF (>= MN extent)            */
+    int64_t sfa_batch_stride, sfb_batch_stride;
+    int32_t d_dtype;              /* DG_DTYPE_*                                              */
+    int32_t accumulate;           /* 1: D = D + alpha * A B^T                                */
+    float alpha;                  /* 1.0f for plain                                          */
+    int32_t alignment;            /* MGROUPED_* row alignment (128 or 256)                   */
+    int32_t block_m, block_n;     /* 0 = library heuristic                                    */
+    int32_t num_cus;              /* 0 = all CUs of the device (set_num_sms)                 */
+} dg_gemm_args;
+
+/* Launch one GEMM.  Entry point replacing deep_gemm::launch_fp8_gemm /
+ * launch_fp4_gemm / launch_fp8_dequant_gemm / launch_bf16_gemm (see dg_gemm_args). */
+int dg_gemm(const dg_gemm_args *args, void *stream);
+
+/*
+ * Scale-factor layout transform.  Replaces launch_transform_sf
+ * (csrc/jit_kernels/transform_sf.hpp:15-105) behind
+ * transform_sf_into_required_layout (csrc/apis/layout.hpp:68-92).
+ *
+ * src: [num_batches][sf_mn][sf_k] of DG_SF_F32 (sf_k = ceil(K / gran_k)) or DG_SF_I16
+ *      (sf_k = ceil(K / 64)), element (b, i, j) at src[b*stride_b + i*stride_mn + j*stride_k].
+ * dst: packed int16, element (b, mn, k64) at dst[b*dst_stride_b + k64*mn + mn_idx],
+ *      k64 < ceil(K/64), mn_idx < mn.  Row mn_idx takes SF row mn_idx / gran_mn.
+ * gran_k: 32 or 128 for DG_SF_F32 (128 repeats each exponent over four 32-blocks), 32 for I16.
+ * psum (optional, device int32[num_groups]): M-grouped padding rows
+ *      [ceil(psum[g]/gran_mn), align(psum[g], alignment)/gran_mn) (in SF rows) become 0.
+ * err_flag (optional, device int32): set to 1 when an fp32 SF has sign or mantissa bits
+ *      (the reference traps on this, deep_gemm/include/deep_gemm/transform_sf.hpp:13-21).
+ */
+int dg_transform_sf(const void *src, int32_t src_kind, int64_t stride_b, int64_t stride_mn,
+                    int64_t stride_k, int32_t num_batches, int32_t sf_mn, int32_t sf_k,
+                    int32_t mn, int32_t k, int32_t gran_mn, int32_t gran_k,
+                    const int32_t *psum, int32_t num_groups, int32_t alignment,
+                    int16_t *dst, int64_t dst_stride_b, int32_t *err_flag, void *stream);
+
+/* Number of compute units of `device` (the reference's get_num_sms, csrc/apis/runtime.hpp:13-19). */
+int dg_device_num_cus(int32_t device);
+
+/* Tile shape dg_gemm() would pick for `args` (block_m, block_n written to the pointers). */
+int dg_select_config(const dg_gemm_args *args, int32_t *block_m, int32_t *block_n);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *dg_last_error(void);
+
+/* Library version string. */
+const char *dg_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DEEP_GEMM_AMD_H_ */
