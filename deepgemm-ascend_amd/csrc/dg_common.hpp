@@ -27,11 +27,17 @@ constexpr uint32_t kBufferRsrcWord3 = 0x00020000u;
 // voffset that is always beyond num_records: such a lane reads zeros.
 constexpr uint32_t kOOBOffset = 0x80000000u;
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 pair (low = a), round-to-nearest-even: v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    const bf16x2 h = __builtin_convertvector(f32x2{a, b}, bf16x2);
+    return __builtin_bit_cast(uint32_t, h);
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-    uint32_t u = __builtin_bit_cast(uint32_t, f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // quiet NaN
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    return (uint16_t)(pack_bf16x2(f, 0.f) & 0xffffu);
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {

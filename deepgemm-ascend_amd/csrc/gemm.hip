@@ -8,10 +8,12 @@
 // (256 CUs, waves-of-tiles quantisation, LDS-read efficiency of the wave tile) and memoises
 // the choice per problem signature.
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "gemm_tiles.hpp"
 #include "../../include/deep_gemm_amd.h"
@@ -42,12 +44,12 @@ extern "C" int dg_device_num_cus(int32_t device) {
 
 namespace dg {
 
-KernelFn lookup_kernel(int kind, int bm, int bn) {
+KernelFn lookup_kernel(int kind, int bm, int bn, int epi) {
     switch (kind) {
-        case kFP8FP8: return lookup_kernel_fp8fp8(bm, bn);
-        case kFP8FP4: return lookup_kernel_fp8fp4(bm, bn);
-        case kFP4FP4: return lookup_kernel_fp4fp4(bm, bn);
-        case kBF16: return lookup_kernel_bf16(bm, bn);
+        case kFP8FP8: return lookup_kernel_fp8fp8(bm, bn, epi);
+        case kFP8FP4: return lookup_kernel_fp8fp4(bm, bn, epi);
+        case kFP4FP4: return lookup_kernel_fp4fp4(bm, bn, epi);
+        case kBF16: return lookup_kernel_bf16(bm, bn, epi);
         default: return nullptr;
     }
 }
@@ -197,7 +199,9 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     const TileCfg cfg = choose(a, cus);
     if (cfg.bm == 0) return dg_set_error("dg_gemm: no tile shape fits this problem");
     if (!tile_allowed(a, cfg.bm, cfg.bn)) return dg_set_error("dg_gemm: block_m must divide the M-grouped alignment");
-    KernelFn fn = lookup_kernel(a.kind, cfg.bm, cfg.bn);
+    // Direct register stores measured faster than staging the tile through LDS.
+    const int epi_kind = a.d_dtype == DG_DTYPE_F32 ? kEpiF32 : kEpiBf16;
+    KernelFn fn = lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind);
     if (fn == nullptr) {
         char buf[160];
         snprintf(buf, sizeof(buf), "dg_gemm: no compiled kernel for kind=%d block=%dx%d", a.kind, cfg.bm, cfg.bn);
@@ -228,12 +232,22 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     p.num_n_blocks = ceil_div(a.n, cfg.bn);
     p.kbytes_a = (int)kbytes_a; p.kbytes_b = (int)kbytes_b;
     p.group_m = 4;
+    if (const char* e = getenv("DG_DEBUG_MODE")) p.dbg = atoi(e);
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
     const int64_t grid = (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
     if (grid <= 0) return DG_OK;
     if (grid > 0x7fffffffLL) return dg_set_error("dg_gemm: too many tiles");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const char* ts_path = getenv("DG_DEBUG_TS");
+    if (ts_path) hipMalloc(&p.dbg_ts, (size_t)grid * 8 * sizeof(unsigned long long));
     hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), 0, st, p);
+    if (ts_path) {
+        hipStreamSynchronize(st);
+        std::vector<unsigned long long> h((size_t)grid * 8);
+        hipMemcpy(h.data(), p.dbg_ts, h.size() * 8, hipMemcpyDeviceToHost);
+        if (FILE* f = fopen(ts_path, "wb")) { fwrite(h.data(), 8, h.size(), f); fclose(f); }
+        hipFree(p.dbg_ts);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         dg_set_error(hipGetErrorString(e));

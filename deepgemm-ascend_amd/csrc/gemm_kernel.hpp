@@ -25,6 +25,7 @@
 // ends with four consecutive n of one output row m: 8-byte (bf16) / 16-byte (fp32) stores.
 #pragma once
 
+#include <type_traits>
 #include <utility>
 #include "dg_common.hpp"
 
@@ -49,7 +50,15 @@ struct KParams {
     int num_m_blocks, num_n_blocks;
     int kbytes_a, kbytes_b;    // bytes of one K row (multiple of 16)
     int group_m;               // tile-order swizzle width along M
+    unsigned long long* dbg_ts;  // profiling: per-workgroup timestamps (null = off)
+    int dbg;                   // profiling switch: 1 = skip operand loads, 2 = skip MFMA,
+                               // 3 = skip scale loads, 4 = skip all loads, 5 = epilogue only
 };
+
+// Epilogue variants.
+constexpr int kEpiLdsBf16 = 0;   // bf16 D, no accumulation, 16-byte aligned rows
+constexpr int kEpiF32 = 1;       // fp32 D (bias / accumulate allowed)
+constexpr int kEpiBf16 = 2;      // bf16 D with accumulation or unaligned rows
 
 template <int N>
 struct Int { static constexpr int value = N; };
@@ -64,17 +73,26 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // Slot swizzle inside one LDS row: 8 slots (128-byte rows) or 4 slots (64-byte rows).
+// Chosen so that the 16 rows one ds_read_b128 phase touches (lanes r = 0..15 at a fixed lane
+// group) land on distinct 16-byte bank groups both for a 64 x 4-byte and a 32 x 4-byte bank
+// organisation.
 template <int SPR>
 __device__ __forceinline__ int slot_swizzle(int row) {
-    if constexpr (SPR == 8) return row & 7;
-    else return (row >> 1) & 3;
+    if constexpr (SPR == 8) return ((row >> 1) ^ (row << 2)) & 7;
+    else return ((row >> 1) ^ (row >> 3)) & 3;
 }
 
+// Buffer resource over [base, base + bytes); every field is forced wave-uniform (SGPRs) so no
+// buffer instruction using it ever needs a waterfall loop.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
     if (bytes > 0x7fffffffLL) bytes = 0x7fffffffLL;
     if (bytes < 0) bytes = 0;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                             (int)kBufferRsrcWord3);
+    const uint64_t addr = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)addr);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32));
+    const int nbytes = __builtin_amdgcn_readfirstlane((int)bytes);
+    void* ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(ub, (short)0, nbytes, (int)kBufferRsrcWord3);
 }
 
 // Spread consecutive workgroup ids over the 8 XCDs so that each XCD (own L2) receives a
@@ -103,7 +121,7 @@ __device__ __forceinline__ f32x4 mfma_scaled(const i32x8& a, const i32x8& b, con
                                                             OPSEL_B, sb);
 }
 
-template <int BM, int BN, int KIND>
+template <int BM, int BN, int KIND, int EPI>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(const KParams p) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
@@ -120,9 +138,16 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const KParams p) {
     static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "tile rows must fill waves");
     constexpr int SC_BYTES = kBf16 ? 0 : 1024;
     constexpr int STAGE = A_BYTES + B_BYTES + 2 * SC_BYTES;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+    constexpr int CROW = BN * 2 + 32;                       // LDS row pitch of the bf16 epilogue tile
+    constexpr int EPI_BYTES = EPI == kEpiLdsBf16 ? BM * CROW : 0;
+    constexpr int SMEM = 2 * STAGE > EPI_BYTES ? 2 * STAGE : EPI_BYTES;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
     const int tid = threadIdx.x;
+    unsigned long long* ts = p.dbg_ts ? p.dbg_ts + (size_t)blockIdx.x * 8 : nullptr;
+    auto stamp = [&](int i) { if (ts && tid == 0) ts[i] = __builtin_amdgcn_s_memrealtime(); };
+    stamp(0);
+    if (ts && tid == 0) ts[2] = __builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11));  // HW_ID
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
@@ -177,10 +202,12 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const KParams p) {
             if (valid_end <= m0) zero_tile = true;
         }
     } else if (p.gemm_type == kMGroupedIdx) {
-        group = p.layout[m0];
+        group = __builtin_amdgcn_readfirstlane(p.layout[m0]);
         if (group < 0) zero_tile = true;
     }
 
+    group = __builtin_amdgcn_readfirstlane(group);
+    valid_end = __builtin_amdgcn_readfirstlane(valid_end);
     if (zero_tile) {
         // Padding-only tile of an M-grouped layout: its D rows are exact zeros.
         const int rows = min(BM, M - m0), cols = min(BN, N - n0);
@@ -205,59 +232,91 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const KParams p) {
     const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(b_base + (int64_t)n0 * ldb, (int64_t)rows_b * ldb);
     const int kbytes_a = p.kbytes_a, kbytes_b = p.kbytes_b;
     const int KC = kBf16 ? 64 : 128;
-    const int num_chunks = ceil_div(p.k, KC);
+    const int num_chunks = p.dbg == 11 ? 0 : ceil_div(p.k, KC);
     const int nk64 = ceil_div(p.k, 64);
 
     // ------------------------------------------------------------------ loaders
+    // Operand tiles: each wave-level buffer_load_dwordx4 ... lds fills 1 KB (64 lanes x 16 B)
+    // of an LDS stage; lane slots map to XOR-swizzled (row, 16-byte K piece) positions.  The
+    // chunk's K offset rides in the scalar soffset so the per-lane voffset is chunk-invariant,
+    // and the lane index is made opaque to the optimiser so that voffset is recomputed (a few
+    // VALU ops) instead of being hoisted into long-lived VGPRs.
+    constexpr int NLA = A_BYTES / 4096 + (A_BYTES % 4096 ? 1 : 0);   // loads per wave, A tile
+    constexpr int NLB = B_BYTES / 4096 + (B_BYTES % 4096 ? 1 : 0);   // loads per wave, B tile
+    constexpr int NL = NLA + NLB;
+    // Per-load chunk-invariant voffsets (row * ld + swizzled K piece, or out of range).
+    auto load_geom = [&](auto idx_tag, int t, int& row, int& lk) {
+        constexpr int IDX = decltype(idx_tag)::value;
+        constexpr bool kIsA = IDX < NLA;
+        constexpr int it = kIsA ? IDX : IDX - NLA;
+        constexpr int SPR = kIsA ? SPRA : SPRB;
+        const int slot = it * 256 + t;
+        row = slot / SPR;
+        lk = ((slot % SPR) ^ slot_swizzle<SPR>(row)) * 16;
+    };
+    uint32_t voff_pre[NL];
+    static_for<NL>([&](auto i) {
+        constexpr int IDX = decltype(i)::value;
+        constexpr bool kIsA = IDX < NLA;
+        int row, lk;
+        load_geom(i, tid, row, lk);
+        voff_pre[IDX] = row < (kIsA ? rows_a : rows_b) ? (uint32_t)(row * (kIsA ? lda : ldb) + lk) : kOOBOffset;
+    });
+    // The swizzled K piece of a lane's slot is the same for every load of one operand (the
+    // swizzle only reads row bits that a whole 4 KB load block leaves unchanged).
+    int lk_a, lk_b, row_unused;
+    load_geom(Int<0>{}, tid, row_unused, lk_a);
+    load_geom(Int<NLA>{}, tid, row_unused, lk_b);
+    // Loads of chunk c into stage s.  Branch-free so the scheduler can interleave them with
+    // MFMAs: `live == false` moves every lane out of range through the scalar offset (no
+    // memory traffic, zeros into an idle stage); K-tail pieces go out of range per lane.
+    constexpr int kDeadOffset = 0x40000000;
+    auto issue_one = [&](auto idx_tag, int c, int s, bool live) {
+        constexpr int IDX = decltype(idx_tag)::value;
+        constexpr bool kIsA = IDX < NLA;
+        constexpr int it = kIsA ? IDX : IDX - NLA;
+        constexpr int BYTES = kIsA ? A_BYTES : B_BYTES;
+        constexpr int RB = kIsA ? RBA : RBB;
+        if (BYTES % 4096 != 0 && (it * 256 + wave * 64) * 16 >= BYTES) return;
+        const int kb = (p.dbg == 9 ? 0 : c) * RB;
+        const int krem = (kIsA ? kbytes_a : kbytes_b) - kb;
+        const uint32_t voff = (kIsA ? lk_a : lk_b) < krem ? voff_pre[IDX] : kOOBOffset;
+        uint8_t* sdst = smem + s * STAGE + (kIsA ? 0 : A_BYTES);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kIsA ? rs_a : rs_b,
+                                                 (lds_void*)(sdst + (it * 256 + wave * 64) * 16), 16, voff,
+                                                 live ? kb : kDeadOffset, 0, 0);
+    };
     auto issue_data = [&](int c, int s) {
-        uint8_t* sA = smem + s * STAGE;
-        uint8_t* sB = sA + A_BYTES;
-        const int kb_a = c * RBA, kb_b = c * RBB;
-#pragma unroll
-        for (int it = 0; it < A_BYTES / 4096 + (A_BYTES % 4096 ? 1 : 0); ++it) {
-            if (A_BYTES % 4096 == 0 || (it * 256 + wave * 64) * 16 < A_BYTES) {
-                const int slot = it * 256 + tid;
-                const int row = slot / SPRA;
-                const int logical = (slot % SPRA) ^ slot_swizzle<SPRA>(row);
-                const int kb = kb_a + logical * 16;
-                const uint32_t voff = (row < rows_a && kb < kbytes_a)
-                                          ? (uint32_t)(row * lda + kb) : kOOBOffset;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rs_a, (lds_void*)(sA + (it * 256 + wave * 64) * 16), 16, voff, 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int it = 0; it < B_BYTES / 4096 + (B_BYTES % 4096 ? 1 : 0); ++it) {
-            if (B_BYTES % 4096 == 0 || (it * 256 + wave * 64) * 16 < B_BYTES) {
-                const int slot = it * 256 + tid;
-                const int row = slot / SPRB;
-                const int logical = (slot % SPRB) ^ slot_swizzle<SPRB>(row);
-                const int kb = kb_b + logical * 16;
-                const uint32_t voff = (row < rows_b && kb < kbytes_b)
-                                          ? (uint32_t)(row * ldb + kb) : kOOBOffset;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rs_b, (lds_void*)(sB + (it * 256 + wave * 64) * 16), 16, voff, 0, 0, 0);
-            }
-        }
+        static_for<NL>([&](auto i) { issue_one(i, c, s, true); });
     };
 
+    // Scales: the two packed int16 rows (k64 = 2c, 2c+1) of this chunk for the tile's rows,
+    // through buffer loads (out-of-range rows / K blocks read 0: their operand data is 0 too).
     constexpr int NSA = (2 * BM + 255) / 256, NSB = (2 * BN + 255) / 256;
     uint32_t sa_reg[NSA], sb_reg[NSB];
-    auto issue_scales = [&](int c) {
+    __amdgpu_buffer_rsrc_t rs_sa, rs_sb;
+    if constexpr (!kBf16) {
+        rs_sa = make_rsrc(sfa + m0, ((int64_t)nk64 * p.sfa_ld - m0) * 2);
+        rs_sb = make_rsrc(sfb + n0, ((int64_t)nk64 * p.sfb_ld - n0) * 2);
+    }
+    // byte distance between the packed-SF rows of consecutive chunks (two int16 rows)
+    const int sfa_step = __builtin_amdgcn_readfirstlane((int)(p.sfa_ld * 4));
+    const int sfb_step = __builtin_amdgcn_readfirstlane((int)(p.sfb_ld * 4));
+    auto issue_scales = [&](int c, bool live) {
         if constexpr (!kBf16) {
 #pragma unroll
             for (int i = 0; i < NSA; ++i) {
                 const int idx = i * 256 + tid;
-                const int h = idx / BM, row = idx % BM, k64 = 2 * c + h;
-                sa_reg[i] = (idx < 2 * BM && row < rows_a && k64 < nk64)
-                                ? (uint32_t)sfa[(int64_t)k64 * p.sfa_ld + m0 + row] : 0x7f7fu;
+                const int h = idx / BM, row = idx % BM;
+                const uint32_t voff = idx < 2 * BM ? (uint32_t)((h * p.sfa_ld + row) * 2) : kOOBOffset;
+                sa_reg[i] = __builtin_amdgcn_raw_buffer_load_b16(rs_sa, voff, live ? c * sfa_step : kDeadOffset, 0);
             }
 #pragma unroll
             for (int i = 0; i < NSB; ++i) {
                 const int idx = i * 256 + tid;
-                const int h = idx / BN, row = idx % BN, k64 = 2 * c + h;
-                sb_reg[i] = (idx < 2 * BN && row < rows_b && k64 < nk64)
-                                ? (uint32_t)sfb[(int64_t)k64 * p.sfb_ld + n0 + row] : 0x7f7fu;
+                const int h = idx / BN, row = idx % BN;
+                const uint32_t voff = idx < 2 * BN ? (uint32_t)((h * p.sfb_ld + row) * 2) : kOOBOffset;
+                sb_reg[i] = __builtin_amdgcn_raw_buffer_load_b16(rs_sb, voff, live ? c * sfb_step : kDeadOffset, 0);
             }
         }
     };
@@ -315,128 +374,200 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const KParams p) {
         return f;
     };
 
-    auto compute = [&](int s) {
+    // One K chunk of MFMAs from LDS stage s.  When `next` is set, the loads of chunk c + 1
+    // (into stage s ^ 1) are interleaved with the MFMA groups: a buffer_load ... lds blocks
+    // issue while the texture path drains, so issuing them in one burst would stall the MFMA
+    // pipe.  They go out over the first groups to leave latency slack before the next wait.
+    constexpr int kLoadGroups = TN > 2 ? (TN * 2 + 2) / 3 : TN;
+    constexpr int kLPG = (NL + kLoadGroups - 1) / kLoadGroups;    // loads per MFMA group
+    auto compute = [&](int s, int cn, bool next) {
         const uint8_t* sA = smem + s * STAGE;
         const uint8_t* sB = sA + A_BYTES;
         i32x8 fa[TM];
 #pragma unroll
         for (int jm = 0; jm < TM; ++jm) fa[jm] = load_frag(sA, wm * WM + jm * 16 + r, Int<SPRA>{});
-        if constexpr (kBf16) {
-#pragma unroll
-            for (int jn = 0; jn < TN; ++jn) {
-                const i32x8 fb = load_frag(sB, wn * WN + jn * 16 + r, Int<SPRB>{});
-                const i32x4 blo = {fb[0], fb[1], fb[2], fb[3]}, bhi = {fb[4], fb[5], fb[6], fb[7]};
-#pragma unroll
-                for (int jm = 0; jm < TM; ++jm) {
+        i32x2 sa2 = {0, 0}, sb2 = {0, 0};
+        if constexpr (!kBf16) {
+            const uint8_t* sSA = sA + A_BYTES + B_BYTES;
+            const uint8_t* sSB = sSA + SC_BYTES;
+            sa2 = *reinterpret_cast<const i32x2*>(sSA + (q * 16 + r) * 16 + wm * 8);
+            sb2 = *reinterpret_cast<const i32x2*>(sSB + (q * 16 + r) * 16 + wn * 8);
+        }
+        i32x8 fb_cur = load_frag(sB, wn * WN + r, Int<SPRB>{});
+        static_for<TN>([&](auto jn_c) {
+            constexpr int jn = decltype(jn_c)::value;
+            i32x8 fb_next = fb_cur;
+            if constexpr (jn + 1 < TN) fb_next = load_frag(sB, wn * WN + (jn + 1) * 16 + r, Int<SPRB>{});
+            static_for<TM>([&](auto jm_c) {
+                constexpr int jm = decltype(jm_c)::value;
+                if constexpr (kBf16) {
+                    const i32x4 blo = {fb_cur[0], fb_cur[1], fb_cur[2], fb_cur[3]};
+                    const i32x4 bhi = {fb_cur[4], fb_cur[5], fb_cur[6], fb_cur[7]};
                     const i32x4 alo = {fa[jm][0], fa[jm][1], fa[jm][2], fa[jm][3]};
                     const i32x4 ahi = {fa[jm][4], fa[jm][5], fa[jm][6], fa[jm][7]};
                     acc[jn][jm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         __builtin_bit_cast(bf16x8, blo), __builtin_bit_cast(bf16x8, alo), acc[jn][jm], 0, 0, 0);
                     acc[jn][jm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         __builtin_bit_cast(bf16x8, bhi), __builtin_bit_cast(bf16x8, ahi), acc[jn][jm], 0, 0, 0);
-                }
-            }
-        } else {
-            const uint8_t* sSA = sA + A_BYTES + B_BYTES;
-            const uint8_t* sSB = sSA + SC_BYTES;
-            const i32x2 sa2 = *reinterpret_cast<const i32x2*>(sSA + (q * 16 + r) * 16 + wm * 8);
-            const i32x2 sb2 = *reinterpret_cast<const i32x2*>(sSB + (q * 16 + r) * 16 + wn * 8);
-            static_for<TN>([&](auto jn_c) {
-                constexpr int jn = decltype(jn_c)::value;
-                const i32x8 fb = load_frag(sB, wn * WN + jn * 16 + r, Int<SPRB>{});
-                static_for<TM>([&](auto jm_c) {
-                    constexpr int jm = decltype(jm_c)::value;
+                } else {
                     acc[jn][jm] = mfma_scaled<kFmtB, kFmtA, jn % 4, jm % 4>(
-                        fb, fa[jm], acc[jn][jm], sb2[jn / 4], sa2[jm / 4]);
-                });
+                        fb_cur, fa[jm], acc[jn][jm], sb2[jn / 4], sa2[jm / 4]);
+                }
             });
-        }
+            constexpr int kScaleLoads = (!kBf16 && jn == 0) ? NSA + NSB : 0;
+            constexpr int kVmem = (jn * kLPG >= NL ? 0 : (NL - jn * kLPG < kLPG ? NL - jn * kLPG : kLPG)) + kScaleLoads;
+            constexpr int kDs = jn + 1 < TN ? 2 : 0;
+            if constexpr (jn == 0) issue_scales(cn, next);
+            static_for<kLPG>([&](auto li) {
+                constexpr int idx = jn * kLPG + decltype(li)::value;
+                if constexpr (idx < NL) issue_one(Int<idx>{}, cn, s ^ 1, next);
+            });
+            // interleave: each MFMA is followed by at most one LDS read and one buffer load
+            static_for<TM>([&](auto i_c) {
+                constexpr int i = decltype(i_c)::value;
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if constexpr (i < kDs) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if constexpr (i < kVmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            fb_cur = fb_next;
+        });
     };
 
     // ------------------------------------------------------------------ main loop
     if (num_chunks > 0) {
         issue_data(0, 0);
-        issue_scales(0);
+        issue_scales(0, true);
     }
     for (int c = 0; c < num_chunks; ++c) {
         const int s = c & 1;
         __builtin_amdgcn_s_waitcnt(0);   // chunk c data (LDS) and scales (VGPR) have landed
         write_scales(s);
         __syncthreads();
-        if (c + 1 < num_chunks) {
-            issue_data(c + 1, s ^ 1);
-            issue_scales(c + 1);
-        }
-        compute(s);
+        compute(s, c + 1, c + 1 < num_chunks && p.dbg != 10);
     }
-
     // ------------------------------------------------------------------ epilogue
+    // All accumulator indexing below is in compile-time-unrolled loops (static_for): a
+    // runtime index would demote the accumulator array to scratch memory.
     const float alpha = p.alpha;
-    const bool grouped_rows = p.gemm_type == kMGroupedPsum || p.gemm_type == kMGroupedIdx;
-#pragma unroll
-    for (int jm = 0; jm < TM; ++jm) {
-        const int m = m0 + wm * WM + jm * 16 + r;
-        if (m >= M) continue;
-        if (p.gemm_type == kMasked && m >= valid_end) continue;
-        bool pad_row = false;
-        if (p.gemm_type == kMGroupedPsum) pad_row = m >= valid_end;
-        else if (p.gemm_type == kMGroupedIdx) pad_row = p.layout[m] != group;
-        (void)grouped_rows;
-#pragma unroll
-        for (int jn = 0; jn < TN; ++jn) {
-            const int nbase = n0 + wn * WN + jn * 16 + 4 * q;
-            if (nbase >= N) continue;
-            float v[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = acc[jn][jm][i] * alpha;
-            if (pad_row) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = 0.f;
+    if constexpr (EPI == kEpiLdsBf16) {
+        // bf16 D without accumulation: alpha / bias / padding-row zeroing in registers, the
+        // tile staged through LDS as bf16, then written with 16-byte row-contiguous stores.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();                                     // all waves are done with the operands
+        const bool bias = p.has_bias;
+        const uint16_t* bp = reinterpret_cast<const uint16_t*>(p.bias);
+        static_for<TM>([&](auto jm_c) {
+            constexpr int jm = decltype(jm_c)::value;
+            const int ml = wm * WM + jm * 16 + r;
+            const int m = m0 + ml;
+            bool zero = false;
+            if (p.gemm_type == kMGroupedPsum) zero = m >= valid_end;
+            else if (p.gemm_type == kMGroupedIdx) zero = m < M && p.layout[m] != group;
+            static_for<TN>([&](auto jn_c) {
+                constexpr int jn = decltype(jn_c)::value;
+                const int nl = wn * WN + jn * 16 + 4 * q;
+                float v0 = acc[jn][jm][0] * alpha, v1 = acc[jn][jm][1] * alpha;
+                float v2 = acc[jn][jm][2] * alpha, v3 = acc[jn][jm][3] * alpha;
+                if (bias) {
+                    const int n = n0 + nl;
+                    v0 += n + 0 < N ? bf16_to_f32(bp[n + 0]) : 0.f;
+                    v1 += n + 1 < N ? bf16_to_f32(bp[n + 1]) : 0.f;
+                    v2 += n + 2 < N ? bf16_to_f32(bp[n + 2]) : 0.f;
+                    v3 += n + 3 < N ? bf16_to_f32(bp[n + 3]) : 0.f;
+                }
+                uint32_t lo = pack_bf16x2(v0, v1);
+                uint32_t hi = pack_bf16x2(v2, v3);
+                if (zero) lo = hi = 0;
+                *reinterpret_cast<i32x2*>(smem + ml * CROW + nl * 2) = i32x2{(int)lo, (int)hi};
+            });
+        });
+        __syncthreads();
+        const int rows = min(BM, (p.gemm_type == kMasked ? valid_end : M) - m0);
+        const int cols = min(BN, N - n0);
+        constexpr int CPR = BN * 2 / 16;                     // 16-byte chunks per tile row
+        uint16_t* dbase = reinterpret_cast<uint16_t*>(d_base);
+        for (int e = tid; e < BM * CPR; e += 256) {
+            const int row = e / CPR, ch = e % CPR;
+            if (row >= rows) break;
+            const int col = ch * 8;
+            if (col >= cols) continue;
+            const i32x4 val = *reinterpret_cast<const i32x4*>(smem + row * CROW + ch * 16);
+            uint16_t* dp = dbase + (int64_t)(m0 + row) * p.ldd + n0 + col;
+            if (col + 8 <= cols) {
+                *reinterpret_cast<i32x4*>(dp) = val;
             } else {
-                if (p.has_bias) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        if (nbase + i < N)
-                            v[i] += p.out_f32 ? reinterpret_cast<const float*>(p.bias)[nbase + i]
-                                              : bf16_to_f32(reinterpret_cast<const uint16_t*>(p.bias)[nbase + i]);
-                    }
-                }
-            }
-            const int64_t off = (int64_t)m * p.ldd + nbase;
-            const bool full = p.vec_store && nbase + 3 < N;
-            if (p.out_f32) {
-                float* dp = reinterpret_cast<float*>(d_base) + off;
-                if (full) {
-                    f32x4 o = {v[0], v[1], v[2], v[3]};
-                    if (p.accumulate && !pad_row) o += *reinterpret_cast<const f32x4*>(dp);
-                    *reinterpret_cast<f32x4*>(dp) = o;
-                } else {
-                    for (int i = 0; i < 4 && nbase + i < N; ++i)
-                        dp[i] = (p.accumulate && !pad_row) ? dp[i] + v[i] : v[i];
-                }
-            } else {
-                uint16_t* dp = reinterpret_cast<uint16_t*>(d_base) + off;
-                if (full) {
-                    if (p.accumulate && !pad_row) {
-                        const i32x2 old = *reinterpret_cast<const i32x2*>(dp);
-                        v[0] += bf16_to_f32((uint16_t)(old[0] & 0xffff));
-                        v[1] += bf16_to_f32((uint16_t)((uint32_t)old[0] >> 16));
-                        v[2] += bf16_to_f32((uint16_t)(old[1] & 0xffff));
-                        v[3] += bf16_to_f32((uint16_t)((uint32_t)old[1] >> 16));
-                    }
-                    i32x2 o;
-                    o[0] = (int)((uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16));
-                    o[1] = (int)((uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16));
-                    *reinterpret_cast<i32x2*>(dp) = o;
-                } else {
-                    for (int i = 0; i < 4 && nbase + i < N; ++i) {
-                        float x = v[i];
-                        if (p.accumulate && !pad_row) x += bf16_to_f32(dp[i]);
-                        dp[i] = f32_to_bf16_rne(x);
-                    }
-                }
+                const uint16_t* hv = reinterpret_cast<const uint16_t*>(&val);
+                for (int i = 0; i < cols - col; ++i) dp[i] = hv[i];
             }
         }
+        stamp(1);
+    } else {
+        // fp32 D (EPI == kEpiF32) or bf16 D with accumulation / unaligned rows (kEpiBf16):
+        // direct stores of each lane's four consecutive columns.
+        constexpr bool kF32 = EPI == kEpiF32;
+        using OutT = std::conditional_t<kF32, float, uint16_t>;
+        OutT* dbase = reinterpret_cast<OutT*>(d_base);
+        const OutT* bp = reinterpret_cast<const OutT*>(p.bias);
+        const bool acc_old = p.accumulate, bias = p.has_bias, vec = p.vec_store;
+        auto to_f = [](OutT x) -> float {
+            if constexpr (kF32) return x; else return bf16_to_f32(x);
+        };
+        auto from_f = [](float x) -> OutT {
+            if constexpr (kF32) return x; else return f32_to_bf16_rne(x);
+        };
+        static_for<TM>([&](auto jm_c) {
+            constexpr int jm = decltype(jm_c)::value;
+            const int m = m0 + wm * WM + jm * 16 + r;
+            const bool row_ok = m < M && !(p.gemm_type == kMasked && m >= valid_end);
+            bool pad_row = false;
+            if (p.gemm_type == kMGroupedPsum) pad_row = m >= valid_end;
+            else if (p.gemm_type == kMGroupedIdx) pad_row = row_ok && p.layout[m] != group;
+            static_for<TN>([&](auto jn_c) {
+                constexpr int jn = decltype(jn_c)::value;
+                const int nb = n0 + wn * WN + jn * 16 + 4 * q;
+                float v[4] = {acc[jn][jm][0] * alpha, acc[jn][jm][1] * alpha,
+                              acc[jn][jm][2] * alpha, acc[jn][jm][3] * alpha};
+                if (row_ok && nb < N) {
+                    OutT* dp = dbase + (int64_t)m * p.ldd + nb;
+                    if (vec && nb + 3 < N) {
+                        if constexpr (kF32) {
+                            f32x4 o = {v[0], v[1], v[2], v[3]};
+                            if (bias) o += f32x4{bp[nb], bp[nb + 1], bp[nb + 2], bp[nb + 3]};
+                            if (acc_old) o += *reinterpret_cast<const f32x4*>(dp);
+                            if (pad_row) o = f32x4{0.f, 0.f, 0.f, 0.f};
+                            *reinterpret_cast<f32x4*>(dp) = o;
+                        } else {
+                            if (bias) {
+                                const i32x2 b2 = *reinterpret_cast<const i32x2*>(bp + nb);
+                                v[0] += bf16_to_f32((uint16_t)(b2[0] & 0xffff));
+                                v[1] += bf16_to_f32((uint16_t)((uint32_t)b2[0] >> 16));
+                                v[2] += bf16_to_f32((uint16_t)(b2[1] & 0xffff));
+                                v[3] += bf16_to_f32((uint16_t)((uint32_t)b2[1] >> 16));
+                            }
+                            if (acc_old) {
+                                const i32x2 o2 = *reinterpret_cast<const i32x2*>(dp);
+                                v[0] += bf16_to_f32((uint16_t)(o2[0] & 0xffff));
+                                v[1] += bf16_to_f32((uint16_t)((uint32_t)o2[0] >> 16));
+                                v[2] += bf16_to_f32((uint16_t)(o2[1] & 0xffff));
+                                v[3] += bf16_to_f32((uint16_t)((uint32_t)o2[1] >> 16));
+                            }
+                            uint32_t lo = pack_bf16x2(v[0], v[1]);
+                            uint32_t hi = pack_bf16x2(v[2], v[3]);
+                            if (pad_row) lo = hi = 0;
+                            *reinterpret_cast<i32x2*>(dp) = i32x2{(int)lo, (int)hi};
+                        }
+                    } else {
+                        for (int i = 0; i < 4 && nb + i < N; ++i) {
+                            float x = v[i];
+                            if (bias) x += to_f(bp[nb + i]);
+                            if (acc_old) x += to_f(dp[i]);
+                            dp[i] = pad_row ? from_f(0.f) : from_f(x);
+                        }
+                    }
+                }
+            });
+        });
     }
 }
 

@@ -10,6 +10,7 @@ The kernels read K-major operands with 16-byte-aligned rows.  Operands given MN-
 with a K extent / stride that is not 16-byte aligned, are first copied into that layout on
 the device (a layout conversion, not a change of the arithmetic).
 """
+import os
 from typing import Optional, Tuple
 
 import torch
@@ -115,6 +116,9 @@ def _fill_common(args, d, k_kernel, alpha, kind):
     args.k = k_kernel
     args.num_cus = get_num_sms()
     args.alignment = get_mk_alignment_for_contiguous_layout()
+    forced = os.environ.get('DG_FORCE_BLOCK')   # e.g. "256x224": tuning override of the heuristic
+    if forced:
+        args.block_m, args.block_n = (int(x) for x in forced.split('x'))
 
 
 def _early_return(m, n, k, d, c, is_cd_same, with_bias) -> bool:
