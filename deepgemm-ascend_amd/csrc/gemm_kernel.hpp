@@ -510,12 +510,6 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const KParams p) {
         OutT* dbase = reinterpret_cast<OutT*>(d_base);
         const OutT* bp = reinterpret_cast<const OutT*>(p.bias);
         const bool acc_old = p.accumulate, bias = p.has_bias, vec = p.vec_store;
-        auto to_f = [](OutT x) -> float {
-            if constexpr (kF32) return x; else return bf16_to_f32(x);
-        };
-        auto from_f = [](float x) -> OutT {
-            if constexpr (kF32) return x; else return f32_to_bf16_rne(x);
-        };
         static_for<TM>([&](auto jm_c) {
             constexpr int jm = decltype(jm_c)::value;
             const int m = m0 + wm * WM + jm * 16 + r;
@@ -523,50 +517,100 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const KParams p) {
             bool pad_row = false;
             if (p.gemm_type == kMGroupedPsum) pad_row = m >= valid_end;
             else if (p.gemm_type == kMGroupedIdx) pad_row = row_ok && p.layout[m] != group;
-            static_for<TN>([&](auto jn_c) {
-                constexpr int jn = decltype(jn_c)::value;
-                const int nb = n0 + wn * WN + jn * 16 + 4 * q;
-                float v[4] = {acc[jn][jm][0] * alpha, acc[jn][jm][1] * alpha,
-                              acc[jn][jm][2] * alpha, acc[jn][jm][3] * alpha};
-                if (row_ok && nb < N) {
-                    OutT* dp = dbase + (int64_t)m * p.ldd + nb;
-                    if (vec && nb + 3 < N) {
-                        if constexpr (kF32) {
+            OutT* drow = dbase + (int64_t)m * p.ldd;
+            if constexpr (kF32) {
+                static_for<TN>([&](auto jn_c) {
+                    constexpr int jn = decltype(jn_c)::value;
+                    const int nb = n0 + wn * WN + jn * 16 + 4 * q;
+                    float v[4] = {acc[jn][jm][0] * alpha, acc[jn][jm][1] * alpha,
+                                  acc[jn][jm][2] * alpha, acc[jn][jm][3] * alpha};
+                    if (row_ok && nb < N) {
+                        float* dp = drow + nb;
+                        if (vec && nb + 3 < N) {
                             f32x4 o = {v[0], v[1], v[2], v[3]};
                             if (bias) o += f32x4{bp[nb], bp[nb + 1], bp[nb + 2], bp[nb + 3]};
                             if (acc_old) o += *reinterpret_cast<const f32x4*>(dp);
                             if (pad_row) o = f32x4{0.f, 0.f, 0.f, 0.f};
                             *reinterpret_cast<f32x4*>(dp) = o;
                         } else {
-                            if (bias) {
-                                const i32x2 b2 = *reinterpret_cast<const i32x2*>(bp + nb);
-                                v[0] += bf16_to_f32((uint16_t)(b2[0] & 0xffff));
-                                v[1] += bf16_to_f32((uint16_t)((uint32_t)b2[0] >> 16));
-                                v[2] += bf16_to_f32((uint16_t)(b2[1] & 0xffff));
-                                v[3] += bf16_to_f32((uint16_t)((uint32_t)b2[1] >> 16));
+                            for (int i = 0; i < 4 && nb + i < N; ++i) {
+                                float x = v[i];
+                                if (bias) x += bp[nb + i];
+                                if (acc_old) x += dp[i];
+                                dp[i] = pad_row ? 0.f : x;
                             }
-                            if (acc_old) {
-                                const i32x2 o2 = *reinterpret_cast<const i32x2*>(dp);
-                                v[0] += bf16_to_f32((uint16_t)(o2[0] & 0xffff));
-                                v[1] += bf16_to_f32((uint16_t)((uint32_t)o2[0] >> 16));
-                                v[2] += bf16_to_f32((uint16_t)(o2[1] & 0xffff));
-                                v[3] += bf16_to_f32((uint16_t)((uint32_t)o2[1] >> 16));
-                            }
-                            uint32_t lo = pack_bf16x2(v[0], v[1]);
-                            uint32_t hi = pack_bf16x2(v[2], v[3]);
-                            if (pad_row) lo = hi = 0;
-                            *reinterpret_cast<i32x2*>(dp) = i32x2{(int)lo, (int)hi};
-                        }
-                    } else {
-                        for (int i = 0; i < 4 && nb + i < N; ++i) {
-                            float x = v[i];
-                            if (bias) x += to_f(bp[nb + i]);
-                            if (acc_old) x += to_f(dp[i]);
-                            dp[i] = pad_row ? from_f(0.f) : from_f(x);
                         }
                     }
-                }
-            });
+                });
+            } else {
+                // Round every block to bf16 pairs (bias / accumulation in fp32 first).
+                uint32_t pk[TN][2];
+                static_for<TN>([&](auto jn_c) {
+                    constexpr int jn = decltype(jn_c)::value;
+                    const int nb = n0 + wn * WN + jn * 16 + 4 * q;
+                    float v[4] = {acc[jn][jm][0] * alpha, acc[jn][jm][1] * alpha,
+                                  acc[jn][jm][2] * alpha, acc[jn][jm][3] * alpha};
+                    const bool full = vec && nb + 3 < N;
+                    if (bias) {
+                        if (full) {
+                            const i32x2 b2 = *reinterpret_cast<const i32x2*>(bp + nb);
+                            v[0] += bf16_to_f32((uint16_t)(b2[0] & 0xffff));
+                            v[1] += bf16_to_f32((uint16_t)((uint32_t)b2[0] >> 16));
+                            v[2] += bf16_to_f32((uint16_t)(b2[1] & 0xffff));
+                            v[3] += bf16_to_f32((uint16_t)((uint32_t)b2[1] >> 16));
+                        } else {
+                            for (int i = 0; i < 4; ++i) v[i] += nb + i < N ? bf16_to_f32(bp[nb + i]) : 0.f;
+                        }
+                    }
+                    if (acc_old && row_ok) {
+                        if (full) {
+                            const i32x2 o2 = *reinterpret_cast<const i32x2*>(drow + nb);
+                            v[0] += bf16_to_f32((uint16_t)(o2[0] & 0xffff));
+                            v[1] += bf16_to_f32((uint16_t)((uint32_t)o2[0] >> 16));
+                            v[2] += bf16_to_f32((uint16_t)(o2[1] & 0xffff));
+                            v[3] += bf16_to_f32((uint16_t)((uint32_t)o2[1] >> 16));
+                        } else {
+                            for (int i = 0; i < 4; ++i) v[i] += nb + i < N ? bf16_to_f32(drow[nb + i]) : 0.f;
+                        }
+                    }
+                    pk[jn][0] = pad_row ? 0u : pack_bf16x2(v[0], v[1]);
+                    pk[jn][1] = pad_row ? 0u : pack_bf16x2(v[2], v[3]);
+                });
+                // Stores.  Two n-blocks (jn0, jn0 + 1) are regrouped across the lane halves of
+                // each 32-lane row with v_permlane16_swap so that every lane owns 8 consecutive
+                // columns: one 16-byte store per lane, 64 contiguous bytes per row.
+                auto store8 = [&](auto jn_c) {
+                    constexpr int jn = decltype(jn_c)::value;
+                    const int nb = n0 + wn * WN + jn * 16 + 4 * q;
+                    if (!row_ok || nb >= N) return;
+                    uint16_t* dp = drow + nb;
+                    if (vec && nb + 3 < N) {
+                        *reinterpret_cast<i32x2*>(dp) = i32x2{(int)pk[jn][0], (int)pk[jn][1]};
+                    } else {
+                        for (int i = 0; i < 4 && nb + i < N; ++i)
+                            dp[i] = (uint16_t)(pk[jn][i >> 1] >> ((i & 1) * 16));
+                    }
+                };
+                static_for<(TN + 1) / 2>([&](auto jp_c) {
+                    constexpr int jn0 = 2 * decltype(jp_c)::value;
+                    if constexpr (jn0 + 1 < TN) {
+                        const int nbase = n0 + wn * WN + jn0 * 16;      // wave-uniform
+                        if (vec && nbase + 32 <= N) {
+                            const auto s0 = __builtin_amdgcn_permlane16_swap(pk[jn0][0], pk[jn0 + 1][0], false, false);
+                            const auto s1 = __builtin_amdgcn_permlane16_swap(pk[jn0][1], pk[jn0 + 1][1], false, false);
+                            const int ncol = nbase + ((q & 1) ? 16 + 4 * (q - 1) : 4 * q);
+                            if (row_ok)
+                                *reinterpret_cast<i32x4*>(drow + ncol) =
+                                    i32x4{(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
+                        } else {
+                            store8(Int<jn0>{});
+                            store8(Int<jn0 + 1>{});
+                        }
+                    } else {
+                        store8(Int<jn0>{});
+                    }
+                });
+            }
         });
     }
 }
