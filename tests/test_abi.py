@@ -1,0 +1,104 @@
+"""C ABI of libdeep_gemm_amd.so: loads without a GPU, exports every symbol the header
+declares, and rejects bad arguments with error codes (no kernel is launched here)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from deep_gemm import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / 'include' / 'deep_gemm_amd.h'
+
+
+@pytest.fixture(scope='module')
+def lib():
+    path = _lib.library_path()
+    if not path.exists():
+        import importlib.util
+        spec = importlib.util.spec_from_file_location('dg_build', ROOT / 'deepgemm-ascend_amd' / 'build.py')
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    return _lib.load()
+
+
+def _declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r'^\s*(?:int|const char \*)\s*(dg_\w+)\s*\(', text, re.M)))
+
+
+def test_header_declares_the_binding_table():
+    assert _declared_symbols() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_empty_error(lib):
+    assert b'gfx950' in lib.dg_version()
+    assert lib.dg_last_error() is not None
+
+
+def test_gemm_rejects_null_and_bad_kind(lib):
+    assert lib.dg_gemm(None, None) == -1
+    assert b'null args' in lib.dg_last_error()
+    args = _lib.GemmArgs()
+    args.kind = 9
+    assert lib.dg_gemm(ctypes.byref(args), None) == -1
+    assert b'unknown kind' in lib.dg_last_error()
+
+
+def test_gemm_rejects_misaligned_rows(lib):
+    args = _lib.GemmArgs()
+    args.kind, args.gemm_type, args.m, args.n, args.k = 0, 0, 64, 64, 100   # K=100 bytes: not 16-aligned
+    args.a = args.b = args.d = 4096
+    args.sfa = args.sfb = 4096
+    args.lda = args.ldb = 100
+    args.ldd = 64
+    assert lib.dg_gemm(ctypes.byref(args), None) == -1
+    assert b'16-byte aligned' in lib.dg_last_error()
+
+
+def test_gemm_zero_size_is_a_noop(lib):
+    args = _lib.GemmArgs()
+    args.kind, args.m, args.n, args.k = 0, 0, 64, 128
+    assert lib.dg_gemm(ctypes.byref(args), None) == 0
+
+
+def test_grouped_requires_layout(lib):
+    args = _lib.GemmArgs()
+    args.kind, args.gemm_type, args.m, args.n, args.k, args.num_groups = 0, 2, 256, 256, 128, 4
+    args.a = args.b = args.d = args.sfa = args.sfb = 4096
+    args.lda = args.ldb = 128
+    args.ldd = 256
+    args.alignment = 256
+    assert lib.dg_gemm(ctypes.byref(args), None) == -1
+    assert b'grouped_layout required' in lib.dg_last_error()
+
+
+def test_select_config_respects_grouped_alignment(lib):
+    for align in (256, 128, 64, 32):
+        args = _lib.GemmArgs()
+        args.kind, args.gemm_type, args.m, args.n, args.k, args.num_groups = 0, 2, 8192, 4096, 7168, 32
+        args.alignment, args.num_cus = align, 256
+        bm, bn = ctypes.c_int32(), ctypes.c_int32()
+        assert lib.dg_select_config(ctypes.byref(args), ctypes.byref(bm), ctypes.byref(bn)) == 0
+        assert align % bm.value == 0 and bn.value > 0
+
+
+def test_transform_sf_argument_checks(lib):
+    f = lib.dg_transform_sf
+    # gran_mn not a power of two
+    assert f(4096, 0, 0, 1, 1, 1, 10, 1, 30, 32, 3, 32, None, 0, 256, 4096, 0, None, None) == -1
+    assert b'power of two' in lib.dg_last_error()
+    # fp32 SF with gran_k 64
+    assert f(4096, 0, 0, 1, 1, 1, 10, 1, 10, 64, 1, 64, None, 0, 256, 4096, 0, None, None) == -1
+    # wrong sf_k extent
+    assert f(4096, 0, 0, 1, 1, 1, 10, 5, 10, 64, 1, 32, None, 0, 256, 4096, 0, None, None) == -1
+    assert b'sf_k' in lib.dg_last_error()
+    # psum with an alignment that gran_mn does not divide
+    assert f(4096, 0, 0, 1, 1, 1, 1, 2, 128, 64, 128, 32, 4096, 2, 64, 4096, 0, None, None) == -1

@@ -1,0 +1,143 @@
+"""Host-side behaviour of the deep_gemm API that needs no GPU: validation order and
+messages (the reference's csrc/apis/gemm.hpp and csrc/apis/layout.hpp), recipe
+resolution, layout pass-through, and the lazy, fork-safe import."""
+import subprocess
+import sys
+
+import pytest
+import torch
+
+import deep_gemm
+from deep_gemm import layout as dl
+
+
+def test_aliases_are_the_same_objects():
+    assert deep_gemm.fp8_gemm_nt is deep_gemm.fp8_fp4_gemm_nt
+    assert deep_gemm.fp8_gemm_tt is deep_gemm.fp8_fp4_gemm_tt
+    assert deep_gemm.m_grouped_fp8_gemm_nt_contiguous is deep_gemm.m_grouped_fp8_fp4_gemm_nt_contiguous
+    assert deep_gemm.m_grouped_fp8_gemm_nt_masked is deep_gemm.m_grouped_fp8_fp4_gemm_nt_masked
+
+
+def test_default_arguments_match_reference():
+    import inspect
+    sig = inspect.signature(deep_gemm.fp8_fp4_gemm_nt)
+    assert list(sig.parameters) == ['a', 'b', 'd', 'c', 'recipe', 'recipe_a', 'recipe_b', 'compiled_dims',
+                                    'disable_ue8m0_cast', 'alpha', 'epilogue']
+    assert sig.parameters['compiled_dims'].default == 'nk'
+    assert inspect.signature(deep_gemm.fp8_fp4_gemm_tn).parameters['compiled_dims'].default == 'mn'
+    sig = inspect.signature(deep_gemm.m_grouped_fp8_fp4_gemm_nt_contiguous)
+    assert list(sig.parameters)[:4] == ['a', 'b', 'd', 'grouped_layout']
+    assert sig.parameters['use_psum_layout'].default is True
+    sig = inspect.signature(deep_gemm.transform_sf_into_required_layout)
+    assert list(sig.parameters) == ['sf', 'mn', 'k', 'recipe', 'num_groups', 'is_sfa', 'disable_ue8m0_cast',
+                                    'psum_layout']
+
+
+def test_get_recipe_rules():
+    assert dl.get_recipe() == (1, 1, 32)
+    assert dl.get_recipe(recipe_a=(1, 128), recipe_b=(128, 128)) == (1, 128, 128)
+    with pytest.raises(RuntimeError, match='gran_k of recipe_a and recipe_b must be the same'):
+        dl.get_recipe(recipe_a=(1, 128), recipe_b=(1, 32))
+    with pytest.raises(RuntimeError):
+        dl.get_recipe(recipe=(1, 1, 32), recipe_a=(1, 32))
+    # MX-compatible mixed granularity is accepted per operand
+    assert dl.operand_recipes(recipe_a=(1, 128), recipe_b=(1, 32)) == ((1, 128), (1, 32))
+
+
+def _fp8(shape):
+    return torch.zeros(shape, dtype=torch.float8_e4m3fn)
+
+
+def test_alpha_and_bias_rejected_before_any_device_work():
+    a, b = _fp8((64, 128)), _fp8((32, 128))
+    sfa, sfb = torch.ones(64, 4), torch.ones(32, 4)
+    d = torch.empty(64, 32, dtype=torch.bfloat16)
+    bias = torch.zeros(1, 32, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match='alpha and bias cannot be used together'):
+        deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d, c=bias, alpha=2.0)
+
+
+def test_c_shape_validation():
+    a, b = _fp8((64, 128)), _fp8((32, 128))
+    d = torch.empty(64, 32, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="C must match D's pointer and shape"):
+        deep_gemm.fp8_gemm_nt((a, torch.ones(64, 4)), (b, torch.ones(32, 4)), d, c=torch.zeros(2, 32, dtype=torch.bfloat16))
+
+
+def test_shape_mismatch_is_reported():
+    a, b = _fp8((64, 128)), _fp8((32, 256))
+    d = torch.empty(64, 32, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="Conflicting shape dimension 'k'"):
+        deep_gemm.fp8_gemm_nt((a, torch.ones(64, 4)), (b, torch.ones(32, 8)), d)
+
+
+def test_ambiguous_major_axis():
+    a = torch.zeros(4, 4, dtype=torch.float8_e4m3fn).as_strided((4, 4), (1, 1))
+    b = _fp8((8, 4))
+    d = torch.empty(4, 8, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match='Ambiguous major axis'):
+        deep_gemm.fp8_gemm_nt((a, torch.ones(4, 1)), (b, torch.ones(8, 1)), d)
+
+
+def test_d_dtype_checked():
+    a, b = _fp8((64, 128)), _fp8((32, 128))
+    d = torch.empty(64, 32, dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        deep_gemm.fp8_gemm_nt((a, torch.ones(64, 4)), (b, torch.ones(32, 4)), d)
+
+
+def test_empty_m_returns_without_device_work():
+    a, b = _fp8((0, 128)), _fp8((32, 128))
+    d = torch.empty(0, 32, dtype=torch.bfloat16)
+    deep_gemm.fp8_gemm_nt((a, torch.ones(0, 4)), (b, torch.ones(32, 4)), d)
+
+
+def test_k_zero_zeroes_or_copies_d_on_host_tensors():
+    a, b = _fp8((8, 0)), _fp8((4, 0))
+    d = torch.full((8, 4), 3.0, dtype=torch.bfloat16)
+    deep_gemm.fp8_gemm_nt((a, torch.ones(8, 0)), (b, torch.ones(4, 0)), d)
+    assert torch.equal(d, torch.zeros(8, 4, dtype=torch.bfloat16))
+    bias = torch.arange(4, dtype=torch.bfloat16).reshape(1, 4)
+    deep_gemm.fp8_gemm_nt((a, torch.ones(8, 0)), (b, torch.ones(4, 0)), d, c=bias)
+    assert torch.equal(d, bias.expand(8, 4))
+
+
+def test_sf_layout_checks_and_passthrough():
+    sf = torch.zeros(4, 1000, dtype=torch.int16).t()         # [1000, 4] MN-major packed
+    assert dl.check_sf_layout(sf, 1000, 256, 1, 32, None) is True
+    assert deep_gemm.transform_sf_into_required_layout(sf, 1000, 256, (1, 1, 32), is_sfa=True) is sf
+    with pytest.raises(RuntimeError, match='is_sfa'):
+        deep_gemm.transform_sf_into_required_layout(sf, 1000, 256, (1, 1, 32))
+    with pytest.raises(RuntimeError, match='SF K extent'):
+        dl.check_sf_layout(torch.zeros(1000, 3, dtype=torch.int16), 1000, 256, 1, 32, None)
+    with pytest.raises(RuntimeError, match='disable_ue8m0_cast'):
+        deep_gemm.transform_sf_into_required_layout(torch.ones(8, 4), 8, 128, (1, 1, 32), is_sfa=True,
+                                                    disable_ue8m0_cast=True)
+
+
+def test_mk_alignment_setter():
+    old = deep_gemm.get_mk_alignment_for_contiguous_layout()
+    assert old == 256 == deep_gemm.get_theoretical_mk_alignment_for_contiguous_layout()
+    deep_gemm.set_mk_alignment_for_contiguous_layout(128)
+    assert deep_gemm.get_mk_alignment_for_contiguous_layout() == 128
+    with pytest.raises(RuntimeError):
+        deep_gemm.set_mk_alignment_for_contiguous_layout(100)
+    deep_gemm.set_mk_alignment_for_contiguous_layout(old)
+
+
+def test_unsupported_epilogues_raise():
+    a, b = _fp8((64, 128)), _fp8((32, 128))
+    d = torch.empty(64, 32, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match='not supported'):
+        deep_gemm.fp8_gemm_nt((a, torch.ones(64, 4)), (b, torch.ones(32, 4)), d,
+                              epilogue=deep_gemm.epilogue.BF16StochasticRounding())
+
+
+def test_import_is_lazy_and_fork_safe():
+    """Importing deep_gemm loads neither the HIP library nor a GPU context (the reference
+    keeps import fork-safe, tests/test_lazy_init.py)."""
+    code = ('import sys, torch; sys.path.insert(0, "deepgemm-ascend_amd"); import deep_gemm; '
+            'from deep_gemm import _lib; assert _lib._lib is None; '
+            'assert not torch.cuda.is_initialized(); print("ok")')
+    out = subprocess.run([sys.executable, '-c', code], capture_output=True, text=True, cwd=str(__import__('pathlib').Path(__file__).resolve().parents[1]))
+    assert out.returncode == 0 and 'ok' in out.stdout, out.stderr

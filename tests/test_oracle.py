@@ -1,0 +1,255 @@
+"""Pins the CPU oracle (oracle/) against closed forms, library routines and brute force.
+
+The reference ships no golden vectors for this path (all of its data is generated on the
+fly, tests/generators.py), so each oracle function is checked here against something that
+does not restate its own formula: torch's float8 decode, the e2m1 / UE8M0 bit-field
+definitions, fp64 triple loops, and algebraic properties.
+"""
+import math
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import quant, layout as ol, gemm as og
+
+
+# ----------------------------------------------------------------------------- UE8M0
+def _pow2_ceil(x: float) -> float:
+    """Smallest power of two >= x via frexp, clamped to the UE8M0 range [2^-126, 2^127]."""
+    if x == 0.0:
+        return 2.0 ** -126
+    m, e = math.frexp(x)          # x = m * 2^e, m in [0.5, 1)
+    p = e - 1 if m == 0.5 else e
+    return 2.0 ** min(max(p, -126), 127)
+
+
+def test_ceil_to_ue8m0_matches_frexp():
+    rng = random.Random(0)
+    vals = [rng.uniform(1e-6, 1e3) for _ in range(2000)] + [2.0 ** e for e in range(-120, 120)]
+    vals += [0.0, 1.0, 1.0000001, 0.9999999, 448.0, 1e-30, 3.0e38]
+    t = torch.tensor(vals, dtype=torch.float32)
+    got = quant.ceil_to_ue8m0(t)
+    for v, g in zip(t.tolist(), got.tolist()):
+        assert g == _pow2_ceil(v), (v, g)
+
+
+def test_ceil_to_ue8m0_negative_uses_magnitude():
+    t = torch.tensor([-3.0, -0.3, 3.0, 0.3])
+    assert quant.ceil_to_ue8m0(t).tolist() == [4.0, 0.5, 4.0, 0.5]
+
+
+# ----------------------------------------------------------------------------- e4m3
+def test_e4m3_table_matches_torch_decode():
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    ref = codes.view(torch.float8_e4m3fn).float().numpy()
+    mine = quant.e4m3_decode_table()
+    nan = np.isnan(ref)
+    assert (np.isnan(mine) == nan).all()
+    assert nan.sum() == 2 and nan[0x7f] and nan[0xff]
+    assert (mine[~nan] == ref[~nan]).all()
+    assert mine[0x7e] == 448.0 and mine[0x01] == 2.0 ** -9
+
+
+def test_e4m3_quantize_is_nearest_and_in_range():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(64, 256, generator=g) * 3
+    data, sf, deq = quant.quantize_blockwise(x, (1, 128), 'e4m3')
+    assert not torch.isnan(deq).any()
+    vals = torch.from_numpy(quant.e4m3_decode_table())
+    vals = vals[~torch.isnan(vals)].unique()
+    full = quant.expand_sf(sf, x.shape, (1, 128))
+    scaled = x / full
+    assert scaled.abs().max() <= 448.0
+    # every code is a nearest representable value of x / sf
+    dist = (scaled.reshape(-1, 1) - vals.reshape(1, -1)).abs()
+    best = dist.min(dim=1).values
+    got = (scaled.reshape(-1) - deq.reshape(-1) / full.reshape(-1)).abs()
+    assert torch.all(got <= best + 1e-12)
+
+
+def test_quantize_block_scale_is_absmax_over_448_ceiled():
+    x = torch.zeros(1, 256)
+    x[0, 5] = 100.0          # block 0 absmax 100 -> 100/448 -> ceil pow2 = 0.25
+    x[0, 200] = -1.0         # block 1 absmax 1 -> 1/448 -> 2^-8
+    _, sf, _ = quant.quantize_blockwise(x, (1, 128), 'e4m3')
+    assert sf.tolist() == [[0.25, 2.0 ** -8]]
+
+
+# ----------------------------------------------------------------------------- e2m1
+def _e2m1_value(code: int) -> float:
+    s = -1.0 if code & 8 else 1.0
+    e = (code >> 1) & 3
+    m = code & 1
+    mag = (m / 2.0) if e == 0 else (1.0 + m / 2.0) * 2.0 ** (e - 1)
+    return s * mag
+
+
+def test_fp4_table_matches_bitfield_definition():
+    assert list(quant.FP4_VALUES) == [_e2m1_value(c) for c in range(16)]
+
+
+def test_fp4_quantize_nearest_ties_to_lower_magnitude():
+    xs = torch.linspace(-7, 7, 2801)
+    codes = quant.quantize_fp4_codes(xs)
+    mags = sorted(set(abs(v) for v in quant.FP4_VALUES))
+    for x, c in zip(xs.tolist(), codes.tolist()):
+        v = quant.FP4_VALUES[c]
+        ax = abs(x)
+        best = min(mags, key=lambda m: (abs(ax - m), m))
+        assert abs(v) == best, (x, v)
+        if v != 0:
+            assert (v < 0) == (x < 0)
+
+
+def test_fp4_pack_low_nibble_is_even_element_and_roundtrips():
+    codes = torch.tensor([[1, 2, 3, 15]], dtype=torch.uint8)
+    packed = quant.pack_fp4(codes, 1)
+    assert packed.view(torch.uint8).tolist() == [[0x21, 0xf3]]
+    g = torch.Generator().manual_seed(2)
+    c = torch.randint(0, 16, (6, 10), generator=g, dtype=torch.uint8)
+    for major in (0, 1):
+        p = quant.pack_fp4(c, major)
+        back = quant.unpack_fp4(p, major)
+        ref = torch.tensor([[quant.FP4_VALUES[v] for v in row] for row in c.tolist()])
+        assert torch.equal(back, ref)
+
+
+# ----------------------------------------------------------------------------- SF layout
+def test_transform_sf_known_answer():
+    sf = torch.tensor([[2.0 ** -3, 2.0 ** 5, 1.0]])        # 3 blocks of 32 -> K = 96
+    out = ol.transform_sf(sf, 1, 96, 1)
+    # exponents 124, 132, 127 (+ zero pad byte), little-endian pairs
+    assert out.shape == (1, 2) and out.stride() == (1, 1)
+    assert out.view(torch.uint16).tolist() == [[132 << 8 | 124, 127]]
+
+
+def _transform_brute(sf, mn, k, gran_mn, gran_k=32):
+    """Element-by-element definition of the packed layout."""
+    rows, k64 = mn, (k + 63) // 64
+    out = torch.zeros(rows, k64, dtype=torch.int32)
+    for i in range(rows):
+        for j in range(k64):
+            if sf.dtype == torch.int16:          # packed input passes through unchanged
+                out[i, j] = int(sf[i // gran_mn, j]) & 0xffff
+                continue
+            word = 0
+            for h in range(2):
+                blk = 2 * j + h
+                if blk >= (k + 31) // 32:
+                    continue
+                src = sf[i // gran_mn, blk // (gran_k // 32)]
+                byte = (int(src.view(torch.int32)) >> 23) & 0xff
+                word |= byte << (8 * h)
+            out[i, j] = word
+    return out
+
+
+@pytest.mark.parametrize('dtype,gran_mn,gran_k,mn,k', [(torch.float32, 1, 32, 9, 300), (torch.float32, 4, 32, 10, 64),
+                                                        (torch.float32, 1, 128, 7, 1000), (torch.int16, 2, 32, 9, 200)])
+def test_transform_sf_matches_elementwise_definition(dtype, gran_mn, gran_k, mn, k):
+    g = torch.Generator().manual_seed(mn + k)
+    if dtype == torch.float32:
+        e = torch.randint(1, 255, ((mn + gran_mn - 1) // gran_mn, (k + gran_k - 1) // gran_k), generator=g, dtype=torch.int32)
+        sf = (e << 23).view(torch.float32)
+    else:
+        sf = torch.randint(-32768, 32768, ((mn + gran_mn - 1) // gran_mn, (k + 63) // 64), generator=g).to(torch.int16)
+    out = ol.transform_sf(sf, mn, k, gran_mn, gran_k)
+    assert out.stride(-2) == 1
+    ref = _transform_brute(sf, mn, k, gran_mn, gran_k)
+    assert torch.equal(out.view(torch.uint16).to(torch.int32), ref)
+
+
+def test_transform_sf_psum_zeroes_padding_rows():
+    sizes, align = [3, 0, 5], 8
+    total, ps = ol.psum_from_sizes(sizes, align)
+    assert ps == [3, 8, 13] and total == 16
+    sf = torch.full((total, 1), 2.0)
+    out = ol.transform_sf(sf, total, 32, 1, psum=ps, alignment=align)
+    exp = [128 if (r < 3 or 8 <= r < 13) else 0 for r in range(total)]
+    assert out[:, 0].tolist() == exp
+
+
+def test_psum_helpers_and_m_indices():
+    total, ps = ol.psum_from_sizes([5, 0, 130, 1], 128)
+    assert ps == [5, 128, 258, 385] and total == 512
+    spans = list(ol.psum_slices(ps, 128))
+    assert spans == [slice(0, 5), slice(128, 128), slice(128, 258), slice(384, 385)]
+    idx = ol.m_indices_from_psum(ps, 128, total)
+    for g, sl in enumerate(spans):
+        assert (idx[sl] == g).all()
+    assert int((idx == -1).sum()) == total - 5 - 130 - 1
+    pads = list(ol.psum_pad_slices(ps, 128))
+    assert pads == [slice(5, 128), slice(258, 384), slice(385, 512)]
+
+
+# ----------------------------------------------------------------------------- GEMM
+def test_calc_diff_closed_forms():
+    x = torch.randn(100, generator=torch.Generator().manual_seed(3))
+    assert og.calc_diff(x, x) == pytest.approx(0.0, abs=1e-12)
+    assert og.calc_diff(x, -x) == pytest.approx(2.0)
+    assert og.calc_diff(x, torch.zeros_like(x)) == pytest.approx(1.0)
+    assert og.calc_diff(x, 2 * x) == pytest.approx(1 - 4 / 5)
+    a, b = torch.tensor([1.0, 0.0]), torch.tensor([0.0, 1.0])
+    assert og.calc_diff(a, b) == pytest.approx(1.0)
+    assert og.calc_diff(torch.zeros(3), torch.zeros(3)) == 0.0
+
+
+def test_gemm_nt_matches_fp64_brute_force():
+    g = torch.Generator().manual_seed(4)
+    a, sfa, a_deq = quant.random_codes((5, 96), 'e4m3', -1, g, (1, 32))
+    b, sfb, b_deq = quant.random_codes((7, 96), 'e4m3', -1, g, (1, 32))
+    d = og.gemm_nt(a_deq, b_deq, torch.float32)
+    ref = og.brute_force_nt(a_deq, b_deq)
+    assert torch.allclose(d.double(), ref, rtol=1e-5, atol=1e-6)
+    bias = torch.randn(1, 7, generator=g)
+    d2 = og.gemm_nt(a_deq, b_deq, torch.float32, alpha=-2.0, bias=bias)
+    assert torch.allclose(d2.double(), -2.0 * ref + bias.double(), rtol=1e-5, atol=1e-5)
+
+
+def test_gemm_identity_and_linearity():
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(9, 16, generator=g)
+    eye = torch.eye(16)
+    assert torch.equal(og.gemm_nt(a, eye, torch.float32), a)
+    b1, b2 = torch.randn(4, 16, generator=g), torch.randn(4, 16, generator=g)
+    lhs = og.gemm_nt(a, b1 + b2, torch.float32)
+    rhs = og.gemm_nt(a, b1, torch.float32) + og.gemm_nt(a, b2, torch.float32)
+    assert torch.allclose(lhs, rhs, atol=1e-5)
+
+
+@pytest.mark.parametrize('kind,gran', [('e4m3', (1, 128)), ('e4m3', (128, 128)), ('e2m1', (1, 32)), ('e4m3', (1, 32))])
+def test_dequant_from_packed_sf_matches_generator(kind, gran):
+    """The kernel-side view (codes + packed int16 SF) decodes to the generator's fp32 values."""
+    g = torch.Generator().manual_seed(6)
+    rows, k = 130, 384
+    data, sf, deq = quant.quantize_blockwise(torch.randn(rows, k, generator=g), gran, kind)
+    packed = ol.transform_sf(sf, rows, k, gran[0], gran[1])
+    assert torch.equal(og.dequant_operand(data, packed, k), deq)
+
+
+def test_grouped_psum_and_m_indices_agree():
+    g = torch.Generator().manual_seed(7)
+    total, ps = ol.psum_from_sizes([40, 0, 17, 128], 64)
+    a = torch.randn(total, 32, generator=g)
+    b = torch.randn(4, 24, 32, generator=g)
+    d1 = og.m_grouped_contiguous(a, b, torch.tensor(ps), True, 64, torch.float32)
+    d2 = og.m_grouped_contiguous(a, b, ol.m_indices_from_psum(ps, 64, total), False, 64, torch.float32)
+    assert torch.equal(d1, d2)
+    assert torch.equal(d1[40:64], torch.zeros(24, 24))
+    assert ps == [40, 64, 81, 256]
+    assert torch.allclose(d1[64:81], a[64:81] @ b[2].T)
+    assert torch.equal(d1[81:128], torch.zeros(47, 24))
+    assert torch.allclose(d1[128:256], a[128:256] @ b[3].T)
+
+
+def test_masked_rows_beyond_count_are_zero():
+    g = torch.Generator().manual_seed(8)
+    a = torch.randn(3, 10, 16, generator=g)
+    b = torch.randn(3, 6, 16, generator=g)
+    masked = torch.tensor([10, 0, 4])
+    d = og.m_grouped_masked(a, b, masked, torch.float32)
+    assert torch.equal(d[1], torch.zeros(10, 6))
+    assert torch.equal(d[2, 4:], torch.zeros(6, 6))
+    assert torch.allclose(d[2, :4], a[2, :4] @ b[2].T)
