@@ -36,7 +36,20 @@ def parse():
     ap.add_argument('--m', type=int, default=M)
     ap.add_argument('--n', type=int, default=N)
     ap.add_argument('--k', type=int, default=K)
+    ap.add_argument('--calibrate-copy', action='store_true',
+                    help='run only a 256 MiB device copy (reference kernel for FETCH_SIZE / WRITE_SIZE scaling)')
     return ap.parse_args()
+
+
+def calibrate_copy():
+    import torch
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device='cuda').fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({'calibration': 'device copy', 'bytes_read_per_launch': n, 'bytes_written_per_launch': n}))
 
 
 def make_inputs(m, n, k):
@@ -81,6 +94,9 @@ def main():
         print(f'bench.py measures one GPU only (the hot path does not shard across GPUs in this build); '
               f'got --gpus {args.gpus}', file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     import torch
     import deep_gemm
     from oracle import gemm as og
@@ -118,8 +134,11 @@ def main():
     ms_total = start.elapsed_time(stop)
     ms_per_step = ms_total / args.steps
 
-    # per-launch kernel duration (events on the launch stream around each launch)
+    # per-launch kernel duration (events on the launch stream around each launch); a spin
+    # kernel first keeps the GPU busy while the host queues every launch, so host-side call
+    # overhead never lands between an event pair
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda._sleep(int(2e7))
     for e0, e1 in evs:
         e0.record()
         step()
