@@ -24,7 +24,7 @@ thread_local std::string g_last_error;
 
 }  // namespace
 
-extern "C" int dg_set_error(const char* msg) {
+extern "C" __attribute__((visibility("hidden"))) int dg_set_error(const char* msg) {
     g_last_error = msg;
     return DG_EINVAL;
 }

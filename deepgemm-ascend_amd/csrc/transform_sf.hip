@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
 
 }  // namespace dg
 
-extern "C" int dg_set_error(const char* msg);
+extern "C" __attribute__((visibility("hidden"))) int dg_set_error(const char* msg);
 
 extern "C" int dg_transform_sf(const void* src, int32_t src_kind, int64_t stride_b, int64_t stride_mn,
                                int64_t stride_k, int32_t num_batches, int32_t sf_mn, int32_t sf_k,
