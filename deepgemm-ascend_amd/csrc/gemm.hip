@@ -5,8 +5,8 @@
 // bf16_gemm.hpp:16-78) and its select_gemm_config cost model
 // (csrc/jit_kernels/heuristics.hpp:592-755).  Kernels are compiled ahead of time for a
 // fixed menu of tile shapes; the heuristic scores each shape with a gfx950 model
-// (256 CUs, waves-of-tiles quantisation, LDS-read efficiency of the wave tile) and memoises
-// the choice per problem signature.
+// (256 CUs, waves-of-tiles quantisation, measured cycles per K stage of each tile shape and a
+// fixed per-tile cost) and memoises the choice per problem signature.
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -67,14 +67,6 @@ int device_cus() {
     return cached[dev];
 }
 
-// Relative efficiency of a wave tile: LDS bytes read per MFMA flop falls with the wave
-// tile's (WM * WN) / (WM + WN); 128 x 128 wave tiles keep LDS below the MFMA rate.
-double tile_efficiency(int bm, int bn) {
-    const double wm = bm / 2.0, wn = bn / 2.0;
-    const double ratio = (wm * wn) / (wm + wn) / 64.0;
-    return ratio >= 1.0 ? 1.0 : ratio;
-}
-
 bool tile_allowed(const dg_gemm_args& a, int bm, int bn) {
     if (a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) {
         if (a.alignment % bm != 0) return false;
@@ -86,17 +78,16 @@ bool tile_allowed(const dg_gemm_args& a, int bm, int bn) {
 TileCfg select_tile(const dg_gemm_args& a, int cus) {
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
     double best = 1e300;
-    TileCfg pick = {0, 0};
+    TileCfg pick = {0, 0, 0, 0, 0, 0};
     for (int i = 0; i < kNumTiles; ++i) {
         const int bm = kTiles[i].bm, bn = kTiles[i].bn;
         if (!tile_allowed(a, bm, bn)) continue;
         const int64_t tiles = (int64_t)ceil_div(a.m, bm) * ceil_div(a.n, bn) * groups;
         const int64_t rounds = ceil_div64(tiles, cus);
-        // compute term: padded tile flops at the tile's efficiency
-        const double t_mma = (double)rounds * bm * bn / tile_efficiency(bm, bn);
-        // memory term: operand bytes streamed per round per CU (L2-level), weighted lightly
-        const double t_mem = (double)rounds * (bm + bn) * 40.0;
-        const double t = t_mma + t_mem;
+        // Waves of tiles x (K stages at the tile's measured stage time + the fixed cost of a
+        // tile: pipeline fill and the epilogue's stores).
+        const double t_tile = (double)ceil_div(a.k, 64) * kTiles[i].stage_cycles + 6000.0 + bm * bn / 8.0;
+        const double t = (double)rounds * t_tile;
         if (t < best * 0.999) {
             best = t;
             pick = kTiles[i];
@@ -122,7 +113,7 @@ std::mutex g_memo_mu;
 std::unordered_map<MemoKey, TileCfg, MemoHash> g_memo;
 
 TileCfg choose(const dg_gemm_args& a, int cus) {
-    if (a.block_m > 0 && a.block_n > 0) return {a.block_m, a.block_n};
+    if (a.block_m > 0 && a.block_n > 0) return {a.block_m, a.block_n, 0, 0, 0, 0};
     MemoKey key;
     memset(&key, 0, sizeof(key));
     key.kind = a.kind; key.type = a.gemm_type; key.m = a.m; key.n = a.n; key.k = a.k;
@@ -191,6 +182,8 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
         return dg_set_error("dg_gemm: leading dimension smaller than the row");
     if ((int64_t)256 * lda_b > 0x7fffffffLL || (int64_t)256 * ldb_b > 0x7fffffffLL)
         return dg_set_error("dg_gemm: row stride too large for 32-bit tile offsets");
+    if (!bf16 && ((a.sfa_ld | a.sfb_ld | a.sfa_batch_stride | a.sfb_batch_stride) & 1))
+        return dg_set_error("dg_gemm: SF leading dimensions and batch strides must be even (int16 elements)");
     if (a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) {
         if (a.alignment < 32 || a.alignment % 32 != 0) return dg_set_error("dg_gemm: alignment must be a multiple of 32");
     }
@@ -232,22 +225,12 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     p.num_n_blocks = ceil_div(a.n, cfg.bn);
     p.kbytes_a = (int)kbytes_a; p.kbytes_b = (int)kbytes_b;
     p.group_m = 4;
-    if (const char* e = getenv("DG_DEBUG_MODE")) p.dbg = atoi(e);
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
     const int64_t grid = (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
     if (grid <= 0) return DG_OK;
     if (grid > 0x7fffffffLL) return dg_set_error("dg_gemm: too many tiles");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const char* ts_path = getenv("DG_DEBUG_TS");
-    if (ts_path) hipMalloc(&p.dbg_ts, (size_t)grid * 8 * sizeof(unsigned long long));
-    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), 0, st, p);
-    if (ts_path) {
-        hipStreamSynchronize(st);
-        std::vector<unsigned long long> h((size_t)grid * 8);
-        hipMemcpy(h.data(), p.dbg_ts, h.size() * 8, hipMemcpyDeviceToHost);
-        if (FILE* f = fopen(ts_path, "wb")) { fwrite(h.data(), 8, h.size(), f); fclose(f); }
-        hipFree(p.dbg_ts);
-    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3((unsigned)tile_threads(cfg.bm, cfg.bn)), 0, st, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         dg_set_error(hipGetErrorString(e));

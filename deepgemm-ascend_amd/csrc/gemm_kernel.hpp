@@ -3,26 +3,28 @@
 // D = alpha * A . B^T (+ bias | + D) for K-major A [M,K] and B [N,K], with one UE8M0 scale
 // per 32 K-elements and per row of each operand (the MX recipe of the reference's
 // fp8_gemm_impl, deep_gemm/include/deep_gemm/fp8_gemm.hpp:36-287), computed on CDNA4
-// v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3 / e2m1 operands) or v_mfma_f32_16x16x32_bf16.
+// v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3 / e2m1 operands) or v_mfma_f32_32x32x16_bf16.
 //
-// Data flow of one 256-thread workgroup (4 waves, 2 x 2 over the BM x BN tile):
-//   HBM/L2 --buffer_load_dwordx4 ... lds--> LDS stage (double buffered, XOR-swizzled
-//   16-byte slots) --ds_read_b128--> VGPR fragments --MFMA--> fp32 accumulators
-//   --epilogue (alpha / bias / accumulate, RNE bf16 cast) in registers--> D.
-// Scales stream beside the data: two packed int16 rows of the required SF layout per
-// 128-K chunk are loaded into VGPRs one chunk ahead, re-laid out in LDS so that each lane
-// fetches the bytes of all its row blocks with one ds_read_b64, and fed to the MFMA as the
-// per-lane scale operand (byte picked with op_sel).
+// One workgroup of NW = 4 or 8 waves (WGM x WGN over the BM x BN tile) walks K in stages of
+// 64 (fp8 / fp4) or 32 (bf16) elements through an NSTAGE-deep ring of LDS stages:
+//   HBM/L2 --buffer_load ... lds (operand rows and the packed-SF rows)--> LDS stage
+//          --ds_read_b128--> VGPR fragments --MFMA--> fp32 accumulators (AGPRs)
+//          --epilogue (alpha / bias / accumulate, RNE bf16) in registers--> D.
+// Loads for stage c + NSTAGE - 1 are issued while stage c computes, so a stage has
+// NSTAGE - 2 stages of compute to arrive.  A-side fragments (and scales) of stage c + 1 are
+// read during stage c into a second register set, so the MFMAs never wait on their LDS
+// reads except at a tile's first stage; B-side fragments stream one block ahead.  There is
+// one workgroup barrier per stage.
 //
-// MFMA register layouts (measured on gfx950):
-//   16x16x128 e4m3 operand, lane l = r + 16 q (r = row, q = lane group):
-//       bytes [0,16) hold K [16q, 16q+16), bytes [16,32) hold K [64+16q, 64+16q+16)
-//   16x16x128 e2m1 operand: 16 bytes hold K [32q, 32q+32) (low nibble = even k)
+// MFMA register layouts (measured on gfx950), lane l = r + 32 q (r = row 0..31, q = 0..1):
+//   32x32x64 e4m3 operand: bytes [0,16) hold K [16q, 16q+16), bytes [16,32) hold K [32+16q, +16)
+//   32x32x64 e2m1 operand: 16 bytes hold K [32q, 32q+32) (low nibble = even k)
 //   scale operand of lane (r, q): UE8M0 exponent of K-block q (K [32q, 32q+32)) of row r
-//   16x16x32 bf16 operand: 8 values hold K [8q, 8q+8)
-//   accumulator: lane l, element i -> (row 4*(l/16) + i of the MFMA "A" side, column l%16)
+//   32x32x16 bf16 operand: 8 values hold K [8q, 8q+8)
+//   accumulator: lane l, element i -> (row 4 (l/32) + (i%4) + 8 (i/4) of the MFMA "A" side,
+//                column l%32)
 // The kernel feeds B (n) as the MFMA "A" operand and A (m) as the "B" operand, so each lane
-// ends with four consecutive n of one output row m: 8-byte (bf16) / 16-byte (fp32) stores.
+// ends with groups of four consecutive n of one output row m.
 #pragma once
 
 #include <type_traits>
@@ -44,21 +46,17 @@ struct KParams {
     int64_t ldd;               // elements of D
     int64_t bsa, bsb;          // bytes
     int64_t bsd;               // elements of D
-    int64_t sfa_ld, sfb_ld, sfa_bs, sfb_bs;   // int16 elements
+    int64_t sfa_ld, sfb_ld, sfa_bs, sfb_bs;   // int16 elements (ld even)
     int gemm_type, out_f32, accumulate, has_bias, alignment, vec_store;
     float alpha;
     int num_m_blocks, num_n_blocks;
     int kbytes_a, kbytes_b;    // bytes of one K row (multiple of 16)
     int group_m;               // tile-order swizzle width along M
-    unsigned long long* dbg_ts;  // profiling: per-workgroup timestamps (null = off)
-    int dbg;                   // profiling switch: 1 = skip operand loads, 2 = skip MFMA,
-                               // 3 = skip scale loads, 4 = skip all loads, 5 = epilogue only
 };
 
 // Epilogue variants.
-constexpr int kEpiLdsBf16 = 0;   // bf16 D, no accumulation, 16-byte aligned rows
 constexpr int kEpiF32 = 1;       // fp32 D (bias / accumulate allowed)
-constexpr int kEpiBf16 = 2;      // bf16 D with accumulation or unaligned rows
+constexpr int kEpiBf16 = 2;      // bf16 D
 
 template <int N>
 struct Int { static constexpr int value = N; };
@@ -72,14 +70,22 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// Slot swizzle inside one LDS row: 8 slots (128-byte rows) or 4 slots (64-byte rows).
-// Chosen so that the 16 rows one ds_read_b128 phase touches (lanes r = 0..15 at a fixed lane
-// group) land on distinct 16-byte bank groups both for a 64 x 4-byte and a 32 x 4-byte bank
-// organisation.
+// s_waitcnt that bounds only the vector-memory counter.
+template <int VM>
+__device__ __forceinline__ void wait_vmcnt() {
+    constexpr int v = VM > 63 ? 63 : (VM < 0 ? 0 : VM);
+    __builtin_amdgcn_s_waitcnt((v & 0xf) | ((v >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Slot swizzle inside one LDS row of SPR 16-byte slots (64-byte rows: 4 slots, 32-byte rows:
+// 2 slots).  Chosen so the 16 rows one ds_read_b128 phase touches (lanes r = 0..15 at a
+// fixed lane group) land on distinct 16-byte bank groups both for a 64 x 4-byte and a
+// 32 x 4-byte bank organisation.  Only row bits >= 1 are read, and a 4 KB block of slots
+// shifts rows by a multiple of 64, so a lane's swizzled slot is the same in every block.
 template <int SPR>
 __device__ __forceinline__ int slot_swizzle(int row) {
-    if constexpr (SPR == 8) return ((row >> 1) ^ (row << 2)) & 7;
-    else return ((row >> 1) ^ (row >> 3)) & 3;
+    if constexpr (SPR == 4) return ((row >> 1) ^ (row >> 3)) & 3;
+    else return ((row >> 2) ^ (row >> 3)) & 1;
 }
 
 // Buffer resource over [base, base + bytes); every field is forced wave-uniform (SGPRs) so no
@@ -104,6 +110,12 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
     return (bid % kXCD) * per + bid / kXCD;
 }
 
+// Workgroup barrier for the stage ring.  Unlike __syncthreads() it carries no memory fence,
+// so the LDS-DMA loads of later stages stay in flight across it; the stage it publishes was
+// already waited for with an explicit vmcnt.  The "memory" clobber keeps the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 // GROUP_M tile order: walk n inside bands of `gm` m-blocks (L2 reuse of A and B tiles).
 __device__ __forceinline__ void swizzle_tile(int t, int nm, int nn, int gm, int& mb, int& nb) {
     const int band = gm * nn;
@@ -114,44 +126,39 @@ __device__ __forceinline__ void swizzle_tile(int t, int nm, int nn, int gm, int&
     nb = in_band / size;
 }
 
-template <int FMT_A, int FMT_B, int OPSEL_A, int OPSEL_B>
-__device__ __forceinline__ f32x4 mfma_scaled(const i32x8& a, const i32x8& b, const f32x4& c,
-                                             int sa, int sb) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, OPSEL_A, sa,
-                                                            OPSEL_B, sb);
-}
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int BM, int BN, int KIND, int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_kernel(const KParams p) {
+template <int BM, int BN, int WGM, int NW, int NSTAGE, int KIND, int EPI>
+__global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
     constexpr bool kBf16 = KIND == kBF16;
     constexpr int kFmtA = kAFp4 ? kFmtE2M1 : kFmtE4M3;
     constexpr int kFmtB = kBFp4 ? kFmtE2M1 : kFmtE4M3;
-    constexpr int RBA = kAFp4 ? 64 : 128;       // bytes of one row per K chunk
-    constexpr int RBB = kBFp4 ? 64 : 128;
+    constexpr int KS = kBf16 ? 32 : 64;                  // K elements per stage
+    constexpr int RBA = kAFp4 ? 32 : 64;                 // bytes of one row per stage
+    constexpr int RBB = kBFp4 ? 32 : 64;
     constexpr int SPRA = RBA / 16, SPRB = RBB / 16;
-    constexpr int WM = BM / 2, WN = BN / 2;      // wave tile
-    constexpr int TM = WM / 16, TN = WN / 16;    // MFMA blocks per wave
-    static_assert(TM >= 1 && TM <= 8 && TN >= 1 && TN <= 8, "wave tile must be 16..128");
+    constexpr int NT = NW * 64;                          // threads per workgroup
+    constexpr int WGN = NW / WGM;
+    constexpr int WM = BM / WGM, WN = BN / WGN;          // wave tile
+    constexpr int TM = WM / 32, TN = WN / 32;            // 32x32 MFMA blocks per wave
+    static_assert((NW == 4 || NW == 8) && WGM * WGN == NW && TM >= 1 && TN >= 1 && TM * 32 == WM && TN * 32 == WN, "wave tiling");
     constexpr int A_BYTES = BM * RBA, B_BYTES = BN * RBB;
-    static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "tile rows must fill waves");
-    constexpr int SC_BYTES = kBf16 ? 0 : 1024;
-    constexpr int STAGE = A_BYTES + B_BYTES + 2 * SC_BYTES;
-    constexpr int CROW = BN * 2 + 32;                       // LDS row pitch of the bf16 epilogue tile
-    constexpr int EPI_BYTES = EPI == kEpiLdsBf16 ? BM * CROW : 0;
-    constexpr int SMEM = 2 * STAGE > EPI_BYTES ? 2 * STAGE : EPI_BYTES;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+    constexpr int SCA = kBf16 ? 0 : (BM * 2 + 255) / 256 * 256;   // one packed int16 per row
+    constexpr int SCB = kBf16 ? 0 : (BN * 2 + 255) / 256 * 256;
+    constexpr int NSCA = kBf16 ? 0 : (BM + 127) / 128, NSCB = kBf16 ? 0 : (BN + 127) / 128;
+    // 256 idle bytes per stage that take the dead SF loads of waves without an SF row to fetch
+    constexpr int SPARE = (!kBf16 && NSCA + NSCB < NW) ? 256 : 0;
+    constexpr int STAGE = A_BYTES + B_BYTES + SCA + SCB + SPARE;
+    static_assert(NSTAGE >= 3 && NSTAGE * STAGE <= 160 * 1024, "LDS budget");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * STAGE];
 
     const int tid = threadIdx.x;
-    unsigned long long* ts = p.dbg_ts ? p.dbg_ts + (size_t)blockIdx.x * 8 : nullptr;
-    auto stamp = [&](int i) { if (ts && tid == 0) ts[i] = __builtin_amdgcn_s_memrealtime(); };
-    stamp(0);
-    if (ts && tid == 0) ts[2] = __builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11));  // HW_ID
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 1, wn = wave >> 1;
-    const int r = lane & 15, q = lane >> 4;
+    const int wm = wave % WGM, wn = wave / WGM;
+    const int r = lane & 31, q = lane >> 5;
 
     // ------------------------------------------------------------------ tile selection
     const int nm = p.num_m_blocks, nn = p.num_n_blocks;
@@ -205,13 +212,13 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const KParams p) {
         group = __builtin_amdgcn_readfirstlane(p.layout[m0]);
         if (group < 0) zero_tile = true;
     }
-
     group = __builtin_amdgcn_readfirstlane(group);
     valid_end = __builtin_amdgcn_readfirstlane(valid_end);
+
     if (zero_tile) {
         // Padding-only tile of an M-grouped layout: its D rows are exact zeros.
         const int rows = min(BM, M - m0), cols = min(BN, N - n0);
-        for (int e = tid; e < rows * cols; e += 256) {
+        for (int e = tid; e < rows * cols; e += NT) {
             const int rr = e / cols, cc = e % cols;
             const int64_t off = (int64_t)(m0 + rr) * p.ldd + n0 + cc;
             if (p.out_f32) reinterpret_cast<float*>(d_base)[off] = 0.f;
@@ -219,8 +226,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const KParams p) {
         }
         return;
     }
-    if (p.gemm_type == kMGroupedPsum || p.gemm_type == kMGroupedIdx || p.gemm_type == kBatched ||
-        p.gemm_type == kMasked) {
+    if (p.gemm_type != kNormal) {
         b_base += (int64_t)group * p.bsb;
         if (!kBf16) sfb += (int64_t)group * p.sfb_bs;
     }
@@ -231,388 +237,321 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const KParams p) {
     const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(a_base + (int64_t)m0 * lda, (int64_t)rows_a * lda);
     const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(b_base + (int64_t)n0 * ldb, (int64_t)rows_b * ldb);
     const int kbytes_a = p.kbytes_a, kbytes_b = p.kbytes_b;
-    const int KC = kBf16 ? 64 : 128;
-    const int num_chunks = p.dbg == 11 ? 0 : ceil_div(p.k, KC);
+    // The ring walks an even number of virtual stages so the main loop is a pair of iterations
+    // with static register sets; an odd stage count gets one leading dead stage (all-zero
+    // operands and scales, so it adds nothing to the accumulators).
+    const int num_stages = ceil_div(p.k, KS);
+    const int shift = num_stages & 1;
+    const int num_virtual = num_stages + shift;
     const int nk64 = ceil_div(p.k, 64);
 
-    // ------------------------------------------------------------------ loaders
-    // Operand tiles: each wave-level buffer_load_dwordx4 ... lds fills 1 KB (64 lanes x 16 B)
-    // of an LDS stage; lane slots map to XOR-swizzled (row, 16-byte K piece) positions.  The
-    // chunk's K offset rides in the scalar soffset so the per-lane voffset is chunk-invariant,
-    // and the lane index is made opaque to the optimiser so that voffset is recomputed (a few
-    // VALU ops) instead of being hoisted into long-lived VGPRs.
-    constexpr int NLA = A_BYTES / 4096 + (A_BYTES % 4096 ? 1 : 0);   // loads per wave, A tile
-    constexpr int NLB = B_BYTES / 4096 + (B_BYTES % 4096 ? 1 : 0);   // loads per wave, B tile
-    constexpr int NL = NLA + NLB;
-    // Per-load chunk-invariant voffsets (row * ld + swizzled K piece, or out of range).
-    auto load_geom = [&](auto idx_tag, int t, int& row, int& lk) {
-        constexpr int IDX = decltype(idx_tag)::value;
+    // ------------------------------------------------------------------ loads
+    // Operand rows: each wave-level buffer_load_dwordx4 ... lds fills 1 KB (64 lanes x 16 B)
+    // of a stage; lane slots map to swizzled (row, 16-byte K piece) positions.  The stage's K
+    // offset rides in the scalar soffset, so the per-lane voffset is stage-invariant.
+    constexpr int SLA = BM * SPRA, SLB = BN * SPRB;                    // 16-byte slots per stage
+    constexpr int NLA = (SLA + NT - 1) / NT, NLB = (SLB + NT - 1) / NT;  // per-thread loads
+    // Packed SF rows: one buffer_load_dword ... lds per 128 rows of the tile, issued by waves
+    // 0 .. NSCA-1 (A) and NSCA .. NSCA+NSCB-1 (B).
+    static_assert(NSCA + NSCB <= NW, "scale loads per stage");
+    constexpr int NL = NLA + NLB + (kBf16 ? 0 : 1);
+    // Loads that every wave issues per stage (the waits below count the smallest number).
+    constexpr int kMinLoadsPerStage = (SLA / NT) + (SLB / NT) + (kBf16 ? 0 : 1);
+
+    int lk_a, lk_b;
+    {
+        const int row_a = tid / SPRA, row_b = tid / SPRB;
+        lk_a = ((tid % SPRA) ^ slot_swizzle<SPRA>(row_a)) * 16;
+        lk_b = ((tid % SPRB) ^ slot_swizzle<SPRB>(row_b)) * 16;
+    }
+    uint32_t voff_pre[NLA + NLB];
+    static_for<NLA + NLB>([&](auto i) {
+        constexpr int IDX = decltype(i)::value;
         constexpr bool kIsA = IDX < NLA;
         constexpr int it = kIsA ? IDX : IDX - NLA;
         constexpr int SPR = kIsA ? SPRA : SPRB;
-        const int slot = it * 256 + t;
-        row = slot / SPR;
-        lk = ((slot % SPR) ^ slot_swizzle<SPR>(row)) * 16;
-    };
-    uint32_t voff_pre[NL];
-    static_for<NL>([&](auto i) {
-        constexpr int IDX = decltype(i)::value;
-        constexpr bool kIsA = IDX < NLA;
-        int row, lk;
-        load_geom(i, tid, row, lk);
-        voff_pre[IDX] = row < (kIsA ? rows_a : rows_b) ? (uint32_t)(row * (kIsA ? lda : ldb) + lk) : kOOBOffset;
+        const int row = (it * NT + tid) / SPR;
+        voff_pre[IDX] = row < (kIsA ? rows_a : rows_b)
+                            ? (uint32_t)(row * (kIsA ? lda : ldb) + (kIsA ? lk_a : lk_b)) : kOOBOffset;
     });
-    // The swizzled K piece of a lane's slot is the same for every load of one operand (the
-    // swizzle only reads row bits that a whole 4 KB load block leaves unchanged).
-    int lk_a, lk_b, row_unused;
-    load_geom(Int<0>{}, tid, row_unused, lk_a);
-    load_geom(Int<NLA>{}, tid, row_unused, lk_b);
-    // Loads of chunk c into stage s.  Branch-free so the scheduler can interleave them with
-    // MFMAs: `live == false` moves every lane out of range through the scalar offset (no
-    // memory traffic, zeros into an idle stage); K-tail pieces go out of range per lane.
-    constexpr int kDeadOffset = 0x40000000;
-    auto issue_one = [&](auto idx_tag, int c, int s, bool live) {
-        constexpr int IDX = decltype(idx_tag)::value;
-        constexpr bool kIsA = IDX < NLA;
-        constexpr int it = kIsA ? IDX : IDX - NLA;
-        constexpr int BYTES = kIsA ? A_BYTES : B_BYTES;
-        constexpr int RB = kIsA ? RBA : RBB;
-        if (BYTES % 4096 != 0 && (it * 256 + wave * 64) * 16 >= BYTES) return;
-        const int kb = (p.dbg == 9 ? 0 : c) * RB;
-        const int krem = (kIsA ? kbytes_a : kbytes_b) - kb;
-        const uint32_t voff = (kIsA ? lk_a : lk_b) < krem ? voff_pre[IDX] : kOOBOffset;
-        uint8_t* sdst = smem + s * STAGE + (kIsA ? 0 : A_BYTES);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(kIsA ? rs_a : rs_b,
-                                                 (lds_void*)(sdst + (it * 256 + wave * 64) * 16), 16, voff,
-                                                 live ? kb : kDeadOffset, 0, 0);
-    };
-    auto issue_data = [&](int c, int s) {
-        static_for<NL>([&](auto i) { issue_one(i, c, s, true); });
-    };
-
-    // Scales: the two packed int16 rows (k64 = 2c, 2c+1) of this chunk for the tile's rows,
-    // through buffer loads (out-of-range rows / K blocks read 0: their operand data is 0 too).
-    constexpr int NSA = (2 * BM + 255) / 256, NSB = (2 * BN + 255) / 256;
-    uint32_t sa_reg[NSA], sb_reg[NSB];
-    __amdgpu_buffer_rsrc_t rs_sa, rs_sb;
+    // Per-wave packed-SF load of a stage: wave w < NSCA fetches A rows [128 w, 128 w + 128),
+    // waves NSCA .. NSCA+NSCB-1 the B rows; the other waves issue a dead (out-of-range) load
+    // into an idle word so that every wave runs the same branch-free instruction stream.
+    __amdgpu_buffer_rsrc_t rs_sc;
+    uint32_t sc_voff = kOOBOffset;
+    int sc_step = 0, sc_lds = 0;
+    bool sc_live = false;
     if constexpr (!kBf16) {
-        rs_sa = make_rsrc(sfa + m0, ((int64_t)nk64 * p.sfa_ld - m0) * 2);
-        rs_sb = make_rsrc(sfb + n0, ((int64_t)nk64 * p.sfb_ld - n0) * 2);
+        const bool is_a = wave < NSCA;
+        const int w = is_a ? wave : wave - NSCA;
+        sc_live = wave < NSCA + NSCB;
+        rs_sc = is_a ? make_rsrc(sfa + m0, ((int64_t)nk64 * p.sfa_ld - m0) * 2)
+                     : make_rsrc(sfb + n0, ((int64_t)nk64 * p.sfb_ld - n0) * 2);
+        const int row = w * 128 + 2 * lane;
+        sc_voff = (sc_live && row < (is_a ? rows_a : rows_b)) ? (uint32_t)(row * 2) : kOOBOffset;
+        sc_step = __builtin_amdgcn_readfirstlane((int)((is_a ? p.sfa_ld : p.sfb_ld) * 2));
+        sc_lds = __builtin_amdgcn_readfirstlane(sc_live ? A_BYTES + B_BYTES + (is_a ? 0 : SCA) + w * 256
+                                                        : A_BYTES + B_BYTES + SCA + SCB);
     }
-    // byte distance between the packed-SF rows of consecutive chunks (two int16 rows)
-    const int sfa_step = __builtin_amdgcn_readfirstlane((int)(p.sfa_ld * 4));
-    const int sfb_step = __builtin_amdgcn_readfirstlane((int)(p.sfb_ld * 4));
-    auto issue_scales = [&](int c, bool live) {
-        if constexpr (!kBf16) {
-#pragma unroll
-            for (int i = 0; i < NSA; ++i) {
-                const int idx = i * 256 + tid;
-                const int h = idx / BM, row = idx % BM;
-                const uint32_t voff = idx < 2 * BM ? (uint32_t)((h * p.sfa_ld + row) * 2) : kOOBOffset;
-                sa_reg[i] = __builtin_amdgcn_raw_buffer_load_b16(rs_sa, voff, live ? c * sfa_step : kDeadOffset, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < NSB; ++i) {
-                const int idx = i * 256 + tid;
-                const int h = idx / BN, row = idx % BN;
-                const uint32_t voff = idx < 2 * BN ? (uint32_t)((h * p.sfb_ld + row) * 2) : kOOBOffset;
-                sb_reg[i] = __builtin_amdgcn_raw_buffer_load_b16(rs_sb, voff, live ? c * sfb_step : kDeadOffset, 0);
-            }
+    constexpr int kDeadOffset = 0x40000000;   // scalar offset that moves every lane out of range
+
+    // Load item IDX of stage c into ring slot s.  `live == false` turns it into an
+    // out-of-range load (zeros into an idle slot, no memory traffic) so that every wave keeps
+    // the same instruction stream and the code stays branch-free for the scheduler.
+    auto issue_item = [&](auto idx_tag, int c, int s, bool live) {
+        constexpr int IDX = decltype(idx_tag)::value;
+        uint8_t* sbase = smem + s * STAGE;
+        if constexpr (IDX < NLA + NLB) {
+            constexpr bool kIsA = IDX < NLA;
+            constexpr int it = kIsA ? IDX : IDX - NLA;
+            constexpr int SL = kIsA ? SLA : SLB;
+            constexpr int RB = kIsA ? RBA : RBB;
+            if (SL % NT != 0 && it * NT + wave * 64 >= SL) return;
+            const int kb = c * RB;
+            const int krem = (kIsA ? kbytes_a : kbytes_b) - kb;
+            const uint32_t voff = (kIsA ? lk_a : lk_b) < krem ? voff_pre[IDX] : kOOBOffset;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                kIsA ? rs_a : rs_b, (lds_void*)(sbase + (kIsA ? 0 : A_BYTES) + (it * NT + wave * 64) * 16), 16,
+                voff, __builtin_amdgcn_readfirstlane(live ? kb : kDeadOffset), 0, 0);
+        } else if constexpr (!kBf16) {
+            // packed-SF row of stage c (its k64 index is c)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_sc, (lds_void*)(sbase + sc_lds), 4, sc_voff,
+                                                     __builtin_amdgcn_readfirstlane((live & sc_live) ? c * sc_step : kDeadOffset),
+                                                     0, 0);
         }
     };
-    // LDS scale layout per operand: byte (q*16 + r)*16 + w*8 + jj holds the exponent of K-block
-    // q of tile row (w*T + jj)*16 + r, T = row blocks per wave; lane (r, q) of wave w reads its
-    // T bytes with one 8-byte load.
-    auto write_scales = [&](int s) {
-        if constexpr (!kBf16) {
-            uint8_t* sSA = smem + s * STAGE + A_BYTES + B_BYTES;
-            uint8_t* sSB = sSA + SC_BYTES;
-#pragma unroll
-            for (int i = 0; i < NSA; ++i) {
-                const int idx = i * 256 + tid;
-                if (idx < 2 * BM) {
-                    const int h = idx / BM, row = idx % BM;
-                    const int j = row >> 4, rr = row & 15;
-                    const int pos = ((2 * h) * 16 + rr) * 16 + (j / TM) * 8 + (j % TM);
-                    sSA[pos] = (uint8_t)(sa_reg[i] & 0xff);
-                    sSA[pos + 256] = (uint8_t)(sa_reg[i] >> 8);
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < NSB; ++i) {
-                const int idx = i * 256 + tid;
-                if (idx < 2 * BN) {
-                    const int h = idx / BN, row = idx % BN;
-                    const int j = row >> 4, rr = row & 15;
-                    const int pos = ((2 * h) * 16 + rr) * 16 + (j / TN) * 8 + (j % TN);
-                    sSB[pos] = (uint8_t)(sb_reg[i] & 0xff);
-                    sSB[pos + 256] = (uint8_t)(sb_reg[i] >> 8);
-                }
-            }
-        }
+    auto issue_stage = [&](int c, int s, bool live) {
+        static_for<NL>([&](auto i) { issue_item(i, c, s, live); });
     };
 
-    f32x4 acc[TN][TM];
+    // ------------------------------------------------------------------ fragments
+    auto frag_addr = [&](int R, int slot, auto spr_tag) -> int {
+        constexpr int SPR = decltype(spr_tag)::value;
+        return R * (SPR * 16) + ((slot ^ slot_swizzle<SPR>(R)) << 4);
+    };
+    // 32 bytes (fp8: K [16q,+16) and [32+16q,+16); bf16: k-steps 0 and 1) or 16 bytes (fp4).
+    auto load_frag = [&](const uint8_t* base, int R, auto spr_tag) -> i32x8 {
+        constexpr int SPR = decltype(spr_tag)::value;
+        const i32x4 lo = *reinterpret_cast<const i32x4*>(base + frag_addr(R, q, spr_tag));
+        if constexpr (SPR == 4) {
+            const i32x4 hi = *reinterpret_cast<const i32x4*>(base + frag_addr(R, 2 + q, spr_tag));
+            return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        } else {
+            return i32x8{lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
+        }
+    };
+    // UE8M0 byte of K-block q of row R (one packed int16 per row in the stage's scale area).
+    auto load_scale = [&](const uint8_t* sc, int R) -> int {
+        const uint32_t v = *reinterpret_cast<const uint16_t*>(sc + R * 2);
+        return (int)((v >> (8 * q)) & 0xffu);
+    };
+
+    f32x16 acc[TN][TM];
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
 
-    auto load_frag = [&](const uint8_t* base, int R, auto spr_tag) -> i32x8 {
-        constexpr int SPR = decltype(spr_tag)::value;
-        i32x8 f;
-        if constexpr (SPR == 8) {
-            const int sw = slot_swizzle<8>(R);
-            const i32x4 lo = *reinterpret_cast<const i32x4*>(base + R * 128 + ((q ^ sw) << 4));
-            const i32x4 hi = *reinterpret_cast<const i32x4*>(base + R * 128 + (((q + 4) ^ sw) << 4));
-            f = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    // Register sets `buf` = 0 / 1 alternate between stages: A-side fragments and scales of the
+    // whole wave tile plus the first B-side block, all read one stage ahead.
+    i32x8 fa[2][TM];
+    int sa[2][TM];
+    i32x8 fb0[2];
+    int sb0[2];
+    auto load_ahead = [&](int s, auto part_tag) {
+        constexpr int part = decltype(part_tag)::value;   // TM: the B block, else A block `part`
+        const uint8_t* st = smem + s * STAGE;
+        if constexpr (part < TM) {
+            const int R = wm * WM + part * 32 + r;
+            return std::pair<i32x8, int>(load_frag(st, R, Int<SPRA>{}),
+                                         kBf16 ? 0 : load_scale(st + A_BYTES + B_BYTES, R));
         } else {
-            const int sw = slot_swizzle<4>(R);
-            const i32x4 lo = *reinterpret_cast<const i32x4*>(base + R * 64 + ((q ^ sw) << 4));
-            f = i32x8{lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
+            const int R = wn * WN + r;
+            return std::pair<i32x8, int>(load_frag(st + A_BYTES, R, Int<SPRB>{}),
+                                         kBf16 ? 0 : load_scale(st + A_BYTES + B_BYTES + SCA, R));
         }
-        return f;
+    };
+    auto prefetch = [&](int s, auto buf_tag, auto part_tag) {
+        constexpr int buf = decltype(buf_tag)::value;
+        constexpr int part = decltype(part_tag)::value;
+        const auto v = load_ahead(s, part_tag);
+        if constexpr (part < TM) { fa[buf][part] = v.first; sa[buf][part] = v.second; }
+        else { fb0[buf] = v.first; sb0[buf] = v.second; }
     };
 
-    // One K chunk of MFMAs from LDS stage s.  When `next` is set, the loads of chunk c + 1
-    // (into stage s ^ 1) are interleaved with the MFMA groups: a buffer_load ... lds blocks
-    // issue while the texture path drains, so issuing them in one burst would stall the MFMA
-    // pipe.  They go out over the first groups to leave latency slack before the next wait.
-    constexpr int kLoadGroups = TN > 2 ? (TN * 2 + 2) / 3 : TN;
-    constexpr int kLPG = (NL + kLoadGroups - 1) / kLoadGroups;    // loads per MFMA group
-    auto compute = [&](int s, int cn, bool next) {
-        const uint8_t* sA = smem + s * STAGE;
-        const uint8_t* sB = sA + A_BYTES;
-        i32x8 fa[TM];
-#pragma unroll
-        for (int jm = 0; jm < TM; ++jm) fa[jm] = load_frag(sA, wm * WM + jm * 16 + r, Int<SPRA>{});
-        i32x2 sa2 = {0, 0}, sb2 = {0, 0};
-        if constexpr (!kBf16) {
-            const uint8_t* sSA = sA + A_BYTES + B_BYTES;
-            const uint8_t* sSB = sSA + SC_BYTES;
-            sa2 = *reinterpret_cast<const i32x2*>(sSA + (q * 16 + r) * 16 + wm * 8);
-            sb2 = *reinterpret_cast<const i32x2*>(sSB + (q * 16 + r) * 16 + wn * 8);
-        }
-        i32x8 fb_cur = load_frag(sB, wn * WN + r, Int<SPRB>{});
+    // One stage of MFMAs from ring slot s with the registers of set `buf`; reads the ahead
+    // registers of the next stage (slot sn) into the other set and issues the loads of stage cl
+    // into slot sl, all interleaved with the MFMA groups (one group = the TM blocks of one jn).
+    constexpr int kLPG = (NL + TN - 1) / TN;
+    auto compute = [&](int s, auto buf_tag, int sn, int cl, int sl, bool load_live) {
+        constexpr int buf = decltype(buf_tag)::value;
+        const uint8_t* sB = smem + s * STAGE + A_BYTES;
+        const uint8_t* sSB = smem + s * STAGE + A_BYTES + B_BYTES + SCA;
+        i32x8 fb_cur = fb0[buf];
+        int sb_cur = sb0[buf];
         static_for<TN>([&](auto jn_c) {
             constexpr int jn = decltype(jn_c)::value;
             i32x8 fb_next = fb_cur;
-            if constexpr (jn + 1 < TN) fb_next = load_frag(sB, wn * WN + (jn + 1) * 16 + r, Int<SPRB>{});
+            int sb_next = sb_cur;
+            if constexpr (jn + 1 < TN) {
+                fb_next = load_frag(sB, wn * WN + (jn + 1) * 32 + r, Int<SPRB>{});
+                if constexpr (!kBf16) sb_next = load_scale(sSB, wn * WN + (jn + 1) * 32 + r);
+            }
             static_for<TM>([&](auto jm_c) {
                 constexpr int jm = decltype(jm_c)::value;
                 if constexpr (kBf16) {
-                    const i32x4 blo = {fb_cur[0], fb_cur[1], fb_cur[2], fb_cur[3]};
-                    const i32x4 bhi = {fb_cur[4], fb_cur[5], fb_cur[6], fb_cur[7]};
-                    const i32x4 alo = {fa[jm][0], fa[jm][1], fa[jm][2], fa[jm][3]};
-                    const i32x4 ahi = {fa[jm][4], fa[jm][5], fa[jm][6], fa[jm][7]};
-                    acc[jn][jm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        __builtin_bit_cast(bf16x8, blo), __builtin_bit_cast(bf16x8, alo), acc[jn][jm], 0, 0, 0);
-                    acc[jn][jm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        __builtin_bit_cast(bf16x8, bhi), __builtin_bit_cast(bf16x8, ahi), acc[jn][jm], 0, 0, 0);
+                    const i32x4 b0 = {fb_cur[0], fb_cur[1], fb_cur[2], fb_cur[3]};
+                    const i32x4 b1 = {fb_cur[4], fb_cur[5], fb_cur[6], fb_cur[7]};
+                    const i32x4 a0 = {fa[buf][jm][0], fa[buf][jm][1], fa[buf][jm][2], fa[buf][jm][3]};
+                    const i32x4 a1 = {fa[buf][jm][4], fa[buf][jm][5], fa[buf][jm][6], fa[buf][jm][7]};
+                    acc[jn][jm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(bf16x8, b0), __builtin_bit_cast(bf16x8, a0), acc[jn][jm], 0, 0, 0);
+                    acc[jn][jm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(bf16x8, b1), __builtin_bit_cast(bf16x8, a1), acc[jn][jm], 0, 0, 0);
                 } else {
-                    acc[jn][jm] = mfma_scaled<kFmtB, kFmtA, jn % 4, jm % 4>(
-                        fb_cur, fa[jm], acc[jn][jm], sb2[jn / 4], sa2[jm / 4]);
+                    acc[jn][jm] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        fb_cur, fa[buf][jm], acc[jn][jm], kFmtB, kFmtA, 0, sb_cur, 0, sa[buf][jm]);
                 }
             });
-            constexpr int kScaleLoads = (!kBf16 && jn == 0) ? NSA + NSB : 0;
-            constexpr int kVmem = (jn * kLPG >= NL ? 0 : (NL - jn * kLPG < kLPG ? NL - jn * kLPG : kLPG)) + kScaleLoads;
-            constexpr int kDs = jn + 1 < TN ? 2 : 0;
-            if constexpr (jn == 0) issue_scales(cn, next);
+            // ahead registers of the next stage: A block jm goes with group jm * TN / TM, the
+            // first B block with the last group (slot sn is always readable; a stage past the
+            // end reads stale bytes that are never used)
+            static_for<TM + 1>([&](auto part_c) {
+                constexpr int part = decltype(part_c)::value;
+                constexpr int grp = part < TM ? part * TN / TM : TN - 1;
+                if constexpr (grp == jn) prefetch(sn, Int<buf ^ 1>{}, Int<part>{});
+            });
             static_for<kLPG>([&](auto li) {
                 constexpr int idx = jn * kLPG + decltype(li)::value;
-                if constexpr (idx < NL) issue_one(Int<idx>{}, cn, s ^ 1, next);
-            });
-            // interleave: each MFMA is followed by at most one LDS read and one buffer load
-            static_for<TM>([&](auto i_c) {
-                constexpr int i = decltype(i_c)::value;
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if constexpr (i < kDs) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                if constexpr (i < kVmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                if constexpr (idx < NL) issue_item(Int<idx>{}, cl, sl, load_live);
             });
             __builtin_amdgcn_sched_barrier(0);
             fb_cur = fb_next;
+            sb_cur = sb_next;
         });
     };
 
     // ------------------------------------------------------------------ main loop
-    if (num_chunks > 0) {
-        issue_data(0, 0);
-        issue_scales(0, true);
+    // Prologue: stages 0 .. NSTAGE-2 in flight, stage 0 visible, its ahead registers loaded.
+    static_for<NSTAGE - 1>([&](auto i) {
+        constexpr int st = decltype(i)::value;
+        issue_stage(st - shift, st, st >= shift && st < num_virtual);
+    });
+    wait_vmcnt<(NSTAGE - 2) * kMinLoadsPerStage>();
+    stage_barrier();
+    static_for<TM + 1>([&](auto part_c) { prefetch(0, Int<0>{}, part_c); });
+
+    // Stage c + 1 must have landed before the barrier of iteration c (its ahead registers are
+    // read during stage c); the loads of stages c + 2 .. c + NSTAGE - 2 may stay in flight.
+    // The barrier also certifies that every wave finished reading stage c - 1 (its B side in
+    // iteration c - 1, its ahead registers in iteration c - 2), so its slot can take stage
+    // c + NSTAGE - 1.
+    auto iteration = [&](int c, auto buf_tag) {
+        wait_vmcnt<(NSTAGE - 3) * kMinLoadsPerStage>();
+        stage_barrier();
+        const int cl = c + NSTAGE - 1;
+        compute(c % NSTAGE, buf_tag, (c + 1) % NSTAGE, cl - shift, cl % NSTAGE, cl < num_virtual);
+    };
+    for (int c = 0; c < num_virtual; c += 2) {
+        iteration(c, Int<0>{});
+        iteration(c + 1, Int<1>{});
     }
-    for (int c = 0; c < num_chunks; ++c) {
-        const int s = c & 1;
-        __builtin_amdgcn_s_waitcnt(0);   // chunk c data (LDS) and scales (VGPR) have landed
-        write_scales(s);
-        __syncthreads();
-        compute(s, c + 1, c + 1 < num_chunks && p.dbg != 10);
-    }
+    __builtin_amdgcn_s_waitcnt(0);
+
     // ------------------------------------------------------------------ epilogue
-    // All accumulator indexing below is in compile-time-unrolled loops (static_for): a
-    // runtime index would demote the accumulator array to scratch memory.
+    // All accumulator indexing is in compile-time-unrolled loops (static_for): a runtime
+    // index would demote the accumulator array to scratch memory.
     const float alpha = p.alpha;
-    if constexpr (EPI == kEpiLdsBf16) {
-        // bf16 D without accumulation: alpha / bias / padding-row zeroing in registers, the
-        // tile staged through LDS as bf16, then written with 16-byte row-contiguous stores.
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();                                     // all waves are done with the operands
-        const bool bias = p.has_bias;
-        const uint16_t* bp = reinterpret_cast<const uint16_t*>(p.bias);
-        static_for<TM>([&](auto jm_c) {
-            constexpr int jm = decltype(jm_c)::value;
-            const int ml = wm * WM + jm * 16 + r;
-            const int m = m0 + ml;
-            bool zero = false;
-            if (p.gemm_type == kMGroupedPsum) zero = m >= valid_end;
-            else if (p.gemm_type == kMGroupedIdx) zero = m < M && p.layout[m] != group;
-            static_for<TN>([&](auto jn_c) {
-                constexpr int jn = decltype(jn_c)::value;
-                const int nl = wn * WN + jn * 16 + 4 * q;
-                float v0 = acc[jn][jm][0] * alpha, v1 = acc[jn][jm][1] * alpha;
-                float v2 = acc[jn][jm][2] * alpha, v3 = acc[jn][jm][3] * alpha;
+    constexpr bool kF32 = EPI == kEpiF32;
+    using OutT = std::conditional_t<kF32, float, uint16_t>;
+    OutT* dbase = reinterpret_cast<OutT*>(d_base);
+    const OutT* bp = reinterpret_cast<const OutT*>(p.bias);
+    const bool acc_old = p.accumulate, bias = p.has_bias, vec = p.vec_store;
+    auto to_f = [](OutT x) -> float {
+        if constexpr (kF32) return x; else return bf16_to_f32(x);
+    };
+    static_for<TM>([&](auto jm_c) {
+        constexpr int jm = decltype(jm_c)::value;
+        const int m = m0 + wm * WM + jm * 32 + r;
+        const bool row_ok = m < M && !(p.gemm_type == kMasked && m >= valid_end);
+        bool pad_row = false;
+        if (p.gemm_type == kMGroupedPsum) pad_row = m >= valid_end;
+        else if (p.gemm_type == kMGroupedIdx) pad_row = row_ok && p.layout[m] != group;
+        OutT* drow = dbase + (int64_t)m * p.ldd;
+        static_for<TN>([&](auto jn_c) {
+            constexpr int jn = decltype(jn_c)::value;
+            const int nblk = n0 + wn * WN + jn * 32;                  // wave-uniform
+            // the lane holds columns nblk + 8 g + 4 q + {0..3} in elements 4 g + {0..3}
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = acc[jn][jm][i] * alpha;
+            const bool full = vec && nblk + 32 <= N;                   // wave-uniform
+            if (full) {
                 if (bias) {
-                    const int n = n0 + nl;
-                    v0 += n + 0 < N ? bf16_to_f32(bp[n + 0]) : 0.f;
-                    v1 += n + 1 < N ? bf16_to_f32(bp[n + 1]) : 0.f;
-                    v2 += n + 2 < N ? bf16_to_f32(bp[n + 2]) : 0.f;
-                    v3 += n + 3 < N ? bf16_to_f32(bp[n + 3]) : 0.f;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) v[4 * g + i] += to_f(bp[nblk + 8 * g + 4 * q + i]);
                 }
-                uint32_t lo = pack_bf16x2(v0, v1);
-                uint32_t hi = pack_bf16x2(v2, v3);
-                if (zero) lo = hi = 0;
-                *reinterpret_cast<i32x2*>(smem + ml * CROW + nl * 2) = i32x2{(int)lo, (int)hi};
-            });
-        });
-        __syncthreads();
-        const int rows = min(BM, (p.gemm_type == kMasked ? valid_end : M) - m0);
-        const int cols = min(BN, N - n0);
-        constexpr int CPR = BN * 2 / 16;                     // 16-byte chunks per tile row
-        uint16_t* dbase = reinterpret_cast<uint16_t*>(d_base);
-        for (int e = tid; e < BM * CPR; e += 256) {
-            const int row = e / CPR, ch = e % CPR;
-            if (row >= rows) break;
-            const int col = ch * 8;
-            if (col >= cols) continue;
-            const i32x4 val = *reinterpret_cast<const i32x4*>(smem + row * CROW + ch * 16);
-            uint16_t* dp = dbase + (int64_t)(m0 + row) * p.ldd + n0 + col;
-            if (col + 8 <= cols) {
-                *reinterpret_cast<i32x4*>(dp) = val;
-            } else {
-                const uint16_t* hv = reinterpret_cast<const uint16_t*>(&val);
-                for (int i = 0; i < cols - col; ++i) dp[i] = hv[i];
-            }
-        }
-        stamp(1);
-    } else {
-        // fp32 D (EPI == kEpiF32) or bf16 D with accumulation / unaligned rows (kEpiBf16):
-        // direct stores of each lane's four consecutive columns.
-        constexpr bool kF32 = EPI == kEpiF32;
-        using OutT = std::conditional_t<kF32, float, uint16_t>;
-        OutT* dbase = reinterpret_cast<OutT*>(d_base);
-        const OutT* bp = reinterpret_cast<const OutT*>(p.bias);
-        const bool acc_old = p.accumulate, bias = p.has_bias, vec = p.vec_store;
-        static_for<TM>([&](auto jm_c) {
-            constexpr int jm = decltype(jm_c)::value;
-            const int m = m0 + wm * WM + jm * 16 + r;
-            const bool row_ok = m < M && !(p.gemm_type == kMasked && m >= valid_end);
-            bool pad_row = false;
-            if (p.gemm_type == kMGroupedPsum) pad_row = m >= valid_end;
-            else if (p.gemm_type == kMGroupedIdx) pad_row = row_ok && p.layout[m] != group;
-            OutT* drow = dbase + (int64_t)m * p.ldd;
-            if constexpr (kF32) {
-                static_for<TN>([&](auto jn_c) {
-                    constexpr int jn = decltype(jn_c)::value;
-                    const int nb = n0 + wn * WN + jn * 16 + 4 * q;
-                    float v[4] = {acc[jn][jm][0] * alpha, acc[jn][jm][1] * alpha,
-                                  acc[jn][jm][2] * alpha, acc[jn][jm][3] * alpha};
-                    if (row_ok && nb < N) {
-                        float* dp = drow + nb;
-                        if (vec && nb + 3 < N) {
-                            f32x4 o = {v[0], v[1], v[2], v[3]};
-                            if (bias) o += f32x4{bp[nb], bp[nb + 1], bp[nb + 2], bp[nb + 3]};
-                            if (acc_old) o += *reinterpret_cast<const f32x4*>(dp);
+                if (acc_old && row_ok) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) v[4 * g + i] += to_f(drow[nblk + 8 * g + 4 * q + i]);
+                }
+                if constexpr (kF32) {
+                    if (row_ok) {
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            f32x4 o = {v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
                             if (pad_row) o = f32x4{0.f, 0.f, 0.f, 0.f};
-                            *reinterpret_cast<f32x4*>(dp) = o;
-                        } else {
-                            for (int i = 0; i < 4 && nb + i < N; ++i) {
-                                float x = v[i];
-                                if (bias) x += bp[nb + i];
-                                if (acc_old) x += dp[i];
-                                dp[i] = pad_row ? 0.f : x;
-                            }
+                            *reinterpret_cast<f32x4*>(drow + nblk + 8 * g + 4 * q) = o;
                         }
                     }
-                });
-            } else {
-                // Round every block to bf16 pairs (bias / accumulation in fp32 first).
-                uint32_t pk[TN][2];
-                static_for<TN>([&](auto jn_c) {
-                    constexpr int jn = decltype(jn_c)::value;
-                    const int nb = n0 + wn * WN + jn * 16 + 4 * q;
-                    float v[4] = {acc[jn][jm][0] * alpha, acc[jn][jm][1] * alpha,
-                                  acc[jn][jm][2] * alpha, acc[jn][jm][3] * alpha};
-                    const bool full = vec && nb + 3 < N;
-                    if (bias) {
-                        if (full) {
-                            const i32x2 b2 = *reinterpret_cast<const i32x2*>(bp + nb);
-                            v[0] += bf16_to_f32((uint16_t)(b2[0] & 0xffff));
-                            v[1] += bf16_to_f32((uint16_t)((uint32_t)b2[0] >> 16));
-                            v[2] += bf16_to_f32((uint16_t)(b2[1] & 0xffff));
-                            v[3] += bf16_to_f32((uint16_t)((uint32_t)b2[1] >> 16));
-                        } else {
-                            for (int i = 0; i < 4; ++i) v[i] += nb + i < N ? bf16_to_f32(bp[nb + i]) : 0.f;
+                } else {
+                    // pk[g] = columns 8 g + 4 q + {0..3} as two bf16 pairs
+                    uint32_t pk[4][2];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        pk[g][0] = pad_row ? 0u : pack_bf16x2(v[4 * g], v[4 * g + 1]);
+                        pk[g][1] = pad_row ? 0u : pack_bf16x2(v[4 * g + 2], v[4 * g + 3]);
+                    }
+                    // v_permlane32_swap regroups the wave halves: afterwards the lower half
+                    // (q = 0) holds columns 16..31 and the upper half (q = 1) columns 0..15 of
+                    // the block, i.e. 32 contiguous bytes per lane.
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const auto s02 = __builtin_amdgcn_permlane32_swap(pk[2][h], pk[0][h], false, false);
+                        const auto s13 = __builtin_amdgcn_permlane32_swap(pk[3][h], pk[1][h], false, false);
+                        pk[2][h] = s02[0]; pk[0][h] = s02[1];
+                        pk[3][h] = s13[0]; pk[1][h] = s13[1];
+                    }
+                    if (row_ok) {
+                        // q = 0: pk2 = 16..19, pk0 = 20..23, pk3 = 24..27, pk1 = 28..31
+                        // q = 1: pk2 = 0..3,   pk0 = 4..7,   pk3 = 8..11,  pk1 = 12..15
+                        uint16_t* dp = drow + nblk + (q ? 0 : 16);
+                        *reinterpret_cast<i32x4*>(dp) = i32x4{(int)pk[2][0], (int)pk[2][1], (int)pk[0][0], (int)pk[0][1]};
+                        *reinterpret_cast<i32x4*>(dp + 8) = i32x4{(int)pk[3][0], (int)pk[3][1], (int)pk[1][0], (int)pk[1][1]};
+                    }
+                }
+            } else if (row_ok) {
+                // ragged / unaligned block: element stores with bounds
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int n = nblk + 8 * g + 4 * q + i;
+                        if (n < N) {
+                            float x = v[4 * g + i];
+                            if (bias) x += to_f(bp[n]);
+                            if (acc_old) x += to_f(drow[n]);
+                            if constexpr (kF32) drow[n] = pad_row ? 0.f : x;
+                            else drow[n] = pad_row ? (uint16_t)0 : f32_to_bf16_rne(x);
                         }
                     }
-                    if (acc_old && row_ok) {
-                        if (full) {
-                            const i32x2 o2 = *reinterpret_cast<const i32x2*>(drow + nb);
-                            v[0] += bf16_to_f32((uint16_t)(o2[0] & 0xffff));
-                            v[1] += bf16_to_f32((uint16_t)((uint32_t)o2[0] >> 16));
-                            v[2] += bf16_to_f32((uint16_t)(o2[1] & 0xffff));
-                            v[3] += bf16_to_f32((uint16_t)((uint32_t)o2[1] >> 16));
-                        } else {
-                            for (int i = 0; i < 4; ++i) v[i] += nb + i < N ? bf16_to_f32(drow[nb + i]) : 0.f;
-                        }
-                    }
-                    pk[jn][0] = pad_row ? 0u : pack_bf16x2(v[0], v[1]);
-                    pk[jn][1] = pad_row ? 0u : pack_bf16x2(v[2], v[3]);
-                });
-                // Stores.  Two n-blocks (jn0, jn0 + 1) are regrouped across the lane halves of
-                // each 32-lane row with v_permlane16_swap so that every lane owns 8 consecutive
-                // columns: one 16-byte store per lane, 64 contiguous bytes per row.
-                auto store8 = [&](auto jn_c) {
-                    constexpr int jn = decltype(jn_c)::value;
-                    const int nb = n0 + wn * WN + jn * 16 + 4 * q;
-                    if (!row_ok || nb >= N) return;
-                    uint16_t* dp = drow + nb;
-                    if (vec && nb + 3 < N) {
-                        *reinterpret_cast<i32x2*>(dp) = i32x2{(int)pk[jn][0], (int)pk[jn][1]};
-                    } else {
-                        for (int i = 0; i < 4 && nb + i < N; ++i)
-                            dp[i] = (uint16_t)(pk[jn][i >> 1] >> ((i & 1) * 16));
-                    }
-                };
-                static_for<(TN + 1) / 2>([&](auto jp_c) {
-                    constexpr int jn0 = 2 * decltype(jp_c)::value;
-                    if constexpr (jn0 + 1 < TN) {
-                        const int nbase = n0 + wn * WN + jn0 * 16;      // wave-uniform
-                        if (vec && nbase + 32 <= N) {
-                            const auto s0 = __builtin_amdgcn_permlane16_swap(pk[jn0][0], pk[jn0 + 1][0], false, false);
-                            const auto s1 = __builtin_amdgcn_permlane16_swap(pk[jn0][1], pk[jn0 + 1][1], false, false);
-                            const int ncol = nbase + ((q & 1) ? 16 + 4 * (q - 1) : 4 * q);
-                            if (row_ok)
-                                *reinterpret_cast<i32x4*>(drow + ncol) =
-                                    i32x4{(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
-                        } else {
-                            store8(Int<jn0>{});
-                            store8(Int<jn0 + 1>{});
-                        }
-                    } else {
-                        store8(Int<jn0>{});
-                    }
-                });
             }
         });
-    }
+    });
 }
 
 }  // namespace dg

@@ -2,5 +2,5 @@
 #include "gemm_tiles.hpp"
 
 namespace dg {
-KernelFn lookup_kernel_bf16(int bm, int bn, int epi) { DG_TILE_TABLE(kBF16) }
+KernelFn lookup_kernel_bf16(int bm, int bn, int epi) { return lookup_tile<kBF16>(bm, bn, epi); }
 }  // namespace dg

@@ -2,5 +2,5 @@
 #include "gemm_tiles.hpp"
 
 namespace dg {
-KernelFn lookup_kernel_fp8fp4(int bm, int bn, int epi) { DG_TILE_TABLE(kFP8FP4) }
+KernelFn lookup_kernel_fp8fp4(int bm, int bn, int epi) { return lookup_tile<kFP8FP4>(bm, bn, epi); }
 }  // namespace dg

@@ -2,5 +2,5 @@
 #include "gemm_tiles.hpp"
 
 namespace dg {
-KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi) { DG_TILE_TABLE(kFP8FP8) }
+KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi) { return lookup_tile<kFP8FP8>(bm, bn, epi); }
 }  // namespace dg

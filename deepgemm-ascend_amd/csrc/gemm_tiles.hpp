@@ -11,22 +11,46 @@ using KernelFn = void (*)(const KParams);
 
 struct TileCfg {
     int bm, bn;
+    int wgm;      // waves along M (nw / wgm along N)
+    int nw;       // waves per workgroup: 8 = two per SIMD, so one wave's MFMAs issue while the
+                  // other waits on loads; 4 where a 4-wave tile needs more than 256 registers
+    int stages;   // depth of the LDS ring (64-K stages; deeper for small tiles to keep more
+                  // bytes in flight per CU)
+    int stage_cycles;   // measured cycles per 64-K stage with every CU busy (fp8, MI355X)
 };
 
-// Tile shapes compiled for every operand kind (BM x BN, 4 waves in 2 x 2).
-constexpr TileCfg kTiles[] = {{256, 256}, {256, 224}, {256, 128}, {128, 256},
-                              {128, 128}, {64, 128},  {32, 128}};
+// Measured on MI355X at M=4096, N=7168, K=2048 (fp8): 256x256/8 waves 65 us, 256x224/4 waves
+// 75 us, 128x128/4 waves 76 us; at M=128, N=7168, K=7168: 64x128 35 us, 128x128 44 us.
+constexpr TileCfg kTiles[] = {
+    {256, 256, 4, 8, 4, 1440}, {256, 224, 4, 4, 4, 1743}, {256, 128, 4, 8, 4, 937},
+    {128, 256, 2, 8, 4, 985},  {128, 128, 2, 4, 6, 1056}, {64, 128, 2, 4, 8, 588},
+    {32, 128, 1, 4, 8, 643},
+};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-#define DG_TILE_TABLE(KIND_)                                          \
-    if (bm == 256 && bn == 256) return epi == kEpiF32 ? &gemm_kernel<256, 256, KIND_, kEpiF32> : &gemm_kernel<256, 256, KIND_, kEpiBf16>; \
-    if (bm == 256 && bn == 224) return epi == kEpiF32 ? &gemm_kernel<256, 224, KIND_, kEpiF32> : &gemm_kernel<256, 224, KIND_, kEpiBf16>; \
-    if (bm == 256 && bn == 128) return epi == kEpiF32 ? &gemm_kernel<256, 128, KIND_, kEpiF32> : &gemm_kernel<256, 128, KIND_, kEpiBf16>; \
-    if (bm == 128 && bn == 256) return epi == kEpiF32 ? &gemm_kernel<128, 256, KIND_, kEpiF32> : &gemm_kernel<128, 256, KIND_, kEpiBf16>; \
-    if (bm == 128 && bn == 128) return epi == kEpiF32 ? &gemm_kernel<128, 128, KIND_, kEpiF32> : &gemm_kernel<128, 128, KIND_, kEpiBf16>; \
-    if (bm == 64 && bn == 128) return epi == kEpiF32 ? &gemm_kernel<64, 128, KIND_, kEpiF32> : &gemm_kernel<64, 128, KIND_, kEpiBf16>;   \
-    if (bm == 32 && bn == 128) return epi == kEpiF32 ? &gemm_kernel<32, 128, KIND_, kEpiF32> : &gemm_kernel<32, 128, KIND_, kEpiBf16>;   \
-    return nullptr;
+template <int I, int KIND>
+KernelFn pick_epi(int epi) {
+    constexpr TileCfg t = kTiles[I];
+    return epi == kEpiF32 ? &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.stages, KIND, kEpiF32>
+                          : &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.stages, KIND, kEpiBf16>;
+}
+
+template <int KIND, int I = 0>
+KernelFn lookup_tile(int bm, int bn, int epi) {
+    if constexpr (I == kNumTiles) {
+        return nullptr;
+    } else {
+        if (bm == kTiles[I].bm && bn == kTiles[I].bn) return pick_epi<I, KIND>(epi);
+        return lookup_tile<KIND, I + 1>(bm, bn, epi);
+    }
+}
+
+// Threads per workgroup of the (bm, bn) kernel (0 if not in the menu).
+inline int tile_threads(int bm, int bn) {
+    for (const TileCfg& t : kTiles)
+        if (t.bm == bm && t.bn == bn) return t.nw * 64;
+    return 0;
+}
 
 KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi);
 KernelFn lookup_kernel_fp8fp4(int bm, int bn, int epi);

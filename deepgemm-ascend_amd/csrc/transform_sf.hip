@@ -7,7 +7,9 @@
 // gran_mn times, M-grouped psum padding rows zeroed, invalid fp32 SF flagged.
 //
 // One thread produces one output int16; consecutive threads walk the contiguous MN axis so
-// the stores are fully coalesced (the output is the larger side of the transform).
+// the stores are fully coalesced (the output is the larger side of the transform).  The MN
+// axis is stored with an even leading dimension ld = align(MN, 2) (the GEMM kernel fetches
+// SF rows in pairs with 4-byte loads); the padding element of every column is written as 0.
 #include "dg_common.hpp"
 #include "../../include/deep_gemm_amd.h"
 
@@ -16,7 +18,7 @@ namespace dg {
 struct SfParams {
     const uint8_t* src;
     int64_t stride_b, stride_mn, stride_k;   // elements of the source type
-    int num_batches, sf_mn, sf_k, mn, k64, k32, gran_mn, gran_k;
+    int num_batches, sf_mn, sf_k, mn, ld, k64, k32, gran_mn, gran_k;
     const int* psum;
     int num_groups, alignment;
     int16_t* dst;
@@ -39,16 +41,16 @@ __device__ __forceinline__ bool sf_row_is_padding(const SfParams& p, int i) {
 
 template <bool kFloat>
 __global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
-    const int64_t per_batch = (int64_t)p.k64 * p.mn;
+    const int64_t per_batch = (int64_t)p.k64 * p.ld;
     const int64_t total = per_batch * p.num_batches;
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
         const int b = (int)(e / per_batch);
         const int64_t rem = e - (int64_t)b * per_batch;
-        const int k64 = (int)(rem / p.mn);
-        const int mn = (int)(rem - (int64_t)k64 * p.mn);
+        const int k64 = (int)(rem / p.ld);
+        const int mn = (int)(rem - (int64_t)k64 * p.ld);
         const int i = mn / p.gran_mn;
         uint16_t out = 0;
-        if (i < p.sf_mn && !(p.psum != nullptr && sf_row_is_padding(p, i))) {
+        if (mn < p.mn && i < p.sf_mn && !(p.psum != nullptr && sf_row_is_padding(p, i))) {
             const int64_t row_off = (int64_t)b * p.stride_b + (int64_t)i * p.stride_mn;
             if constexpr (kFloat) {
                 const uint32_t* s = reinterpret_cast<const uint32_t*>(p.src);
@@ -71,7 +73,7 @@ __global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
                 if (k64 < p.sf_k) out = s[row_off + (int64_t)k64 * p.stride_k];
             }
         }
-        p.dst[(int64_t)b * p.dst_stride_b + (int64_t)k64 * p.mn + mn] = (int16_t)out;
+        p.dst[(int64_t)b * p.dst_stride_b + (int64_t)k64 * p.ld + mn] = (int16_t)out;
     }
 }
 
@@ -100,16 +102,18 @@ extern "C" int dg_transform_sf(const void* src, int32_t src_kind, int64_t stride
         return dg_set_error("dg_transform_sf: unknown src_kind");
     }
     if (sf_mn != ceil_div(mn, gran_mn)) return dg_set_error("dg_transform_sf: sf_mn != ceil(MN / gran_mn)");
+    if (num_batches > 1 && dst_stride_b < (int64_t)ceil_div(k, 64) * align_up(mn, 2))
+        return dg_set_error("dg_transform_sf: dst batch stride smaller than ceil(K / 64) * align(MN, 2)");
     if (psum != nullptr && (num_groups < 1 || alignment < 1 || alignment % gran_mn != 0))
         return dg_set_error("dg_transform_sf: psum needs num_groups >= 1 and alignment % gran_mn == 0");
     SfParams p;
     p.src = reinterpret_cast<const uint8_t*>(src);
     p.stride_b = stride_b; p.stride_mn = stride_mn; p.stride_k = stride_k;
-    p.num_batches = num_batches; p.sf_mn = sf_mn; p.sf_k = sf_k; p.mn = mn;
+    p.num_batches = num_batches; p.sf_mn = sf_mn; p.sf_k = sf_k; p.mn = mn; p.ld = align_up(mn, 2);
     p.k64 = ceil_div(k, 64); p.k32 = ceil_div(k, 32); p.gran_mn = gran_mn; p.gran_k = gran_k;
     p.psum = psum; p.num_groups = num_groups; p.alignment = alignment;
     p.dst = dst; p.dst_stride_b = dst_stride_b; p.err = err_flag;
-    const int64_t total = (int64_t)p.k64 * mn * num_batches;
+    const int64_t total = (int64_t)p.k64 * p.ld * num_batches;
     if (total == 0) return DG_OK;
     int64_t blocks = ceil_div64(total, 256);
     if (blocks > 8192) blocks = 8192;

@@ -31,6 +31,10 @@ def _split_recipe(recipe, is_sfa: Optional[bool]) -> Tuple[int, int]:
     return (int(recipe[0]) if is_sfa else int(recipe[1])), int(recipe[2])
 
 
+def _align(x: int, a: int) -> int:
+    return (x + a - 1) // a * a
+
+
 def check_sf_layout(sf: torch.Tensor, mn: int, k: int, gran_mn: int, gran_k: int,
                     num_groups: Optional[int]) -> bool:
     """Validate ``sf``; True when it is already in the required layout (csrc/apis/layout.hpp:37-65)."""
@@ -48,9 +52,9 @@ def check_sf_layout(sf: torch.Tensor, mn: int, k: int, gran_mn: int, gran_k: int
         div_k = 64
     _assert(sf.size(-2) == _ceil_div(mn, gran_mn), f'SF MN extent {sf.size(-2)} != ceil({mn}/{gran_mn})')
     _assert(sf.size(-1) == _ceil_div(k, div_k), f'SF K extent {sf.size(-1)} != ceil({k}/{div_k})')
-    if sf.dtype == torch.int16 and gran_mn == 1 and sf.stride(-2) == 1 and sf.stride(-1) == sf.size(-2):
+    if sf.dtype == torch.int16 and gran_mn == 1 and sf.stride(-2) == 1 and sf.stride(-1) == _align(sf.size(-2), 2):
         if num_groups is not None:
-            return sf.stride(-3) == sf.size(-2) * sf.size(-1)
+            return sf.stride(-3) == sf.stride(-1) * sf.size(-1)
         return True
     return False
 
@@ -74,7 +78,9 @@ def _launch_transform_sf(sf: torch.Tensor, mn: int, k: int, gran_mn: int, gran_k
         num_groups = psum.numel()
         _assert(num_groups > 0, 'grouped_layout must contain at least one group')
     k64 = _ceil_div(k, 64)
-    out = torch.empty((num_batches, k64, mn), dtype=torch.int16, device=sf.device).transpose(-2, -1)
+    # MN axis padded to an even leading dimension (the GEMM kernels fetch SF rows in pairs)
+    ld = _align(mn, 2)
+    out = torch.empty((num_batches, k64, ld), dtype=torch.int16, device=sf.device)[:, :, :mn].transpose(-2, -1)
     if out.numel() == 0 or get_dry_run_safe():
         return out.squeeze(0) if squeeze else out
     check_err = os.environ.get('DG_CHECK_SF', '0') == '1' and sf.dtype == torch.float32
@@ -84,7 +90,7 @@ def _launch_transform_sf(sf: torch.Tensor, mn: int, k: int, gran_mn: int, gran_k
         sf.data_ptr(), _lib.DG_SF_F32 if sf.dtype == torch.float32 else _lib.DG_SF_I16,
         sf.stride(0), sf.stride(1), sf.stride(2), num_batches, sf_mn, sf_k, mn, k, gran_mn, gran_k,
         psum.data_ptr() if psum is not None else None, num_groups, alignment,
-        out.data_ptr(), k64 * mn, err.data_ptr() if err is not None else None,
+        out.data_ptr(), k64 * ld, err.data_ptr() if err is not None else None,
         torch.cuda.current_stream(sf.device).cuda_stream)
     _lib.check(rc, lib)
     if err is not None and int(err.item()) != 0:

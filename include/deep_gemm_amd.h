@@ -10,7 +10,8 @@
  * dg_transform_sf() produces, which is the layout the reference documents for
  * transform_sf_into_required_layout (csrc/apis/layout.hpp:18-35): one UE8M0 exponent byte
  * per 32 K-elements, two K-adjacent bytes per int16 (even block in the low byte), stored
- * MN-major: element (mn, k64) at sf[k64 * sf_ld + mn].
+ * MN-major: element (mn, k64) at sf[k64 * sf_ld + mn], with sf_ld (and any batch stride)
+ * even -- the kernels fetch SF rows two at a time.
  */
 #ifndef DEEP_GEMM_AMD_H_
 #define DEEP_GEMM_AMD_H_
@@ -68,7 +69,7 @@ typedef struct dg_gemm_args {
     int32_t num_groups;           /* batches / groups                                        */
     int64_t lda, ldb, ldd;
     int64_t batch_stride_a, batch_stride_b, batch_stride_d;   /* elements                   */
-    int64_t sfa_ld, sfb_ld;       /* stride between k64 rows of SF (>= MN extent)            */
+    int64_t sfa_ld, sfb_ld;       /* stride between k64 rows of SF (even, >= MN extent)      */
     int64_t sfa_batch_stride, sfb_batch_stride;
     int32_t d_dtype;              /* DG_DTYPE_*                                              */
     int32_t accumulate;           /* 1: D = D + alpha * A B^T                                */
@@ -89,8 +90,9 @@ int dg_gemm(const dg_gemm_args *args, void *stream);
  *
  * src: [num_batches][sf_mn][sf_k] of DG_SF_F32 (sf_k = ceil(K / gran_k)) or DG_SF_I16
  *      (sf_k = ceil(K / 64)), element (b, i, j) at src[b*stride_b + i*stride_mn + j*stride_k].
- * dst: packed int16, element (b, mn, k64) at dst[b*dst_stride_b + k64*mn + mn_idx],
- *      k64 < ceil(K/64), mn_idx < mn.  Row mn_idx takes SF row mn_idx / gran_mn.
+ * dst: packed int16, element (b, mn, k64) at dst[b*dst_stride_b + k64*ld + mn_idx] with
+ *      ld = align(mn, 2), k64 < ceil(K/64), mn_idx < ld; mn_idx == mn (odd mn) is written 0.
+ *      Row mn_idx < mn takes SF row mn_idx / gran_mn.  dst_stride_b >= ceil(K/64) * ld.
  * gran_k: 32 or 128 for DG_SF_F32 (128 repeats each exponent over four 32-blocks), 32 for I16.
  * psum (optional, device int32[num_groups]): M-grouped padding rows
  *      [ceil(psum[g]/gran_mn), align(psum[g], alignment)/gran_mn) (in SF rows) become 0.

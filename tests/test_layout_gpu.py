@@ -29,8 +29,13 @@ def _with_major(sf, mn_major):
 def _check(out, exp):
     assert out.dtype == torch.int16
     assert tuple(out.shape) == tuple(exp.shape)
-    assert out.stride(-2) == 1 and out.stride(-1) == out.size(-2)
+    mn = out.size(-2)
+    ld = mn + (mn & 1)   # even leading dimension; the padding element of each column is 0
+    assert out.stride(-2) == 1 and out.stride(-1) == ld
     assert torch.equal(out.cpu(), exp)
+    if mn & 1:
+        full = torch.as_strided(out, out.shape[:-2] + (ld, out.size(-1)), out.stride())
+        assert torch.all(full[..., mn, :].cpu() == 0)
 
 
 CASES = list(itertools.product((torch.float32, torch.int16), (False, True), (4096, 4097, 8192), (128, 7168, 7296),
