@@ -78,7 +78,7 @@ bool tile_allowed(const dg_gemm_args& a, int bm, int bn) {
 TileCfg select_tile(const dg_gemm_args& a, int cus) {
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
     double best = 1e300;
-    TileCfg pick = {0, 0, 0, 0, 0, 0};
+    TileCfg pick = {0, 0, 0, 0, 0, 0, 0};
     for (int i = 0; i < kNumTiles; ++i) {
         const int bm = kTiles[i].bm, bn = kTiles[i].bn;
         if (!tile_allowed(a, bm, bn)) continue;
@@ -113,7 +113,7 @@ std::mutex g_memo_mu;
 std::unordered_map<MemoKey, TileCfg, MemoHash> g_memo;
 
 TileCfg choose(const dg_gemm_args& a, int cus) {
-    if (a.block_m > 0 && a.block_n > 0) return {a.block_m, a.block_n, 0, 0, 0, 0};
+    if (a.block_m > 0 && a.block_n > 0) return {a.block_m, a.block_n, 0, 0, 0, 0, 0};
     MemoKey key;
     memset(&key, 0, sizeof(key));
     key.kind = a.kind; key.type = a.gemm_type; key.m = a.m; key.n = a.n; key.k = a.k;

@@ -128,7 +128,7 @@ __device__ __forceinline__ void swizzle_tile(int t, int nm, int nn, int gm, int&
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int BM, int BN, int WGM, int NW, int NSTAGE, int KIND, int EPI>
+template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KIND, int EPI>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
@@ -140,6 +140,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     constexpr int RBB = kBFp4 ? 32 : 64;
     constexpr int SPRA = RBA / 16, SPRB = RBB / 16;
     constexpr int NT = NW * 64;                          // threads per workgroup
+    // The last LW waves issue every global->LDS load; with LW < NW the other waves only read
+    // LDS and run MFMAs, so a stall in the load-issue path never blocks a whole SIMD.
+    constexpr int LT = LW * 64, FW = NW - LW;            // loader threads, first loader wave
+    static_assert(LW == NW || (NW == 8 && LW == 4), "loader waves");
     constexpr int WGN = NW / WGM;
     constexpr int WM = BM / WGM, WN = BN / WGN;          // wave tile
     constexpr int TM = WM / 32, TN = WN / 32;            // 32x32 MFMA blocks per wave
@@ -149,7 +153,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     constexpr int SCB = kBf16 ? 0 : (BN * 2 + 255) / 256 * 256;
     constexpr int NSCA = kBf16 ? 0 : (BM + 127) / 128, NSCB = kBf16 ? 0 : (BN + 127) / 128;
     // 256 idle bytes per stage that take the dead SF loads of waves without an SF row to fetch
-    constexpr int SPARE = (!kBf16 && NSCA + NSCB < NW) ? 256 : 0;
+    constexpr int SPARE = (!kBf16 && NSCA + NSCB < LW) ? 256 : 0;
     constexpr int STAGE = A_BYTES + B_BYTES + SCA + SCB + SPARE;
     static_assert(NSTAGE >= 3 && NSTAGE * STAGE <= 160 * 1024, "LDS budget");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * STAGE];
@@ -157,6 +161,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lwave = wave - FW, ltid = tid - FW * 64;   // loader wave / thread index
+    const bool is_loader = lwave >= 0;
     const int wm = wave % WGM, wn = wave / WGM;
     const int r = lane & 31, q = lane >> 5;
 
@@ -250,19 +256,19 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     // of a stage; lane slots map to swizzled (row, 16-byte K piece) positions.  The stage's K
     // offset rides in the scalar soffset, so the per-lane voffset is stage-invariant.
     constexpr int SLA = BM * SPRA, SLB = BN * SPRB;                    // 16-byte slots per stage
-    constexpr int NLA = (SLA + NT - 1) / NT, NLB = (SLB + NT - 1) / NT;  // per-thread loads
+    constexpr int NLA = (SLA + LT - 1) / LT, NLB = (SLB + LT - 1) / LT;  // per-thread loads
     // Packed SF rows: one buffer_load_dword ... lds per 128 rows of the tile, issued by waves
     // 0 .. NSCA-1 (A) and NSCA .. NSCA+NSCB-1 (B).
-    static_assert(NSCA + NSCB <= NW, "scale loads per stage");
+    static_assert(NSCA + NSCB <= LW, "scale loads per stage");
     constexpr int NL = NLA + NLB + (kBf16 ? 0 : 1);
     // Loads that every wave issues per stage (the waits below count the smallest number).
-    constexpr int kMinLoadsPerStage = (SLA / NT) + (SLB / NT) + (kBf16 ? 0 : 1);
+    constexpr int kMinLoadsPerStage = (SLA / LT) + (SLB / LT) + (kBf16 ? 0 : 1);
 
     int lk_a, lk_b;
     {
-        const int row_a = tid / SPRA, row_b = tid / SPRB;
-        lk_a = ((tid % SPRA) ^ slot_swizzle<SPRA>(row_a)) * 16;
-        lk_b = ((tid % SPRB) ^ slot_swizzle<SPRB>(row_b)) * 16;
+        const int row_a = ltid / SPRA, row_b = ltid / SPRB;
+        lk_a = ((ltid % SPRA) ^ slot_swizzle<SPRA>(row_a)) * 16;
+        lk_b = ((ltid % SPRB) ^ slot_swizzle<SPRB>(row_b)) * 16;
     }
     uint32_t voff_pre[NLA + NLB];
     static_for<NLA + NLB>([&](auto i) {
@@ -270,21 +276,21 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
         constexpr bool kIsA = IDX < NLA;
         constexpr int it = kIsA ? IDX : IDX - NLA;
         constexpr int SPR = kIsA ? SPRA : SPRB;
-        const int row = (it * NT + tid) / SPR;
+        const int row = (it * LT + ltid) / SPR;
         voff_pre[IDX] = row < (kIsA ? rows_a : rows_b)
                             ? (uint32_t)(row * (kIsA ? lda : ldb) + (kIsA ? lk_a : lk_b)) : kOOBOffset;
     });
-    // Per-wave packed-SF load of a stage: wave w < NSCA fetches A rows [128 w, 128 w + 128),
-    // waves NSCA .. NSCA+NSCB-1 the B rows; the other waves issue a dead (out-of-range) load
+    // Per-wave packed-SF load of a stage: loader wave w < NSCA fetches A rows [128 w, 128 w + 128),
+    // loader waves NSCA .. NSCA+NSCB-1 the B rows; the other waves issue a dead (out-of-range) load
     // into an idle word so that every wave runs the same branch-free instruction stream.
     __amdgpu_buffer_rsrc_t rs_sc;
     uint32_t sc_voff = kOOBOffset;
     int sc_step = 0, sc_lds = 0;
     bool sc_live = false;
     if constexpr (!kBf16) {
-        const bool is_a = wave < NSCA;
-        const int w = is_a ? wave : wave - NSCA;
-        sc_live = wave < NSCA + NSCB;
+        const bool is_a = lwave < NSCA;
+        const int w = is_a ? lwave : lwave - NSCA;
+        sc_live = lwave >= 0 && lwave < NSCA + NSCB;
         rs_sc = is_a ? make_rsrc(sfa + m0, ((int64_t)nk64 * p.sfa_ld - m0) * 2)
                      : make_rsrc(sfb + n0, ((int64_t)nk64 * p.sfb_ld - n0) * 2);
         const int row = w * 128 + 2 * lane;
@@ -306,12 +312,12 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
             constexpr int it = kIsA ? IDX : IDX - NLA;
             constexpr int SL = kIsA ? SLA : SLB;
             constexpr int RB = kIsA ? RBA : RBB;
-            if (SL % NT != 0 && it * NT + wave * 64 >= SL) return;
+            if (SL % LT != 0 && it * LT + lwave * 64 >= SL) return;
             const int kb = c * RB;
             const int krem = (kIsA ? kbytes_a : kbytes_b) - kb;
             const uint32_t voff = (kIsA ? lk_a : lk_b) < krem ? voff_pre[IDX] : kOOBOffset;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                kIsA ? rs_a : rs_b, (lds_void*)(sbase + (kIsA ? 0 : A_BYTES) + (it * NT + wave * 64) * 16), 16,
+                kIsA ? rs_a : rs_b, (lds_void*)(sbase + (kIsA ? 0 : A_BYTES) + (it * LT + lwave * 64) * 16), 16,
                 voff, __builtin_amdgcn_readfirstlane(live ? kb : kDeadOffset), 0, 0);
         } else if constexpr (!kBf16) {
             // packed-SF row of stage c (its k64 index is c)
@@ -383,8 +389,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     // registers of the next stage (slot sn) into the other set and issues the loads of stage cl
     // into slot sl, all interleaved with the MFMA groups (one group = the TM blocks of one jn).
     constexpr int kLPG = (NL + TN - 1) / TN;
-    auto compute = [&](int s, auto buf_tag, int sn, int cl, int sl, bool load_live) {
+    auto compute = [&](int s, auto buf_tag, auto loads_tag, int sn, int cl, int sl, bool load_live) {
         constexpr int buf = decltype(buf_tag)::value;
+        constexpr bool kLoads = decltype(loads_tag)::value != 0;
         const uint8_t* sB = smem + s * STAGE + A_BYTES;
         const uint8_t* sSB = smem + s * STAGE + A_BYTES + B_BYTES + SCA;
         i32x8 fb_cur = fb0[buf];
@@ -423,7 +430,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
             });
             static_for<kLPG>([&](auto li) {
                 constexpr int idx = jn * kLPG + decltype(li)::value;
-                if constexpr (idx < NL) issue_item(Int<idx>{}, cl, sl, load_live);
+                if constexpr (kLoads && idx < NL) issue_item(Int<idx>{}, cl, sl, load_live);
             });
             __builtin_amdgcn_sched_barrier(0);
             fb_cur = fb_next;
@@ -435,7 +442,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     // Prologue: stages 0 .. NSTAGE-2 in flight, stage 0 visible, its ahead registers loaded.
     static_for<NSTAGE - 1>([&](auto i) {
         constexpr int st = decltype(i)::value;
-        issue_stage(st - shift, st, st >= shift && st < num_virtual);
+        if (is_loader) issue_stage(st - shift, st, st >= shift && st < num_virtual);
     });
     wait_vmcnt<(NSTAGE - 2) * kMinLoadsPerStage>();
     stage_barrier();
@@ -446,16 +453,21 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     // The barrier also certifies that every wave finished reading stage c - 1 (its B side in
     // iteration c - 1, its ahead registers in iteration c - 2), so its slot can take stage
     // c + NSTAGE - 1.
-    auto iteration = [&](int c, auto buf_tag) {
+    auto iteration = [&](int c, auto buf_tag, auto loads_tag) {
         wait_vmcnt<(NSTAGE - 3) * kMinLoadsPerStage>();
         stage_barrier();
         const int cl = c + NSTAGE - 1;
-        compute(c % NSTAGE, buf_tag, (c + 1) % NSTAGE, cl - shift, cl % NSTAGE, cl < num_virtual);
+        compute(c % NSTAGE, buf_tag, loads_tag, (c + 1) % NSTAGE, cl - shift, cl % NSTAGE, cl < num_virtual);
     };
-    for (int c = 0; c < num_virtual; c += 2) {
-        iteration(c, Int<0>{});
-        iteration(c + 1, Int<1>{});
-    }
+    // Loader and non-loader waves run separate copies of the loop, each branch-free.
+    auto main_loop = [&](auto loads_tag) {
+        for (int c = 0; c < num_virtual; c += 2) {
+            iteration(c, Int<0>{}, loads_tag);
+            iteration(c + 1, Int<1>{}, loads_tag);
+        }
+    };
+    if (LW == NW || is_loader) main_loop(Int<1>{});
+    else main_loop(Int<0>{});
     __builtin_amdgcn_s_waitcnt(0);
 
     // ------------------------------------------------------------------ epilogue

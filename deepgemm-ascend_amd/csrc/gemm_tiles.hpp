@@ -14,25 +14,26 @@ struct TileCfg {
     int wgm;      // waves along M (nw / wgm along N)
     int nw;       // waves per workgroup: 8 = two per SIMD, so one wave's MFMAs issue while the
                   // other waits on loads; 4 where a 4-wave tile needs more than 256 registers
+    int lw;       // waves that issue the global->LDS loads (nw, or 4 of 8)
     int stages;   // depth of the LDS ring (64-K stages; deeper for small tiles to keep more
                   // bytes in flight per CU)
     int stage_cycles;   // measured cycles per 64-K stage with every CU busy (fp8, MI355X)
 };
 
-// Measured on MI355X at M=4096, N=7168, K=2048 (fp8): 256x256/8 waves 65 us, 256x224/4 waves
+// Measured on MI355X at M=4096, N=7168, K=2048 (fp8): 256x256/8 waves (4 loaders) 63 us, 256x224/4 waves
 // 75 us, 128x128/4 waves 76 us; at M=128, N=7168, K=7168: 64x128 35 us, 128x128 44 us.
 constexpr TileCfg kTiles[] = {
-    {256, 256, 4, 8, 4, 1440}, {256, 224, 4, 4, 4, 1743}, {256, 128, 4, 8, 4, 937},
-    {128, 256, 2, 8, 4, 985},  {128, 128, 2, 4, 6, 1056}, {64, 128, 2, 4, 8, 588},
-    {32, 128, 1, 4, 8, 643},
+    {256, 256, 4, 8, 4, 4, 1380}, {256, 224, 4, 4, 4, 4, 1743}, {256, 128, 4, 8, 8, 4, 937},
+    {128, 256, 2, 8, 8, 4, 985},  {128, 128, 2, 4, 4, 4, 1056}, {64, 128, 2, 4, 4, 8, 588},
+    {32, 128, 1, 4, 4, 8, 643},
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
 template <int I, int KIND>
 KernelFn pick_epi(int epi) {
     constexpr TileCfg t = kTiles[I];
-    return epi == kEpiF32 ? &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.stages, KIND, kEpiF32>
-                          : &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.stages, KIND, kEpiBf16>;
+    return epi == kEpiF32 ? &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiF32>
+                          : &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiBf16>;
 }
 
 template <int KIND, int I = 0>
