@@ -113,8 +113,13 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
 // Workgroup barrier for the stage ring.  Unlike __syncthreads() it carries no memory fence,
 // so the LDS-DMA loads of later stages stay in flight across it; the stage it publishes was
 // already waited for with an explicit vmcnt.  The "memory" clobber keeps the compiler from
-// moving LDS accesses across it.
-__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// moving LDS accesses across it, the scheduling barriers keep register-only work (MFMAs) of one
+// stage from drifting past the next stage's barrier.
+__device__ __forceinline__ void stage_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
 
 // GROUP_M tile order: walk n inside bands of `gm` m-blocks (L2 reuse of A and B tiles).
 __device__ __forceinline__ void swizzle_tile(int t, int nm, int nn, int gm, int& mb, int& nb) {
@@ -264,22 +269,19 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     // Loads that every wave issues per stage (the waits below count the smallest number).
     constexpr int kMinLoadsPerStage = (SLA / LT) + (SLB / LT) + (kBf16 ? 0 : 1);
 
+    // Per-lane byte offset of the thread's first 16-byte slot of the A / B stage and the K piece
+    // it covers; load item `it` adds it * LT / SPR rows through the scalar offset.
     int lk_a, lk_b;
+    uint32_t vbase_a, vbase_b;
     {
         const int row_a = ltid / SPRA, row_b = ltid / SPRB;
         lk_a = ((ltid % SPRA) ^ slot_swizzle<SPRA>(row_a)) * 16;
         lk_b = ((ltid % SPRB) ^ slot_swizzle<SPRB>(row_b)) * 16;
+        vbase_a = row_a < rows_a ? (uint32_t)(row_a * lda + lk_a) : kOOBOffset;
+        vbase_b = row_b < rows_b ? (uint32_t)(row_b * ldb + lk_b) : kOOBOffset;
     }
-    uint32_t voff_pre[NLA + NLB];
-    static_for<NLA + NLB>([&](auto i) {
-        constexpr int IDX = decltype(i)::value;
-        constexpr bool kIsA = IDX < NLA;
-        constexpr int it = kIsA ? IDX : IDX - NLA;
-        constexpr int SPR = kIsA ? SPRA : SPRB;
-        const int row = (it * LT + ltid) / SPR;
-        voff_pre[IDX] = row < (kIsA ? rows_a : rows_b)
-                            ? (uint32_t)(row * (kIsA ? lda : ldb) + (kIsA ? lk_a : lk_b)) : kOOBOffset;
-    });
+    const int vstep_a = __builtin_amdgcn_readfirstlane((int)((LT / SPRA) * lda));
+    const int vstep_b = __builtin_amdgcn_readfirstlane((int)((LT / SPRB) * ldb));
     // Per-wave packed-SF load of a stage: loader wave w < NSCA fetches A rows [128 w, 128 w + 128),
     // loader waves NSCA .. NSCA+NSCB-1 the B rows; the other waves issue a dead (out-of-range) load
     // into an idle word so that every wave runs the same branch-free instruction stream.
@@ -315,10 +317,13 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
             if (SL % LT != 0 && it * LT + lwave * 64 >= SL) return;
             const int kb = c * RB;
             const int krem = (kIsA ? kbytes_a : kbytes_b) - kb;
-            const uint32_t voff = (kIsA ? lk_a : lk_b) < krem ? voff_pre[IDX] : kOOBOffset;
+            // Rows past a ragged tile's edge fall outside the tile's buffer range and read zeros.
+            // The item's row step rides in the scalar offset with the stage's K offset.
+            const uint32_t voff = (kIsA ? lk_a : lk_b) < krem ? (kIsA ? vbase_a : vbase_b) : kOOBOffset;
+            const int soff = kb + it * (kIsA ? vstep_a : vstep_b);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 kIsA ? rs_a : rs_b, (lds_void*)(sbase + (kIsA ? 0 : A_BYTES) + (it * LT + lwave * 64) * 16), 16,
-                voff, __builtin_amdgcn_readfirstlane(live ? kb : kDeadOffset), 0, 0);
+                voff, __builtin_amdgcn_readfirstlane(live ? soff : kDeadOffset), 0, 0);
         } else if constexpr (!kBf16) {
             // packed-SF row of stage c (its k64 index is c)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_sc, (lds_void*)(sbase + sc_lds), 4, sc_voff,
