@@ -25,6 +25,8 @@ constexpr int kFmtE2M1 = 4;
 // Buffer-resource word 3 for raw (stride 0) loads with range checking on gfx9-class parts.
 constexpr uint32_t kBufferRsrcWord3 = 0x00020000u;
 // voffset that is always beyond num_records: such a lane reads zeros.
+// Buffer-instruction cache-policy bit sc0: a load that misses the CU's L1 (served by the L2).
+constexpr int kCacheSc0 = 1;
 constexpr uint32_t kOOBOffset = 0x80000000u;
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -46,6 +48,7 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
 
 __host__ __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ __forceinline__ int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ __forceinline__ int64_t align_up64(int64_t a, int64_t b) { return ceil_div64(a, b) * b; }
 __host__ __device__ __forceinline__ int align_up(int a, int b) { return ceil_div(a, b) * b; }
 
 }  // namespace dg

@@ -75,29 +75,113 @@ bool tile_allowed(const dg_gemm_args& a, int bm, int bn) {
     return true;
 }
 
-TileCfg select_tile(const dg_gemm_args& a, int cus) {
+// Launch plan: tile shape and K split.
+struct Plan {
+    TileCfg tile;
+    int split;          // K ranges per tile (1 = no split)
+    int split_stages;   // K stages per range
+};
+
+int k_stage_elems(int kind) { return kind == kBF16 ? 32 : 64; }
+
+// Split-K is offered to dense / batched GEMMs whose tiles alone cannot fill the CUs.
+bool split_capable(const dg_gemm_args& a) { return a.gemm_type == kNormal || a.gemm_type == kBatched; }
+
+int64_t plan_tiles(const dg_gemm_args& a, const TileCfg& t) {
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
+    return (int64_t)ceil_div(a.m, t.bm) * ceil_div(a.n, t.bn) * groups;
+}
+
+// Workspace layout: a fixed area of tile counters that every launch leaves at zero (shared by
+// all plans, so a partial tile of one plan never lands on another plan's counters), then the
+// partial tiles.
+constexpr int64_t kCounterBytes = 64 * 1024;
+constexpr int kXcds = 8;   // MI355X: 8 XCDs, workgroup b dispatched to XCD b % 8
+constexpr int64_t kMaxSplitTiles = kCounterBytes / 4;
+
+int64_t plan_workspace(const dg_gemm_args& a, const Plan& pl) {
+    if (pl.split <= 1) return 0;
+    const int64_t tiles = plan_tiles(a, pl.tile);
+    return kCounterBytes + tiles * pl.split * (int64_t)pl.tile.bm * pl.tile.bn * 4;
+}
+
+// Skinny (M <= 128) dense / batched GEMMs are bound by how many bytes the CUs keep in flight,
+// not by MFMA time.  Measured on MI355X (fp8, us): 128x2112x7168 64x128/split 4 17.9 (unsplit
+// 27.5), 128x4096x7168 64x128/3 20.6 (unsplit 28.3), 128x7168x16384 128x128/4 40.1,
+// 128x7168x2048 64x128/1 13.2 (split 2: 15.5), 128x24576x1536 128x128/1 16.6.  The split
+// reduction costs a few microseconds, so K is split only when it is long (about one range per
+// 2048 K) and the tiles alone leave CUs idle.
+bool skinny_plan(const dg_gemm_args& a, int cus, bool allow_split, Plan& out) {
+    if (a.m > 128 || !(a.gemm_type == kNormal || a.gemm_type == kBatched)) return false;
+    const TileCfg* t64 = nullptr;
+    const TileCfg* t128 = nullptr;
+    for (const TileCfg& c : kTiles) {
+        if (c.bm == 64 && c.bn == 128) t64 = &c;
+        if (c.bm == 128 && c.bn == 128) t128 = &c;
+    }
+    if (t64 == nullptr || t128 == nullptr) return false;
+    const TileCfg& tc = plan_tiles(a, *t64) > cus && a.m > 64 ? *t128 : *t64;
+    const int64_t tiles = plan_tiles(a, tc);
+    const int ns = ceil_div(a.k, k_stage_elems(a.kind));
+    int sp = 1;
+    if (allow_split && a.k > 2048 && tiles <= kMaxSplitTiles) {
+        sp = (a.k + 1024) / 2048;
+        sp = (int)std::min<int64_t>(sp, std::max<int64_t>(1, cus / tiles));
+        sp = (int)std::min<int64_t>(sp, std::max<int64_t>(1, (cus / kXcds) / ceil_div64(tiles, kXcds)));
+        sp = std::max(1, std::min(sp, 16));
+    }
+    const int sps = ceil_div(ns, sp);
+    out = {tc, ceil_div(ns, sps), sps};
+    return true;
+}
+
+Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
+    Plan skinny;
+    if (skinny_plan(a, cus, allow_split, skinny)) return skinny;
+    allow_split = false;   // wide problems fill the CUs with tiles
+    const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
+    const int ns = ceil_div(a.k, k_stage_elems(a.kind));
+    // HBM floor: operands once, D once (8 TB/s at ~2.1 GHz is ~3800 bytes per cycle).
+    const double esz = a.kind == kBF16 ? 2.0 : 1.0;
+    // (The plan must not depend on D's dtype: a bf16 D is then exactly the RNE rounding of the
+    // fp32 D of the same call, with the same K split and summation order.)
+    const double hbm_bytes = esz * ((double)a.m + a.n) * a.k * groups + 2.0 * a.m * a.n * groups;
     double best = 1e300;
-    TileCfg pick = {0, 0, 0, 0, 0, 0, 0};
+    Plan pick = {{0, 0, 0, 0, 0, 0}, 1, ns};
     for (int i = 0; i < kNumTiles; ++i) {
-        const int bm = kTiles[i].bm, bn = kTiles[i].bn;
-        if (!tile_allowed(a, bm, bn)) continue;
-        const int64_t tiles = (int64_t)ceil_div(a.m, bm) * ceil_div(a.n, bn) * groups;
-        const int64_t rounds = ceil_div64(tiles, cus);
-        // Waves of tiles x (K stages at the tile's measured stage time + the fixed cost of a
-        // tile: pipeline fill and the epilogue's stores).
-        const double t_tile = (double)ceil_div(a.k, 64) * kTiles[i].stage_cycles + 6000.0 + bm * bn / 8.0;
-        const double t = (double)rounds * t_tile;
-        if (t < best * 0.999) {
-            best = t;
-            pick = kTiles[i];
+        const TileCfg& tc = kTiles[i];
+        if (!tile_allowed(a, tc.bm, tc.bn)) continue;
+        const int64_t tiles = plan_tiles(a, tc);
+        const int max_split = allow_split && tiles <= kMaxSplitTiles ? std::min(16, std::max(1, ns / 4)) : 1;
+        for (int sp = 1; sp <= max_split; ++sp) {
+            const int sps = ceil_div(ns, sp);
+            const int s_eff = ceil_div(ns, sps);
+            if (sp > 1 && s_eff != sp) continue;
+            // The splits of a tile run on one XCD (kXcds of them, cus / kXcds CUs each).
+            const int64_t rounds = sp == 1 ? ceil_div64(tiles, cus)
+                                           : ceil_div64(ceil_div64(tiles, kXcds) * sp, std::max(1, cus / kXcds));
+            if (sp > 1 && rounds > 1) break;
+            // Waves of workgroups x (their K stages at the tile's measured stage time + the
+            // fixed cost of a tile: pipeline fill and the epilogue's stores), plus the split
+            // reduction (measured ~10K cycles: partial stores, arrival count, partial reads).
+            double t = (double)rounds * ((double)sps * tc.stage_cycles + 6000.0 + tc.bm * tc.bn / 8.0);
+            double bytes = hbm_bytes;
+            if (sp > 1) {
+                t += 10000.0 + 500.0 * sp;
+                bytes += 8.0 * a.m * a.n * groups * sp;
+            }
+            t = std::max(t, bytes / 3800.0);
+            if (t < best * 0.97) {
+                best = t;
+                pick = {tc, sp, sps};
+            }
         }
     }
     return pick;
 }
 
 struct MemoKey {
-    int kind, type, m, n, k, g, cus, align;
+    int kind, type, m, n, k, g, cus, align, allow_split;
     bool operator==(const MemoKey& o) const { return memcmp(this, &o, sizeof(*this)) == 0; }
 };
 struct MemoHash {
@@ -110,20 +194,42 @@ struct MemoHash {
 };
 
 std::mutex g_memo_mu;
-std::unordered_map<MemoKey, TileCfg, MemoHash> g_memo;
+std::unordered_map<MemoKey, Plan, MemoHash> g_memo;
 
-TileCfg choose(const dg_gemm_args& a, int cus) {
-    if (a.block_m > 0 && a.block_n > 0) return {a.block_m, a.block_n, 0, 0, 0, 0, 0};
+Plan choose(const dg_gemm_args& a, int cus, bool allow_split) {
+    const int ns = ceil_div(a.k, k_stage_elems(a.kind));
+    allow_split = allow_split && split_capable(a);
+    if (a.block_m > 0 && a.block_n > 0) {
+        TileCfg t = {a.block_m, a.block_n, 0, 0, 0, 0, 0};
+        for (const TileCfg& c : kTiles)
+            if (c.bm == a.block_m && c.bn == a.block_n) t = c;
+        int sp = allow_split && a.split_k > 1 && plan_tiles(a, t) <= kMaxSplitTiles ? std::min(a.split_k, std::max(1, ns)) : 1;
+        const int sps = ceil_div(ns, sp);
+        return {t, ceil_div(ns, sps), sps};
+    }
     MemoKey key;
     memset(&key, 0, sizeof(key));
     key.kind = a.kind; key.type = a.gemm_type; key.m = a.m; key.n = a.n; key.k = a.k;
     key.g = a.num_groups; key.cus = cus; key.align = a.alignment;
-    std::lock_guard<std::mutex> lk(g_memo_mu);
-    auto it = g_memo.find(key);
-    if (it != g_memo.end()) return it->second;
-    const TileCfg c = select_tile(a, cus);
-    g_memo.emplace(key, c);
-    return c;
+    key.allow_split = allow_split && a.split_k != 1;
+    Plan pl;
+    {
+        std::lock_guard<std::mutex> lk(g_memo_mu);
+        auto it = g_memo.find(key);
+        if (it != g_memo.end()) {
+            pl = it->second;
+        } else {
+            pl = select_plan(a, cus, key.allow_split);
+            g_memo.emplace(key, pl);
+        }
+    }
+    if (allow_split && a.split_k > 1 && plan_tiles(a, pl.tile) <= kMaxSplitTiles) {
+        // forced split count (tuning), on the heuristic's tile shape
+        const int sps = ceil_div(ns, std::min(a.split_k, std::max(1, ns)));
+        pl.split = ceil_div(ns, sps);
+        pl.split_stages = sps;
+    }
+    return pl;
 }
 
 int elem_bytes_times2(int kind, bool is_a) {
@@ -142,10 +248,21 @@ int elem_bytes_times2(int kind, bool is_a) {
 extern "C" int dg_select_config(const dg_gemm_args* args, int32_t* block_m, int32_t* block_n) {
     if (args == nullptr) return dg_set_error("dg_select_config: null args");
     const int cus = args->num_cus > 0 ? args->num_cus : dg::device_cus();
-    const dg::TileCfg c = dg::choose(*args, cus);
-    if (c.bm == 0) return dg_set_error("no tile shape fits this problem (M-grouped alignment must be a multiple of 32)");
-    if (block_m) *block_m = c.bm;
-    if (block_n) *block_n = c.bn;
+    const dg::Plan pl = dg::choose(*args, cus, args->workspace != nullptr || args->split_k > 1);
+    if (pl.tile.bm == 0) return dg_set_error("no tile shape fits this problem (M-grouped alignment must be a multiple of 32)");
+    if (block_m) *block_m = pl.tile.bm;
+    if (block_n) *block_n = pl.tile.bn;
+    return DG_OK;
+}
+
+extern "C" int dg_gemm_workspace_size(const dg_gemm_args* args, int64_t* bytes) {
+    if (args == nullptr || bytes == nullptr) return dg_set_error("dg_gemm_workspace_size: null argument");
+    *bytes = 0;
+    if (args->m <= 0 || args->n <= 0 || args->k <= 0) return DG_OK;
+    const int cus = args->num_cus > 0 ? args->num_cus : dg::device_cus();
+    const dg::Plan pl = dg::choose(*args, cus, true);
+    if (pl.tile.bm == 0) return dg_set_error("no tile shape fits this problem (M-grouped alignment must be a multiple of 32)");
+    *bytes = dg::plan_workspace(*args, pl);
     return DG_OK;
 }
 
@@ -189,7 +306,13 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     }
 
     const int cus = a.num_cus > 0 ? a.num_cus : device_cus();
-    const TileCfg cfg = choose(a, cus);
+    if (a.split_k < 0) return dg_set_error("dg_gemm: split_k must be >= 0");
+    Plan plan = choose(a, cus, a.workspace != nullptr);
+    if (plan.split > 1 && plan_workspace(a, plan) > a.workspace_bytes) {
+        if (a.split_k > 1) return dg_set_error("dg_gemm: workspace smaller than dg_gemm_workspace_size() reports");
+        plan = choose(a, cus, false);
+    }
+    const TileCfg cfg = plan.tile;
     if (cfg.bm == 0) return dg_set_error("dg_gemm: no tile shape fits this problem");
     if (!tile_allowed(a, cfg.bm, cfg.bn)) return dg_set_error("dg_gemm: block_m must divide the M-grouped alignment");
     // Direct register stores measured faster than staging the tile through LDS.
@@ -226,9 +349,18 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     p.kbytes_a = (int)kbytes_a; p.kbytes_b = (int)kbytes_b;
     p.group_m = 4;
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
-    const int64_t grid = (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
-    if (grid <= 0) return DG_OK;
+    const int64_t tiles = (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
+    if (tiles <= 0) return DG_OK;
+    // split-K grids are padded to whole groups of 8 tiles (one per XCD)
+    const int64_t grid = plan.split > 1 ? align_up64(tiles, 8) * plan.split : tiles;
     if (grid > 0x7fffffffLL) return dg_set_error("dg_gemm: too many tiles");
+    p.split_k = plan.split;
+    p.split_stages = plan.split_stages;
+    p.num_tiles = (int)tiles;
+    if (plan.split > 1) {
+        p.counters = reinterpret_cast<int*>(a.workspace);
+        p.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.workspace) + kCounterBytes);
+    }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3((unsigned)tile_threads(cfg.bm, cfg.bn)), 0, st, p);
     const hipError_t e = hipGetLastError();

@@ -52,6 +52,13 @@ struct KParams {
     int num_m_blocks, num_n_blocks;
     int kbytes_a, kbytes_b;    // bytes of one K row (multiple of 16)
     int group_m;               // tile-order swizzle width along M
+    // Split-K: the K loop of every tile is cut into split_k ranges of split_stages 64-K stages,
+    // one workgroup each; the partial fp32 tiles meet in `ws` and the last workgroup of a tile
+    // (per `counters`, which every launch leaves at zero) reduces them and runs the epilogue.
+    int split_k, split_stages;
+    int num_tiles;             // tiles of the launch (split-K grids are padded past it)
+    float* ws;
+    int* counters;
 };
 
 // Epilogue variants.
@@ -173,7 +180,19 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
 
     // ------------------------------------------------------------------ tile selection
     const int nm = p.num_m_blocks, nn = p.num_n_blocks;
-    int t = xcd_remap(blockIdx.x, gridDim.x);
+    int t, split = 0;
+    if (p.split_k > 1) {
+        // Split-K launch: grid = 8 * ceil(tiles / 8) * split_k, and workgroup b serves tile
+        // (b / 8 / split_k) * 8 + b % 8, split (b / 8) % split_k, so all splits of a tile share
+        // b % 8 -- the XCD (and L2) the dispatcher places them on.
+        const int b = blockIdx.x, r = b >> 3;
+        t = (r / p.split_k) * 8 + (b & 7);
+        split = r % p.split_k;
+        if (t >= p.num_tiles) return;
+    } else {
+        t = xcd_remap(blockIdx.x, gridDim.x);
+    }
+    const int tile_id = t;
     int batch = 0;
     if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
         batch = t / (nm * nn);
@@ -251,7 +270,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     // The ring walks an even number of virtual stages so the main loop is a pair of iterations
     // with static register sets; an odd stage count gets one leading dead stage (all-zero
     // operands and scales, so it adds nothing to the accumulators).
-    const int num_stages = ceil_div(p.k, KS);
+    // K stages of this workgroup: [c0, c0 + num_stages) of the whole K loop.
+    const int c0 = split * p.split_stages;
+    const int num_stages = p.split_k > 1 ? min(p.split_stages, ceil_div(p.k, KS) - c0) : ceil_div(p.k, KS);
     const int shift = num_stages & 1;
     const int num_virtual = num_stages + shift;
     const int nk64 = ceil_div(p.k, 64);
@@ -447,7 +468,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     // Prologue: stages 0 .. NSTAGE-2 in flight, stage 0 visible, its ahead registers loaded.
     static_for<NSTAGE - 1>([&](auto i) {
         constexpr int st = decltype(i)::value;
-        if (is_loader) issue_stage(st - shift, st, st >= shift && st < num_virtual);
+        if (is_loader) issue_stage(c0 + st - shift, st, st >= shift && st < num_virtual);
     });
     wait_vmcnt<(NSTAGE - 2) * kMinLoadsPerStage>();
     stage_barrier();
@@ -462,7 +483,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
         wait_vmcnt<(NSTAGE - 3) * kMinLoadsPerStage>();
         stage_barrier();
         const int cl = c + NSTAGE - 1;
-        compute(c % NSTAGE, buf_tag, loads_tag, (c + 1) % NSTAGE, cl - shift, cl % NSTAGE, cl < num_virtual);
+        compute(c % NSTAGE, buf_tag, loads_tag, (c + 1) % NSTAGE, c0 + cl - shift, cl % NSTAGE, cl < num_virtual);
     };
     // Loader and non-loader waves run separate copies of the loop, each branch-free.
     auto main_loop = [&](auto loads_tag) {
@@ -474,6 +495,72 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     if (LW == NW || is_loader) main_loop(Int<1>{});
     else main_loop(Int<0>{});
     __builtin_amdgcn_s_waitcnt(0);
+
+    // ------------------------------------------------------------------ split-K reduction
+    if (p.split_k > 1) {
+        // This workgroup's partial tile, in accumulator-register order (coalesced 16-byte
+        // stores and loads; the reducing workgroup uses the same lane mapping).
+        float* const tile_ws = p.ws + (int64_t)tile_id * p.split_k * (BM * BN);
+        auto part = [&](int sp, int jn, int jm) {
+            return tile_ws + (int64_t)sp * (BM * BN) + (((wave * TN + jn) * TM + jm) * 64 + lane) * 16;
+        };
+        static_for<TN>([&](auto jn_c) {
+            constexpr int jn = decltype(jn_c)::value;
+            static_for<TM>([&](auto jm_c) {
+                constexpr int jm = decltype(jm_c)::value;
+                float* dst = part(split, jn, jm);
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    *reinterpret_cast<f32x4*>(dst + 4 * g) =
+                        f32x4{acc[jn][jm][4 * g], acc[jn][jm][4 * g + 1], acc[jn][jm][4 * g + 2], acc[jn][jm][4 * g + 3]};
+            });
+        });
+        // Publish the partial and count arrivals; only the last workgroup of the tile goes on.
+        // A workgroup on its tile's home XCD (hardware XCC id == b % 8) only waits for its
+        // stores to reach the XCD's L2, which every split on that XCD reads; one elsewhere (a
+        // dispatcher that does not place workgroups round-robin) makes its partial visible
+        // device-wide and marks the counter (+ 1 << 16), and the reducer then also acquires
+        // device-wide.  Either way no L2 is flushed or invalidated on the fast path.
+        const int xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xf;   // HW_REG_XCC_ID[3:0]
+        const bool home = xcc == (int)(blockIdx.x & 7);
+        // Every wave waits until its own partial stores are acknowledged by the L2 (the "memory"
+        // clobber keeps the compiler from sinking them past the wait) before the arrival count.
+        if (home) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else __threadfence();
+        __syncthreads();
+        int* flag = reinterpret_cast<int*>(smem);
+        if (tid == 0)
+            *flag = __hip_atomic_fetch_add(p.counters + tile_id, home ? 1 : 1 + (1 << 16), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const int prev = *flag;
+        if ((prev & 0xffff) != p.split_k - 1) return;
+        if (!home || (prev >> 16) != 0) __threadfence();
+        // Sum the partials in split order, whichever split arrived last, so a launch's result
+        // does not depend on workgroup timing.
+        static_for<TN>([&](auto i) {
+            static_for<TM>([&](auto j) { acc[decltype(i)::value][decltype(j)::value] = f32x16{}; });
+        });
+        const __amdgpu_buffer_rsrc_t rs_ws = make_rsrc(tile_ws, (int64_t)p.split_k * (BM * BN) * 4);
+        for (int sp = 0; sp < p.split_k; ++sp) {
+            static_for<TN>([&](auto jn_c) {
+                constexpr int jn = decltype(jn_c)::value;
+                static_for<TM>([&](auto jm_c) {
+                    constexpr int jm = decltype(jm_c)::value;
+                    // sc0 loads miss this CU's L1 (which may hold stale lines) and read the L2
+                    const uint32_t off = (uint32_t)((part(sp, jn, jm) - tile_ws) * 4);
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const f32x4 v = __builtin_bit_cast(
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_ws, off + 16 * g, 0, kCacheSc0));
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[jn][jm][4 * g + i] += v[i];
+                    }
+                });
+            });
+        }
+        if (tid == 0) __hip_atomic_store(p.counters + tile_id, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 
     // ------------------------------------------------------------------ epilogue
     // All accumulator indexing is in compile-time-unrolled loops (static_for): a runtime

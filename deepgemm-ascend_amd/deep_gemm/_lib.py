@@ -20,7 +20,7 @@ DG_SF_F32, DG_SF_I16 = 0, 1
 
 # Every symbol include/deep_gemm_amd.h declares.
 EXPORTED_SYMBOLS = ('dg_gemm', 'dg_transform_sf', 'dg_device_num_cus', 'dg_select_config',
-                    'dg_last_error', 'dg_version')
+                    'dg_gemm_workspace_size', 'dg_last_error', 'dg_version')
 
 
 class GemmArgs(ctypes.Structure):
@@ -37,7 +37,8 @@ class GemmArgs(ctypes.Structure):
         ('sfa_batch_stride', ctypes.c_int64), ('sfb_batch_stride', ctypes.c_int64),
         ('d_dtype', ctypes.c_int32), ('accumulate', ctypes.c_int32), ('alpha', ctypes.c_float),
         ('alignment', ctypes.c_int32), ('block_m', ctypes.c_int32), ('block_n', ctypes.c_int32),
-        ('num_cus', ctypes.c_int32),
+        ('num_cus', ctypes.c_int32), ('split_k', ctypes.c_int32),
+        ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_int64),
     ]
 
 
@@ -74,6 +75,8 @@ def load(path=None) -> ctypes.CDLL:
         lib.dg_select_config.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(ctypes.c_int32),
                                          ctypes.POINTER(ctypes.c_int32)]
         lib.dg_select_config.restype = ctypes.c_int
+        lib.dg_gemm_workspace_size.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(ctypes.c_int64)]
+        lib.dg_gemm_workspace_size.restype = ctypes.c_int
         lib.dg_last_error.restype = ctypes.c_char_p
         lib.dg_version.restype = ctypes.c_char_p
         if path is None:

@@ -10,7 +10,9 @@ The kernels read K-major operands with 16-byte-aligned rows.  Operands given MN-
 with a K extent / stride that is not 16-byte aligned, are first copied into that layout on
 the device (a layout conversion, not a change of the arithmetic).
 """
+import ctypes
 import os
+import threading
 from typing import Optional, Tuple
 
 import torch
@@ -100,10 +102,36 @@ def _kind(a: torch.Tensor, b: torch.Tensor) -> int:
     raise RuntimeError('Unsupported operand dtypes')
 
 
-def _launch(args: _lib.GemmArgs, stream: int) -> None:
+# Split-K workspaces, one per (device, stream): zero-filled at allocation and left zero-filled by
+# every launch, so back-to-back launches on one stream share it.
+_workspaces = {}
+_ws_lock = threading.Lock()
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index, stream)
+    with _ws_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
+        return ws
+
+
+def _launch(args: _lib.GemmArgs, d: torch.Tensor) -> None:
     if get_dry_run():
         return
     lib = _lib.load()
+    stream = _stream(d)
+    forced = os.environ.get('DG_SPLIT_K')   # tuning override: 1 = never split, n > 1 = split n ways
+    if forced:
+        args.split_k = int(forced)
+    if args.gemm_type in (_lib.DG_GEMM_NORMAL, _lib.DG_GEMM_BATCHED) and args.split_k != 1:
+        nbytes = ctypes.c_int64(0)
+        _lib.check(lib.dg_gemm_workspace_size(args, ctypes.byref(nbytes)), lib)
+        if nbytes.value > 0:
+            ws = _workspace(d.device, stream, nbytes.value)
+            args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
     _lib.check(lib.dg_gemm(args, stream), lib)
 
 
@@ -197,7 +225,7 @@ def _dense_gemm(a, sfa, b, sfb, d, c, recipe, recipe_a, recipe_b, disable_ue8m0_
     args.m, args.n, args.num_groups = m, n, 1
     args.accumulate = 1 if is_cd_same else 0
     args.bias = c.data_ptr() if with_bias else None
-    _launch(args, _stream(d))
+    _launch(args, d)
 
 
 def _pad_k(t: torch.Tensor, k: int) -> torch.Tensor:
@@ -307,7 +335,7 @@ def _grouped_contiguous(a, sfa, b, sfb, d, grouped_layout, recipe, recipe_a, rec
     args.batch_stride_b = b_k.stride(0)
     args.grouped_layout = grouped_layout.data_ptr()
     args.m, args.n, args.num_groups = m, n, g
-    _launch(args, _stream(d))
+    _launch(args, d)
 
 
 def _make_m_grouped_fp8_fp4(trans_b: bool):
@@ -380,7 +408,7 @@ def _masked(a, sfa, b, sfb, d, masked_m, recipe, recipe_a, recipe_b, disable_ue8
     args.batch_stride_a, args.batch_stride_b, args.batch_stride_d = a_k.stride(0), b_k.stride(0), d.stride(0)
     args.grouped_layout = masked_m.data_ptr()
     args.m, args.n, args.num_groups = m, n, g
-    _launch(args, _stream(d))
+    _launch(args, d)
 
 
 def m_grouped_fp8_fp4_gemm_nt_masked(a, b, d, masked_m: torch.Tensor, expected_m: int, recipe=None,

@@ -77,6 +77,10 @@ typedef struct dg_gemm_args {
     int32_t alignment;            /* MGROUPED_* row alignment (128 or 256)                   */
     int32_t block_m, block_n;     /* 0 = library heuristic                                    */
     int32_t num_cus;              /* 0 = all CUs of the device (set_num_sms)                 */
+    int32_t split_k;              /* K split: 0 = library heuristic, 1 = off, > 1 = forced   */
+                                  /* (dense / batched GEMMs with a workspace only)           */
+    void *workspace;              /* device scratch for split-K, or NULL (no split)          */
+    int64_t workspace_bytes;      /* its size; see dg_gemm_workspace_size()                  */
 } dg_gemm_args;
 
 /* Launch one GEMM.  Entry point replacing deep_gemm::launch_fp8_gemm /
@@ -107,6 +111,16 @@ int dg_transform_sf(const void *src, int32_t src_kind, int64_t stride_b, int64_t
 
 /* Number of compute units of `device` (the reference's get_num_sms, csrc/apis/runtime.hpp:13-19). */
 int dg_device_num_cus(int32_t device);
+
+/*
+ * Workspace dg_gemm() can use for `args` (0 when its plan does not split K).  The workspace is
+ * device memory that must be zero-filled before its first use; every dg_gemm() call leaves it
+ * zero-filled again, so one workspace serves any number of calls issued in order on one stream
+ * (calls in flight at the same time need separate workspaces).  With a smaller workspace, or
+ * none, dg_gemm() runs an unsplit plan.  Has no counterpart in the reference, whose kernels do
+ * not split K; callers that cannot provide scratch simply pass NULL.
+ */
+int dg_gemm_workspace_size(const dg_gemm_args *args, int64_t *bytes);
 
 /* Tile shape dg_gemm() would pick for `args` (block_m, block_n written to the pointers). */
 int dg_select_config(const dg_gemm_args *args, int32_t *block_m, int32_t *block_n);
