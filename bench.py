@@ -22,6 +22,9 @@ sys.path.insert(0, ROOT)
 
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense FP8 MFMA (published)
 PEAK_HBM_GBS = 8000.0
+# The reference's published figure for this exact metric and shape (Ascend 950DT, README.md:132
+# of the reference): 838 TFLOP/s.
+REFERENCE_TFLOPS = 838.0
 M, N, K = 4096, 7168, 2048
 TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'fp8_gemm_nt_4096x7168x2048_traffic.json')
 
@@ -158,7 +161,8 @@ def main():
     out = {
         'metric': 'FP8 block-scaled GEMM TFLOPS @ M=4096,N=7168,K=2048 bf16-out; % FP8 MFMA peak',
         'value': round(tflops, 2), 'unit': 'TFLOP/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
-        'ms_per_step': round(ms_per_step, 5), 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+        'ms_per_step': round(ms_per_step, 5), 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': round(tflops / REFERENCE_TFLOPS, 3),
+        'vs_baseline_ref': 'reference published 838 TFLOP/s at this shape on Ascend 950DT',
         'dtype': 'fp8_e4m3 (UE8M0 block scales, fp32 accumulate, bf16 out)', 'data': 'synthetic',
         'config': {'workload': f'fp8_gemm_nt M={m} N={n} K={k} bf16-out, A 1x128 / B 128x128 UE8M0 scales '
                                f'(seeded N(0,1)), SF pre-transformed', 'm': m, 'n': n, 'k': k,
