@@ -16,7 +16,7 @@ typedef __attribute__((address_space(3))) void lds_void;
 // Operand format pair (A x B).  Values match DG_KIND_* in include/deep_gemm_amd.h.
 enum Kind : int { kFP8FP8 = 0, kFP8FP4 = 1, kFP4FP4 = 2, kBF16 = 3 };
 // Work decomposition.  Values match DG_GEMM_* in include/deep_gemm_amd.h.
-enum GemmType : int { kNormal = 0, kBatched = 1, kMGroupedPsum = 2, kMGroupedIdx = 3, kMasked = 4 };
+enum GemmType : int { kNormal = 0, kBatched = 1, kMGroupedPsum = 2, kMGroupedIdx = 3, kMasked = 4, kKGrouped = 5 };
 
 // MFMA operand-format codes of v_mfma_scale_f32_16x16x128_f8f6f4 (cbsz / blgp).
 constexpr int kFmtE4M3 = 0;

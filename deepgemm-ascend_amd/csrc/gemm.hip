@@ -88,7 +88,7 @@ int k_stage_elems(int kind) { return kind == kBF16 ? 32 : 64; }
 bool split_capable(const dg_gemm_args& a) { return a.gemm_type == kNormal || a.gemm_type == kBatched; }
 
 int64_t plan_tiles(const dg_gemm_args& a, const TileCfg& t) {
-    const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
+    const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
     return (int64_t)ceil_div(a.m, t.bm) * ceil_div(a.n, t.bn) * groups;
 }
 
@@ -139,8 +139,10 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     Plan skinny;
     if (skinny_plan(a, cus, allow_split, skinny)) return skinny;
     allow_split = false;   // wide problems fill the CUs with tiles
-    const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
-    const int ns = ceil_div(a.k, k_stage_elems(a.kind));
+    const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
+    // (K-grouped: each tile contracts one group's share of K)
+    const int k_tile = a.gemm_type == kKGrouped ? ceil_div(a.k, std::max(1, a.num_groups)) : a.k;
+    const int ns = ceil_div(k_tile, k_stage_elems(a.kind));
     // HBM floor: operands once, D once (8 TB/s at ~2.1 GHz is ~3800 bytes per cycle).
     const double esz = a.kind == kBF16 ? 2.0 : 1.0;
     // (The plan must not depend on D's dtype: a bf16 D is then exactly the RNE rounding of the
@@ -271,7 +273,7 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     if (args == nullptr) return dg_set_error("dg_gemm: null args");
     const dg_gemm_args& a = *args;
     if (a.kind < kFP8FP8 || a.kind > kBF16) return dg_set_error("dg_gemm: unknown kind");
-    if (a.gemm_type < kNormal || a.gemm_type > kMasked) return dg_set_error("dg_gemm: unknown gemm_type");
+    if (a.gemm_type < kNormal || a.gemm_type > kKGrouped) return dg_set_error("dg_gemm: unknown gemm_type");
     if (a.m < 0 || a.n < 0 || a.k < 0) return dg_set_error("dg_gemm: negative size");
     if (a.d_dtype != DG_DTYPE_BF16 && a.d_dtype != DG_DTYPE_F32) return dg_set_error("dg_gemm: D must be bf16 or fp32");
     if (a.m == 0 || a.n == 0) return DG_OK;
@@ -279,12 +281,15 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     if (a.a == nullptr || a.b == nullptr || a.d == nullptr) return dg_set_error("dg_gemm: null operand");
     if (!bf16 && (a.sfa == nullptr || a.sfb == nullptr)) return dg_set_error("dg_gemm: scale factors required");
     const bool grouped = a.gemm_type != kNormal;
-    if ((a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx || a.gemm_type == kMasked) &&
+    if ((a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx || a.gemm_type == kMasked ||
+         a.gemm_type == kKGrouped) &&
         a.grouped_layout == nullptr)
         return dg_set_error("dg_gemm: grouped_layout required");
     if (grouped && a.num_groups < 1) return dg_set_error("dg_gemm: num_groups must be >= 1");
-    if (grouped && a.accumulate && a.gemm_type != kBatched)
+    if (grouped && a.accumulate && a.gemm_type != kBatched && a.gemm_type != kKGrouped)
         return dg_set_error("dg_gemm: grouped GEMMs do not accumulate");
+    if (a.gemm_type == kKGrouped && (a.alignment < 64 || a.alignment % 64 != 0))
+        return dg_set_error("dg_gemm: K-grouped alignment must be a multiple of 64");
     // storage bytes of one K row
     const int64_t kbytes_a = (int64_t)a.k * elem_bytes_times2(a.kind, true) / 2;
     const int64_t kbytes_b = (int64_t)a.k * elem_bytes_times2(a.kind, false) / 2;
@@ -348,7 +353,7 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     p.num_n_blocks = ceil_div(a.n, cfg.bn);
     p.kbytes_a = (int)kbytes_a; p.kbytes_b = (int)kbytes_b;
     p.group_m = 4;
-    const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
+    const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
     const int64_t tiles = (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
     if (tiles <= 0) return DG_OK;
     // split-K grids are padded to whole groups of 8 tiles (one per XCD)

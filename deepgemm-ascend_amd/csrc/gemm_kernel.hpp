@@ -194,7 +194,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     }
     const int tile_id = t;
     int batch = 0;
-    if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
+    if (p.gemm_type == kBatched || p.gemm_type == kMasked || p.gemm_type == kKGrouped) {
         batch = t / (nm * nn);
         t -= batch * nm * nn;
     }
@@ -212,6 +212,21 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     int group = 0;          // B operand group
     int valid_end = M;      // rows >= valid_end are padding (psum) / not written (masked)
     bool zero_tile = false;
+    int k_len = p.k;        // K extent of this tile's contraction
+
+    if (p.gemm_type == kKGrouped) {
+        // K-grouped: group g contracts K rows [align(psum[g-1]), psum[g]) of A and B into D[g].
+        const int ks = batch == 0 ? 0 : align_up(p.layout[batch - 1], p.alignment);
+        k_len = __builtin_amdgcn_readfirstlane(max(0, p.layout[batch] - ks));
+        const int kso = __builtin_amdgcn_readfirstlane(ks);
+        a_base += (int64_t)kso * (kAFp4 ? 1 : (kBf16 ? 4 : 2)) / 2;
+        b_base += (int64_t)kso * (kBFp4 ? 1 : (kBf16 ? 4 : 2)) / 2;
+        if (!kBf16) {
+            sfa += (int64_t)(kso / 64) * p.sfa_ld;
+            sfb += (int64_t)(kso / 64) * p.sfb_ld;
+        }
+        d_base += (int64_t)batch * p.bsd * out_esize;
+    }
 
     if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
         group = batch;
@@ -256,7 +271,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
         }
         return;
     }
-    if (p.gemm_type != kNormal) {
+    if (p.gemm_type != kNormal && p.gemm_type != kKGrouped) {
         b_base += (int64_t)group * p.bsb;
         if (!kBf16) sfb += (int64_t)group * p.sfb_bs;
     }
@@ -266,16 +281,17 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     const int64_t lda = p.lda, ldb = p.ldb;
     const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(a_base + (int64_t)m0 * lda, (int64_t)rows_a * lda);
     const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(b_base + (int64_t)n0 * ldb, (int64_t)rows_b * ldb);
-    const int kbytes_a = p.kbytes_a, kbytes_b = p.kbytes_b;
+    const int kbytes_a = p.gemm_type == kKGrouped ? k_len * (kAFp4 ? 1 : (kBf16 ? 4 : 2)) / 2 : p.kbytes_a;
+    const int kbytes_b = p.gemm_type == kKGrouped ? k_len * (kBFp4 ? 1 : (kBf16 ? 4 : 2)) / 2 : p.kbytes_b;
     // The ring walks an even number of virtual stages so the main loop is a pair of iterations
     // with static register sets; an odd stage count gets one leading dead stage (all-zero
     // operands and scales, so it adds nothing to the accumulators).
     // K stages of this workgroup: [c0, c0 + num_stages) of the whole K loop.
     const int c0 = split * p.split_stages;
-    const int num_stages = p.split_k > 1 ? min(p.split_stages, ceil_div(p.k, KS) - c0) : ceil_div(p.k, KS);
+    const int num_stages = p.split_k > 1 ? min(p.split_stages, ceil_div(k_len, KS) - c0) : ceil_div(k_len, KS);
     const int shift = num_stages & 1;
     const int num_virtual = num_stages + shift;
-    const int nk64 = ceil_div(p.k, 64);
+    const int nk64 = ceil_div(k_len, 64);
 
     // ------------------------------------------------------------------ loads
     // Operand rows: each wave-level buffer_load_dwordx4 ... lds fills 1 KB (64 lanes x 16 B)

@@ -26,9 +26,11 @@ struct SfParams {
     int* err;
 };
 
-// Is SF row `i` (rows [i*gran, (i+1)*gran) of the operand) padding of an M-grouped layout?
-__device__ __forceinline__ bool sf_row_is_padding(const SfParams& p, int i) {
-    const int row = i * p.gran_mn;
+// Is SF index `i` (operand rows / K columns [i*gran, (i+1)*gran)) inside the padding of a psum
+// layout, i.e. in [ceil(psum[g] / gran), align(psum[g], alignment) / gran) for the group g whose
+// aligned end is the first beyond i*gran?  The M-grouped layout pads MN rows, the K-grouped one K.
+__device__ __forceinline__ bool psum_is_padding(const SfParams& p, int i, int gran) {
+    const int row = i * gran;
     int lo = 0, hi = p.num_groups;   // first g with align(psum[g]) > row
     while (lo < hi) {
         const int mid = (lo + hi) >> 1;
@@ -36,10 +38,12 @@ __device__ __forceinline__ bool sf_row_is_padding(const SfParams& p, int i) {
         else lo = mid + 1;
     }
     if (lo == p.num_groups) return false;   // beyond the last group: untouched
-    return i >= ceil_div(p.psum[lo], p.gran_mn);
+    return i >= ceil_div(p.psum[lo], gran);
 }
 
-template <bool kFloat>
+// kKGrouped: the psum layout splits K (csrc/apis/layout.hpp:94-111): SF of the K padding between
+// groups (fp32 per gran_k column, packed int16 per 64-wide column) becomes 0 and is not validated.
+template <bool kFloat, bool kKGrouped>
 __global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
     const int64_t per_batch = (int64_t)p.k64 * p.ld;
     const int64_t total = per_batch * p.num_batches;
@@ -50,7 +54,8 @@ __global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
         const int mn = (int)(rem - (int64_t)k64 * p.ld);
         const int i = mn / p.gran_mn;
         uint16_t out = 0;
-        if (mn < p.mn && i < p.sf_mn && !(p.psum != nullptr && sf_row_is_padding(p, i))) {
+        const bool mn_pad = !kKGrouped && p.psum != nullptr && psum_is_padding(p, i, p.gran_mn);
+        if (mn < p.mn && i < p.sf_mn && !mn_pad) {
             const int64_t row_off = (int64_t)b * p.stride_b + (int64_t)i * p.stride_mn;
             if constexpr (kFloat) {
                 const uint32_t* s = reinterpret_cast<const uint32_t*>(p.src);
@@ -60,7 +65,7 @@ __global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
                     const int blk = 2 * k64 + h;                       // 32-wide K block
                     if (blk < p.k32) {
                         const int j = p.gran_k == 128 ? blk >> 2 : blk;
-                        if (j < p.sf_k) {
+                        if (j < p.sf_k && !(kKGrouped && psum_is_padding(p, j, p.gran_k))) {
                             const uint32_t bits = s[row_off + (int64_t)j * p.stride_k];
                             if ((bits & 0x807fffffu) != 0 && p.err != nullptr) *p.err = 1;
                             bytes[h] = (bits >> 23) & 0xffu;
@@ -70,7 +75,8 @@ __global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
                 out = (uint16_t)(bytes[0] | (bytes[1] << 8));
             } else {
                 const uint16_t* s = reinterpret_cast<const uint16_t*>(p.src);
-                if (k64 < p.sf_k) out = s[row_off + (int64_t)k64 * p.stride_k];
+                if (k64 < p.sf_k && !(kKGrouped && psum_is_padding(p, k64, 64)))
+                    out = s[row_off + (int64_t)k64 * p.stride_k];
             }
         }
         p.dst[(int64_t)b * p.dst_stride_b + (int64_t)k64 * p.ld + mn] = (int16_t)out;
@@ -81,11 +87,11 @@ __global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
 
 extern "C" __attribute__((visibility("hidden"))) int dg_set_error(const char* msg);
 
-extern "C" int dg_transform_sf(const void* src, int32_t src_kind, int64_t stride_b, int64_t stride_mn,
-                               int64_t stride_k, int32_t num_batches, int32_t sf_mn, int32_t sf_k,
-                               int32_t mn, int32_t k, int32_t gran_mn, int32_t gran_k,
-                               const int32_t* psum, int32_t num_groups, int32_t alignment,
-                               int16_t* dst, int64_t dst_stride_b, int32_t* err_flag, void* stream) {
+static int transform_sf_impl(bool k_grouped, const void* src, int32_t src_kind, int64_t stride_b, int64_t stride_mn,
+                             int64_t stride_k, int32_t num_batches, int32_t sf_mn, int32_t sf_k,
+                             int32_t mn, int32_t k, int32_t gran_mn, int32_t gran_k,
+                             const int32_t* psum, int32_t num_groups, int32_t alignment,
+                             int16_t* dst, int64_t dst_stride_b, int32_t* err_flag, void* stream) {
     using namespace dg;
     if (src == nullptr || dst == nullptr) return dg_set_error("dg_transform_sf: null pointer");
     if (num_batches < 1 || mn < 0 || k < 0 || sf_mn < 0 || sf_k < 0)
@@ -104,8 +110,10 @@ extern "C" int dg_transform_sf(const void* src, int32_t src_kind, int64_t stride
     if (sf_mn != ceil_div(mn, gran_mn)) return dg_set_error("dg_transform_sf: sf_mn != ceil(MN / gran_mn)");
     if (num_batches > 1 && dst_stride_b < (int64_t)ceil_div(k, 64) * align_up(mn, 2))
         return dg_set_error("dg_transform_sf: dst batch stride smaller than ceil(K / 64) * align(MN, 2)");
-    if (psum != nullptr && (num_groups < 1 || alignment < 1 || alignment % gran_mn != 0))
+    if (!k_grouped && psum != nullptr && (num_groups < 1 || alignment < 1 || alignment % gran_mn != 0))
         return dg_set_error("dg_transform_sf: psum needs num_groups >= 1 and alignment % gran_mn == 0");
+    if (k_grouped && (psum == nullptr || num_groups < 1 || num_batches != 1 || alignment < 64 || alignment % 64 != 0))
+        return dg_set_error("dg_transform_k_grouped_sf: needs a psum layout, one batch and alignment % 64 == 0");
     SfParams p;
     p.src = reinterpret_cast<const uint8_t*>(src);
     p.stride_b = stride_b; p.stride_mn = stride_mn; p.stride_k = stride_k;
@@ -118,14 +126,38 @@ extern "C" int dg_transform_sf(const void* src, int32_t src_kind, int64_t stride
     int64_t blocks = ceil_div64(total, 256);
     if (blocks > 8192) blocks = 8192;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (src_kind == DG_SF_F32)
-        hipLaunchKernelGGL(transform_sf_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, p);
-    else
-        hipLaunchKernelGGL(transform_sf_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, p);
+    if (k_grouped) {
+        if (src_kind == DG_SF_F32)
+            hipLaunchKernelGGL((transform_sf_kernel<true, true>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+        else
+            hipLaunchKernelGGL((transform_sf_kernel<false, true>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+    } else {
+        if (src_kind == DG_SF_F32)
+            hipLaunchKernelGGL((transform_sf_kernel<true, false>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+        else
+            hipLaunchKernelGGL((transform_sf_kernel<false, false>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         dg_set_error(hipGetErrorString(e));
         return DG_ELAUNCH;
     }
     return DG_OK;
+}
+
+extern "C" int dg_transform_sf(const void* src, int32_t src_kind, int64_t stride_b, int64_t stride_mn,
+                               int64_t stride_k, int32_t num_batches, int32_t sf_mn, int32_t sf_k,
+                               int32_t mn, int32_t k, int32_t gran_mn, int32_t gran_k,
+                               const int32_t* psum, int32_t num_groups, int32_t alignment,
+                               int16_t* dst, int64_t dst_stride_b, int32_t* err_flag, void* stream) {
+    return transform_sf_impl(false, src, src_kind, stride_b, stride_mn, stride_k, num_batches, sf_mn, sf_k, mn, k,
+                             gran_mn, gran_k, psum, num_groups, alignment, dst, dst_stride_b, err_flag, stream);
+}
+
+extern "C" int dg_transform_k_grouped_sf(const void* src, int32_t src_kind, int64_t stride_mn, int64_t stride_k,
+                                         int32_t sf_mn, int32_t sf_k, int32_t mn, int32_t k, int32_t gran_mn,
+                                         int32_t gran_k, const int32_t* psum, int32_t num_groups, int32_t alignment,
+                                         int16_t* dst, int32_t* err_flag, void* stream) {
+    return transform_sf_impl(true, src, src_kind, 0, stride_mn, stride_k, 1, sf_mn, sf_k, mn, k, gran_mn, gran_k,
+                             psum, num_groups, alignment, dst, 0, err_flag, stream);
 }

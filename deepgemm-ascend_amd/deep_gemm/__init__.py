@@ -23,7 +23,8 @@ from .runtime import (  # noqa: E402
     use_deterministic_algorithms, get_deterministic_algorithms,
     set_dry_run, get_dry_run, init,
 )
-from .layout import transform_sf_into_required_layout, get_recipe  # noqa: E402
+from .layout import (transform_sf_into_required_layout, transform_k_grouped_sf_into_required_layout,  # noqa: E402
+                     get_recipe)
 from .gemm import (  # noqa: E402
     fp8_fp4_gemm_nt, fp8_fp4_gemm_nn, fp8_fp4_gemm_tn, fp8_fp4_gemm_tt,
     m_grouped_fp8_fp4_gemm_nt_contiguous, m_grouped_fp8_fp4_gemm_nn_contiguous,
@@ -31,8 +32,10 @@ from .gemm import (  # noqa: E402
     bf16_gemm_nt, bf16_gemm_nn, bf16_gemm_tn, bf16_gemm_tt,
     m_grouped_bf16_gemm_nt_contiguous, m_grouped_bf16_gemm_nn_contiguous,
     m_grouped_bf16_gemm_nt_masked,
+    k_grouped_fp8_gemm_tn_contiguous, k_grouped_fp8_gemm_nt_contiguous, k_grouped_bf16_gemm_tn_contiguous,
     select_config,
 )
+from .einsum import fp8_bmm, bf16_bmm, einsum, fp8_einsum  # noqa: E402
 from . import epilogue  # noqa: E402
 
 # FP8 aliases are the same objects as the FP8/FP4 entry points (csrc/apis/gemm.hpp:624-629)

@@ -14,12 +14,12 @@ _lock = threading.Lock()
 _lib = None
 
 DG_KIND_FP8_FP8, DG_KIND_FP8_FP4, DG_KIND_FP4_FP4, DG_KIND_BF16 = 0, 1, 2, 3
-DG_GEMM_NORMAL, DG_GEMM_BATCHED, DG_GEMM_MGROUPED_PSUM, DG_GEMM_MGROUPED_IDX, DG_GEMM_MASKED = 0, 1, 2, 3, 4
+DG_GEMM_NORMAL, DG_GEMM_BATCHED, DG_GEMM_MGROUPED_PSUM, DG_GEMM_MGROUPED_IDX, DG_GEMM_MASKED, DG_GEMM_KGROUPED = 0, 1, 2, 3, 4, 5
 DG_DTYPE_BF16, DG_DTYPE_F32 = 0, 1
 DG_SF_F32, DG_SF_I16 = 0, 1
 
 # Every symbol include/deep_gemm_amd.h declares.
-EXPORTED_SYMBOLS = ('dg_gemm', 'dg_transform_sf', 'dg_device_num_cus', 'dg_select_config',
+EXPORTED_SYMBOLS = ('dg_gemm', 'dg_transform_sf', 'dg_transform_k_grouped_sf', 'dg_device_num_cus', 'dg_select_config',
                     'dg_gemm_workspace_size', 'dg_last_error', 'dg_version')
 
 
@@ -70,6 +70,12 @@ def load(path=None) -> ctypes.CDLL:
             ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
             ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
         lib.dg_transform_sf.restype = ctypes.c_int
+        lib.dg_transform_k_grouped_sf.argtypes = [
+            ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64,
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+            ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        lib.dg_transform_k_grouped_sf.restype = ctypes.c_int
         lib.dg_device_num_cus.argtypes = [ctypes.c_int32]
         lib.dg_device_num_cus.restype = ctypes.c_int
         lib.dg_select_config.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(ctypes.c_int32),

@@ -19,7 +19,8 @@ import torch
 
 from . import _lib
 from . import epilogue as _epi
-from .layout import transform_sf_into_required_layout, get_recipe, operand_recipes, _assert
+from .layout import (transform_sf_into_required_layout, transform_k_grouped_sf_into_required_layout, get_recipe,
+                     operand_recipes, _assert)
 from .runtime import get_num_sms, get_mk_alignment_for_contiguous_layout, get_dry_run
 
 PACKED_FP4 = torch.int8   # the reference's kPackedFP4 (csrc/utils/dtype.hpp:9)
@@ -421,6 +422,151 @@ def m_grouped_fp8_fp4_gemm_nt_masked(a, b, d, masked_m: torch.Tensor, expected_m
 def m_grouped_bf16_gemm_nt_masked(a, b, d, masked_m: torch.Tensor, expected_m: int,
                                   compiled_dims: str = 'nk') -> None:
     _masked(a, None, b, None, d, masked_m, None, None, None, False, bf16=True)
+
+
+def _batched(a, sfa, b, sfb, d, c, recipe, bf16: bool):
+    """Batched GEMM D[i] = A[i] @ B[i]^T (+ C[i]): fp8_bmm / bf16_bmm (csrc/apis/einsum.hpp:37-97),
+    get_gemm_desc with GemmType::Batched (csrc/apis/gemm.hpp:60-197)."""
+    if bf16:
+        _assert(a.dtype == torch.bfloat16)
+        _assert(b.dtype == torch.bfloat16)
+    else:
+        _assert(a.dtype == torch.float8_e4m3fn)
+        _assert(b.dtype == torch.float8_e4m3fn)
+    _assert(d.dtype in (torch.bfloat16, torch.float32))
+    _assert(a.dim() == 3 and b.dim() == 3 and d.dim() == 3, 'batched GEMM takes A [B,M,K], B [B,N,K], D [B,M,N]')
+    _assert(a.stride(-1) == 1 or a.stride(-2) == 1)
+    _assert(b.stride(-1) == 1 or b.stride(-2) == 1)
+    _assert(d.stride(-1) == 1)
+    ka, kb = _major_is_k(a), _major_is_k(b)
+    bs, m, k = a.size(0), _logical_mn(a, ka), _logical_k(a, ka)
+    n, k_b = _logical_mn(b, kb), _logical_k(b, kb)
+    if k != k_b:
+        raise RuntimeError(f"Conflicting shape dimension 'k': A gives {k}, B gives {k_b}")
+    _assert(b.size(0) == bs and d.size(0) == bs and d.size(1) == m and d.size(2) == n,
+            f'D shape {tuple(d.shape)} != ({bs}, {m}, {n})')
+    if bs == 0:
+        return
+    is_cd_same = c is not None and c.data_ptr() == d.data_ptr() and d.numel() > 0
+    if c is not None:
+        _assert(c.shape == d.shape and c.dtype == d.dtype and c.stride(-1) == 1)
+    if _early_return(m, n, k, d, c, is_cd_same, False):
+        return
+    args = _lib.GemmArgs()
+    if bf16:
+        kind = _lib.DG_KIND_BF16
+    else:
+        kind = _lib.DG_KIND_FP8_FP8
+        ra, rb = operand_recipes(recipe, None, None)
+        sfa_t = transform_sf_into_required_layout(sfa, m, k, ra, bs, True)
+        sfb_t = transform_sf_into_required_layout(sfb, n, k, rb, bs, False)
+        if sfa_t.dim() == 2:
+            sfa_t = sfa_t.unsqueeze(0)
+        if sfb_t.dim() == 2:
+            sfb_t = sfb_t.unsqueeze(0)
+        args.sfa, args.sfb = sfa_t.data_ptr(), sfb_t.data_ptr()
+        args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
+        args.sfa_batch_stride, args.sfb_batch_stride = sfa_t.stride(0), sfb_t.stride(0)
+    if c is not None and not is_cd_same:
+        d.copy_(c)   # the reference's legacy accumulation path (csrc/utils/layout.hpp:82-84)
+    a_k = _to_kernel_operand(a, k)
+    b_k = _to_kernel_operand(b, k)
+    k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
+    a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
+    _fill_common(args, d, k_kernel, None, kind)
+    args.gemm_type = _lib.DG_GEMM_BATCHED
+    args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
+    args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
+    args.batch_stride_a, args.batch_stride_b, args.batch_stride_d = a_k.stride(0), b_k.stride(0), d.stride(0)
+    args.m, args.n, args.num_groups = m, n, bs
+    args.accumulate = 1 if c is not None else 0
+    _launch(args, d)
+
+
+def _k_grouped(a, sfa, b, sfb, d, grouped_layout, c, recipe, use_psum_layout, epilogue, bf16: bool):
+    """K-grouped contiguous GEMM, D[g] = A[Kg]^T @ B[Kg] (+ C[g]) with A [Ktot, M], B [Ktot, N]
+    (the `tn` layout) and K split by a psum layout: k_grouped_fp8_gemm_tn_contiguous
+    (csrc/apis/gemm.hpp:351-387) and k_grouped_bf16_gemm_tn_contiguous (:515-...)."""
+    _assert(use_psum_layout, 'use_psum_layout must be true')
+    # [K, M] -> logical [M, K] (a view; the data stays MN-major)
+    a_t, b_t = a.transpose(0, 1), b.transpose(0, 1)
+    if bf16:
+        _assert(a.dtype == torch.bfloat16)
+        _assert(b.dtype == torch.bfloat16)
+    else:
+        _assert(a.dtype == torch.float8_e4m3fn or _is_fp4(a))
+        _assert(b.dtype == torch.float8_e4m3fn or _is_fp4(b))
+    _assert(d.dtype in (torch.bfloat16, torch.float32))
+    epi = _epi.resolve(epilogue, None, d)
+    _assert(isinstance(epi, _epi.Identity), 'K-grouped GEMMs only support the identity epilogue')
+    _assert(grouped_layout.is_contiguous() and grouped_layout.dtype == torch.int32 and grouped_layout.dim() == 1)
+    g = grouped_layout.numel()
+    ka, kb = _major_is_k(a_t), _major_is_k(b_t)
+    _assert(not ka and not kb, 'K-grouped operands must be MN-major ([K, M] / [K, N] contiguous along MN)')
+    m, k = _logical_mn(a_t, ka), _logical_k(a_t, ka)
+    n, k_b = _logical_mn(b_t, kb), _logical_k(b_t, kb)
+    if k != k_b:
+        raise RuntimeError(f"Conflicting shape dimension 'k': A gives {k}, B gives {k_b}")
+    _assert(d.dim() == 3 and d.size(0) == g and d.size(1) == m and d.size(2) == n and d.stride(-1) == 1,
+            f'D must be [{g}, {m}, {n}]')
+    is_cd_same = c is not None and c.data_ptr() == d.data_ptr() and d.numel() > 0
+    if c is not None:
+        _assert(c.shape == d.shape and c.dtype == d.dtype and c.stride(-1) == 1)
+    if _early_return(m, n, k, d, c, is_cd_same, False):
+        return
+    alignment = get_mk_alignment_for_contiguous_layout()
+    _assert(alignment % 64 == 0, 'K-grouped GEMMs need an mk alignment that is a multiple of 64')
+    args = _lib.GemmArgs()
+    if bf16:
+        kind = _lib.DG_KIND_BF16
+    else:
+        kind = _kind(a, b)
+        rcp = get_recipe(recipe, None, None)
+        sfa_t = transform_k_grouped_sf_into_required_layout(sfa.transpose(0, 1), m, k, rcp, True, grouped_layout)
+        sfb_t = transform_k_grouped_sf_into_required_layout(sfb.transpose(0, 1), n, k, rcp, False, grouped_layout)
+        args.sfa, args.sfb = sfa_t.data_ptr(), sfb_t.data_ptr()
+        args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
+    if c is not None and not is_cd_same:
+        d.copy_(c)
+    a_k = _to_kernel_operand(a_t, k)
+    b_k = _to_kernel_operand(b_t, k)
+    k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
+    a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
+    _fill_common(args, d, k_kernel, None, kind)
+    args.alignment = alignment
+    args.gemm_type = _lib.DG_GEMM_KGROUPED
+    args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
+    args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
+    args.batch_stride_d = d.stride(0)
+    args.grouped_layout = grouped_layout.data_ptr()
+    args.m, args.n, args.num_groups = m, n, g
+    args.accumulate = 1 if c is not None else 0
+    _launch(args, d)
+
+
+def k_grouped_fp8_gemm_tn_contiguous(a, b, d, ks_cpu, grouped_layout, c=None, recipe=(1, 1, 32),
+                                     compiled_dims: str = 'mn', use_psum_layout: bool = True, epilogue=None) -> None:
+    """K-grouped contiguous low-precision GEMM (csrc/apis/gemm.hpp:326-387): A [Ktot, M], B [Ktot, N], D [G, M, N].
+    ``ks_cpu`` is a hint only (the reference uses it for its cost model)."""
+    (a_, sfa), (b_, sfb) = a, b
+    _k_grouped(a_, sfa, b_, sfb, d, grouped_layout, c, recipe, use_psum_layout, epilogue, bf16=False)
+
+
+def k_grouped_fp8_gemm_nt_contiguous(a, b, d, ks_cpu, grouped_layout, c=None, recipe=(1, 1, 32),
+                                     compiled_dims: str = 'mn', use_psum_layout: bool = True, epilogue=None) -> None:
+    """Deprecated `nt` form (csrc/apis/gemm.hpp:389-411): A [M, Ktot], B [N, Ktot]."""
+    import warnings
+    warnings.warn('Calling k_grouped_fp8_gemm_nt_contiguous is deprecated, please transpose a, b into [k, m] and '
+                  '[k, n] shape and call `k_grouped_fp8_gemm_tn_contiguous` instead', DeprecationWarning, stacklevel=2)
+    (a_, sfa), (b_, sfb) = a, b
+    k_grouped_fp8_gemm_tn_contiguous((a_.transpose(0, 1), sfa.transpose(0, 1)), (b_.transpose(0, 1), sfb.transpose(0, 1)),
+                                     d, ks_cpu, grouped_layout, c, recipe, compiled_dims, use_psum_layout, epilogue)
+
+
+def k_grouped_bf16_gemm_tn_contiguous(a, b, d, ks_cpu, grouped_layout, c=None, compiled_dims: str = 'mn',
+                                      use_psum_layout: bool = True, epilogue=None) -> None:
+    """K-grouped contiguous bf16 GEMM (csrc/apis/gemm.hpp:515-...)."""
+    _k_grouped(a, None, b, None, d, grouped_layout, c, None, use_psum_layout, epilogue, bf16=True)
 
 
 def select_config(m: int, n: int, k: int, kind: int = _lib.DG_KIND_FP8_FP8, gemm_type: int = _lib.DG_GEMM_NORMAL,

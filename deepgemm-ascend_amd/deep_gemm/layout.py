@@ -119,6 +119,43 @@ def transform_sf_into_required_layout(sf: torch.Tensor, mn: int, k: int, recipe,
     return _launch_transform_sf(sf, mn, k, gran_mn, gran_k, psum_layout)
 
 
+def transform_k_grouped_sf_into_required_layout(sf: torch.Tensor, mn: int, k: int, recipe, is_sfa: Optional[bool],
+                                                psum_layout: torch.Tensor) -> torch.Tensor:
+    """Same contract as the reference (csrc/apis/layout.hpp:94-111): ``sf`` is [ceil(MN/gran_mn),
+    ceil(Ktot/gran_k)] (fp32) or [.., ceil(Ktot/64)] (packed int16) over the K axis that ``psum_layout``
+    splits into groups; the SF of the K padding between groups becomes 0 in the output."""
+    _assert(is_sfa is not None, 'is_sfa must be set')
+    gran_mn, gran_k = _split_recipe(recipe, is_sfa)
+    if check_sf_layout(sf, mn, k, gran_mn, gran_k, None):
+        return sf
+    _assert(1 <= gran_mn <= 128 and (gran_mn & (gran_mn - 1)) == 0,
+            'gran_mn only support a power of two in [1, 128]')
+    _assert(sf.is_cuda, 'SF must be a device tensor')
+    _assert(psum_layout.device == sf.device, 'grouped_layout must be on the same device as the SF input')
+    _assert(psum_layout.dtype == torch.int32 and psum_layout.dim() == 1 and psum_layout.is_contiguous(),
+            'grouped_layout must be a contiguous 1D int32 tensor')
+    num_groups = psum_layout.numel()
+    _assert(num_groups > 0, 'grouped_layout must contain at least one group')
+    alignment = get_mk_alignment_for_contiguous_layout()
+    sf_mn, sf_k = sf.shape
+    k64, ld = _ceil_div(k, 64), _align(mn, 2)
+    out = torch.empty((k64, ld), dtype=torch.int16, device=sf.device)[:, :mn].transpose(0, 1)
+    if out.numel() == 0 or get_dry_run_safe():
+        return out
+    check_err = os.environ.get('DG_CHECK_SF', '0') == '1' and sf.dtype == torch.float32
+    err = torch.zeros(1, dtype=torch.int32, device=sf.device) if check_err else None
+    lib = _lib.load()
+    rc = lib.dg_transform_k_grouped_sf(
+        sf.data_ptr(), _lib.DG_SF_F32 if sf.dtype == torch.float32 else _lib.DG_SF_I16,
+        sf.stride(0), sf.stride(1), sf_mn, sf_k, mn, k, gran_mn, gran_k,
+        psum_layout.data_ptr(), num_groups, alignment, out.data_ptr(),
+        err.data_ptr() if err is not None else None, torch.cuda.current_stream(sf.device).cuda_stream)
+    _lib.check(rc, lib)
+    if err is not None and int(err.item()) != 0:
+        raise RuntimeError('Invalid float32 SF: only the 8-bit exponent may be set (sign and mantissa must be 0)')
+    return out
+
+
 def operand_recipes(recipe=None, recipe_a=None, recipe_b=None):
     """((gran_m, gran_k_a), (gran_n, gran_k_b)) for the two operands.
 

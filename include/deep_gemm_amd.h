@@ -35,6 +35,11 @@ extern "C" {
                                     [align(psum[g-1], alignment), psum[g]) uses B[g]          */
 #define DG_GEMM_MGROUPED_IDX  3  /* grouped_layout = m_indices int32[M]; -1 marks padding rows */
 #define DG_GEMM_MASKED        4  /* A[G,M,K], D[G,M,N]; grouped_layout = masked_m int32[G]     */
+#define DG_GEMM_KGROUPED      5  /* A[M,Ktot], B[N,Ktot] (K-major), D[G,M,N]; grouped_layout =
+                                    psum int32[G] over K; group g contracts K
+                                    [align(psum[g-1], alignment), psum[g]) into D[g]
+                                    (k_grouped_fp8_gemm_tn_contiguous, csrc/apis/gemm.hpp:351-387);
+                                    alignment a multiple of 64; accumulate allowed              */
 
 #define DG_DTYPE_BF16 0
 #define DG_DTYPE_F32  1
@@ -108,6 +113,19 @@ int dg_transform_sf(const void *src, int32_t src_kind, int64_t stride_b, int64_t
                     int32_t mn, int32_t k, int32_t gran_mn, int32_t gran_k,
                     const int32_t *psum, int32_t num_groups, int32_t alignment,
                     int16_t *dst, int64_t dst_stride_b, int32_t *err_flag, void *stream);
+
+/*
+ * Scale-factor layout transform of a K-grouped operand.  Replaces launch_transform_sf with
+ * GemmType::KGroupedContiguousWithPsumLayout behind transform_k_grouped_sf_into_required_layout
+ * (csrc/apis/layout.hpp:94-111).  One batch, same src / dst layout as dg_transform_sf.
+ * psum (device int32[num_groups], required): K ranges of the groups; the SF of the K padding
+ *      between groups, columns [ceil(psum[g]/w), align(psum[g], alignment)/w) with w = gran_k
+ *      (DG_SF_F32) or 64 (DG_SF_I16), becomes 0 and is never validated.  alignment % 64 == 0.
+ */
+int dg_transform_k_grouped_sf(const void *src, int32_t src_kind, int64_t stride_mn, int64_t stride_k,
+                              int32_t sf_mn, int32_t sf_k, int32_t mn, int32_t k, int32_t gran_mn,
+                              int32_t gran_k, const int32_t *psum, int32_t num_groups, int32_t alignment,
+                              int16_t *dst, int32_t *err_flag, void *stream);
 
 /* Number of compute units of `device` (the reference's get_num_sms, csrc/apis/runtime.hpp:13-19). */
 int dg_device_num_cus(int32_t device);

@@ -11,6 +11,12 @@ The reference's own reference path: dequantise each operand per block to fp32 (c
 * ``gemm_nt``                 -- D = alpha * A @ B^T (+ bias | + C), fp32 math.
 * ``m_grouped_contiguous``   -- psum layout (group g rows [align(psum[g-1]), psum[g]) use
   B[g], padding rows are 0) or m_indices layout (row r uses B[idx[r]], -1 rows are 0).
+* ``batched_nt``              -- D[i] = A[i] @ B[i]^T (+ C[i]) per batch (tests/generators.py:392-419).
+* ``k_grouped_tn``            -- D[g] = A[Kg]^T @ B[Kg] (+ C[g]) over the K ranges
+  Kg = [align(psum[g-1]), psum[g]) of A [Ktot, M] / B [Ktot, N]; an empty group gives 0 (+ C)
+  (tests/generators.py:361-390).
+* ``einsum_ref``              -- the three fixed expressions of csrc/apis/einsum.hpp:99-199 as
+  torch.einsum in fp32 (a library routine, independent of the permutations the API uses).
 * ``m_grouped_masked``        -- D[g, :masked_m[g]] = A[g, :masked_m[g]] @ B[g]^T; the rest
   is not compared (upstream DeepGEMM semantics; the reference has no masked kernel, so
   this function is "parity unpinned" with respect to the reference and pinned only by the
@@ -102,3 +108,36 @@ def brute_force_nt(a, b):
                 s += float(a[i, t]) * float(b[j, t])
             out[i, j] = s
     return out
+
+
+def batched_nt(a: torch.Tensor, b: torch.Tensor, c=None, out_dtype=torch.bfloat16) -> torch.Tensor:
+    """a [B,M,K] fp32, b [B,N,K] fp32 -> [B,M,N] (tests/generators.py:392-419)."""
+    d = torch.stack([a[i].float() @ b[i].float().T for i in range(a.size(0))]) if a.size(0) else \
+        torch.zeros(0, a.size(1), b.size(1))
+    if c is not None:
+        d = d + c.float()
+    return d.to(out_dtype)
+
+
+def k_grouped_tn(a: torch.Tensor, b: torch.Tensor, psum, alignment: int = 256, c=None,
+                 out_dtype=torch.bfloat16) -> torch.Tensor:
+    """a [Ktot,M] fp32, b [Ktot,N] fp32, psum list of G K-ends -> [G,M,N] (tests/generators.py:361-390)."""
+    g_ = len(psum)
+    d = torch.zeros(g_, a.size(1), b.size(1), dtype=torch.float32)
+    for g, sl in enumerate(psum_slices(list(psum), alignment)):
+        if sl.stop > sl.start:
+            d[g] = a[sl].float().T @ b[sl].float()
+    if c is not None:
+        d = d + c.float()
+    return d.to(out_dtype)
+
+
+EINSUM_EXPRS = ('bhr,hdr->bhd', 'bhd,hdr->bhr', 'bhd,bhr->hdr')
+
+
+def einsum_ref(expr: str, a: torch.Tensor, b: torch.Tensor, c=None, out_dtype=torch.bfloat16) -> torch.Tensor:
+    assert expr in EINSUM_EXPRS
+    d = torch.einsum(expr, a.double(), b.double())
+    if c is not None:
+        d = d + c.double()
+    return d.to(out_dtype)

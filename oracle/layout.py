@@ -6,6 +6,9 @@
   repeated ``gran_mn`` times and cropped to MN.  M-grouped psum padding rows are zeroed
   (``tests/test_layout.py:93-95``, ``deep_gemm/include/deep_gemm/transform_sf.hpp:586-593``).
   Extension: ``gran_k == 128`` fp32 input is first expanded to four identical per-32 scales.
+* ``transform_k_grouped_sf`` -- the same layout over a K axis split by a psum layout; the SF of
+  the K padding between groups (columns ``psum_pad_slices(psum, alignment, w)`` with w = gran_k
+  for fp32 and 64 for packed int16) becomes 0 (``tests/test_layout.py:96-98``).
 * ``psum_*`` / ``m_indices_*`` -- ``tests/generators.py:212-235`` (psum layout walk) and the
   m_indices convention (one int32 per row, -1 on padding rows).
 
@@ -85,6 +88,16 @@ def transform_sf(sf: torch.Tensor, mn: int, k: int, gran_mn: int, gran_k: int = 
         packed = sf
     out = packed.transpose(-2, -1).repeat_interleave(gran_mn, -1)[..., :mn]
     return out.contiguous().transpose(-2, -1)
+
+
+def transform_k_grouped_sf(sf: torch.Tensor, mn: int, k: int, gran_mn: int, psum, gran_k: int = 32,
+                           alignment: int = 256) -> torch.Tensor:
+    """``transform_k_grouped_sf_into_required_layout`` of an [ceil(MN/gran_mn), ceil(K/w)] SF."""
+    sf = sf.clone()
+    w = gran_k if sf.dtype == torch.float32 else 64
+    for span in psum_pad_slices(psum, alignment, w):
+        sf[..., span] = 0
+    return transform_sf(sf, mn, k, gran_mn, gran_k)
 
 
 def unpack_sf_bytes(packed: torch.Tensor, k: int) -> torch.Tensor:

@@ -141,3 +141,61 @@ def test_import_is_lazy_and_fork_safe():
             'assert not torch.cuda.is_initialized(); print("ok")')
     out = subprocess.run([sys.executable, '-c', code], capture_output=True, text=True, cwd=str(__import__('pathlib').Path(__file__).resolve().parents[1]))
     assert out.returncode == 0 and 'ok' in out.stdout, out.stderr
+
+
+def test_batched_and_k_grouped_signatures_match_reference():
+    """csrc/apis/einsum.hpp:201-220 and csrc/apis/gemm.hpp bindings."""
+    import inspect
+    assert list(inspect.signature(deep_gemm.fp8_bmm).parameters) == ['a', 'b', 'd', 'c', 'recipe', 'compiled_dims',
+                                                                      'epilogue']
+    assert inspect.signature(deep_gemm.fp8_bmm).parameters['recipe'].default == (1, 1, 32)
+    assert list(inspect.signature(deep_gemm.bf16_bmm).parameters) == ['a', 'b', 'd', 'c', 'compiled_dims', 'epilogue']
+    assert list(inspect.signature(deep_gemm.einsum).parameters) == ['expr', 'a', 'b', 'd', 'c', 'use_cublaslt',
+                                                                    'epilogue']
+    assert list(inspect.signature(deep_gemm.fp8_einsum).parameters) == ['expr', 'a', 'b', 'd', 'c', 'recipe',
+                                                                        'epilogue']
+    sig = inspect.signature(deep_gemm.k_grouped_fp8_gemm_tn_contiguous)
+    assert list(sig.parameters) == ['a', 'b', 'd', 'ks_cpu', 'grouped_layout', 'c', 'recipe', 'compiled_dims',
+                                    'use_psum_layout', 'epilogue']
+    assert list(inspect.signature(deep_gemm.transform_k_grouped_sf_into_required_layout).parameters) == \
+        ['sf', 'mn', 'k', 'recipe', 'is_sfa', 'psum_layout']
+
+
+def test_einsum_validation_on_host():
+    x = torch.empty(2, 2, 2, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match='Unsupported einsum expression'):
+        deep_gemm.einsum('bhd,hrd->bhr', x, x, x)
+    with pytest.raises(RuntimeError, match='use_cublaslt'):
+        deep_gemm.einsum('bhr,hdr->bhd', x, x, x, use_cublaslt=True)
+    with pytest.raises(RuntimeError, match='Unsupported einsum expression'):
+        deep_gemm.fp8_einsum('xyz', (x, x), (x, x), x)
+
+
+def test_bmm_shape_checks_and_empty_batch():
+    a, b = _fp8((2, 16, 64)), _fp8((3, 8, 64))
+    sf = torch.ones(2, 16, 2)
+    d = torch.empty(2, 16, 8, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        deep_gemm.fp8_bmm((a, sf), (b, torch.ones(3, 8, 2)), d)
+    # batch 0 returns before any device work
+    deep_gemm.bf16_bmm(torch.empty(0, 4, 8, dtype=torch.bfloat16), torch.empty(0, 4, 8, dtype=torch.bfloat16),
+                       torch.empty(0, 4, 4, dtype=torch.bfloat16))
+    # K == 0 zero-fills D on host tensors (csrc/utils/layout.hpp:54-86)
+    d0 = torch.full((2, 4, 3), 5.0, dtype=torch.bfloat16)
+    deep_gemm.bf16_bmm(torch.empty(2, 4, 0, dtype=torch.bfloat16), torch.empty(2, 3, 0, dtype=torch.bfloat16), d0)
+    assert int(d0.count_nonzero()) == 0
+
+
+def test_k_grouped_host_checks():
+    a, b = _fp8((512, 64)), _fp8((512, 32))     # [Ktot, M], [Ktot, N] MN-major
+    sfa, sfb = torch.ones(16, 64), torch.ones(16, 32)
+    d = torch.empty(2, 64, 32, dtype=torch.bfloat16)
+    layout = torch.tensor([256, 512], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match='use_psum_layout must be true'):
+        deep_gemm.k_grouped_fp8_gemm_tn_contiguous((a, sfa), (b, sfb), d, None, layout, use_psum_layout=False)
+    with pytest.raises(RuntimeError, match='MN-major'):
+        deep_gemm.k_grouped_fp8_gemm_tn_contiguous((a.t().contiguous().t(), sfa), (b, sfb), d, None, layout)
+    with pytest.raises(RuntimeError, match='D must be'):
+        deep_gemm.k_grouped_fp8_gemm_tn_contiguous((a, sfa), (b, sfb), d[:1], None, layout)
+    with pytest.warns(DeprecationWarning), pytest.raises(RuntimeError, match='D must be'):
+        deep_gemm.k_grouped_fp8_gemm_nt_contiguous((a.t(), sfa.t()), (b.t(), sfb.t()), d[:1], None, layout)

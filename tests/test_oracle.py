@@ -253,3 +253,75 @@ def test_masked_rows_beyond_count_are_zero():
     assert torch.equal(d[1], torch.zeros(10, 6))
     assert torch.equal(d[2, 4:], torch.zeros(6, 6))
     assert torch.allclose(d[2, :4], a[2, :4] @ b[2].T)
+
+
+def test_batched_matches_per_batch_brute_force():
+    g = torch.Generator().manual_seed(9)
+    a = torch.randn(3, 4, 12, generator=g)
+    b = torch.randn(3, 5, 12, generator=g)
+    c = torch.randn(3, 4, 5, generator=g)
+    d = og.batched_nt(a, b, c, torch.float32)
+    for i in range(3):
+        ref = og.brute_force_nt(a[i], b[i]) + c[i].double()
+        assert torch.allclose(d[i].double(), ref, rtol=1e-5, atol=1e-5)
+    assert og.batched_nt(a[:0], b[:0], None, torch.float32).shape == (0, 4, 5)
+
+
+def test_k_grouped_matches_brute_force_and_full_k():
+    """Each group is a K-slice contraction: brute force on the slices, and with one group of the
+    whole K it is the plain GEMM A^T B; empty groups give exactly C."""
+    g = torch.Generator().manual_seed(10)
+    total, ps = ol.psum_from_sizes([5, 0, 9], 8)
+    assert ps == [5, 8, 17] and total == 24
+    a = torch.randn(total, 3, generator=g)
+    b = torch.randn(total, 4, generator=g)
+    c = torch.randn(3, 3, 4, generator=g)
+    d = og.k_grouped_tn(a, b, ps, 8, c, torch.float32)
+    for gi, (lo, hi) in enumerate([(0, 5), (8, 8), (8, 17)]):
+        ref = c[gi].double()
+        if hi > lo:
+            ref = ref + og.brute_force_nt(a[lo:hi].T.contiguous(), b[lo:hi].T.contiguous())
+        assert torch.allclose(d[gi].double(), ref, rtol=1e-5, atol=1e-5)
+    assert torch.equal(d[1], c[1])
+    full = og.k_grouped_tn(a, b, [total], 8, None, torch.float32)
+    assert torch.allclose(full[0], a.T @ b, atol=1e-5)
+
+
+def test_k_grouped_transform_sf_zeroes_k_padding():
+    # K groups of 40 and 16 rows, alignment 64: fp32 columns (per 32) [2, 2) and [3, 4) ... pad
+    ps = [40, 80]
+    sf = torch.full((2, 4), 2.0)             # [MN=2, ceil(128/32)=4]
+    out = ol.transform_k_grouped_sf(sf, 2, 128, 1, ps, 32, 64)
+    # group 0 ends at 40: column 1 (32..63) still holds its K rows 32..39; group 1 ends at 80,
+    # so column 3 (96..127) is padding: bytes [128, 128 | 128, 0]
+    assert out.shape == (2, 2)
+    assert (out.view(torch.uint16).to(torch.int32)[:, 0] == (128 | (128 << 8))).all()
+    assert (out.view(torch.uint16).to(torch.int32)[:, 1] == 128).all()
+    # packed int16 input: padding per 64 columns
+    sf16 = torch.full((2, 3), 0x1234, dtype=torch.int16)   # ceil(192/64)
+    out16 = ol.transform_k_grouped_sf(sf16, 2, 192, 1, [40, 130], 32, 64)
+    assert out16[:, 0].tolist() == [0x1234] * 2 and out16[:, 1].tolist() == [0x1234] * 2
+    assert out16[:, 2].tolist() == [0x1234] * 2
+    out16 = ol.transform_k_grouped_sf(sf16, 2, 192, 1, [40, 192], 32, 128)
+    assert out16[:, 0].tolist() == [0x1234] * 2 and out16[:, 1].tolist() == [0, 0] and out16[:, 2].tolist() == [0x1234] * 2
+
+
+@pytest.mark.parametrize('expr', og.EINSUM_EXPRS)
+def test_einsum_ref_matches_loops(expr):
+    g = torch.Generator().manual_seed(11)
+    B, H, D, R = 3, 2, 4, 5
+    shapes = {'b': B, 'h': H, 'd': D, 'r': R}
+    ins, out = expr.split('->')
+    ta, tb = ins.split(',')
+    a = torch.randn([shapes[x] for x in ta], generator=g)
+    b = torch.randn([shapes[x] for x in tb], generator=g)
+    d = og.einsum_ref(expr, a, b, None, torch.float64)
+    contracted = (set(ta) | set(tb)) - set(out)
+    (kc,) = contracted
+    for idx in np.ndindex(*[shapes[x] for x in out]):
+        env = dict(zip(out, idx))
+        s = 0.0
+        for kv in range(shapes[kc]):
+            env[kc] = kv
+            s += float(a[tuple(env[x] for x in ta)]) * float(b[tuple(env[x] for x in tb)])
+        assert abs(float(d[idx]) - s) < 1e-9
