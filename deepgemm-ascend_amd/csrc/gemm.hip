@@ -275,7 +275,22 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     if (a.kind < kFP8FP8 || a.kind > kBF16) return dg_set_error("dg_gemm: unknown kind");
     if (a.gemm_type < kNormal || a.gemm_type > kKGrouped) return dg_set_error("dg_gemm: unknown gemm_type");
     if (a.m < 0 || a.n < 0 || a.k < 0) return dg_set_error("dg_gemm: negative size");
-    if (a.d_dtype != DG_DTYPE_BF16 && a.d_dtype != DG_DTYPE_F32) return dg_set_error("dg_gemm: D must be bf16 or fp32");
+    if (a.d_dtype != DG_DTYPE_BF16 && a.d_dtype != DG_DTYPE_F32 && a.d_dtype != DG_DTYPE_FP8_E4M3)
+        return dg_set_error("dg_gemm: D must be bf16, fp32 or e4m3");
+    if (a.epilogue != DG_EPI_DEFAULT && a.epilogue != DG_EPI_BF16_SR) return dg_set_error("dg_gemm: unknown epilogue");
+    if (a.epilogue == DG_EPI_BF16_SR &&
+        (a.d_dtype != DG_DTYPE_BF16 || a.accumulate || a.bias != nullptr || a.alpha != 1.0f))
+        return dg_set_error("Stochastic rounding requires a direct BF16 output");
+    if (a.d_dtype == DG_DTYPE_FP8_E4M3) {
+        if (a.kind != kFP8FP8 || (a.gemm_type != kNormal && a.gemm_type != kBatched))
+            return dg_set_error("dg_gemm: FP8 output needs e4m3 operands and a dense or batched GEMM");
+        if (a.accumulate || a.bias != nullptr || a.alpha != 1.0f || a.epilogue != DG_EPI_DEFAULT)
+            return dg_set_error("FP8 quantization requires a direct E4M3 output");
+        if (a.n % 128 != 0) return dg_set_error("FP8 output requires N to be a multiple of 128");
+        if (a.sfd == nullptr || a.sfd_ld < a.m) return dg_set_error("dg_gemm: FP8 output needs sfd with sfd_ld >= m");
+        if (a.ldd % 4 || (reinterpret_cast<uintptr_t>(a.d) & 3) || (a.gemm_type == kBatched && a.batch_stride_d % 4))
+            return dg_set_error("dg_gemm: FP8 output rows must be 4-byte aligned");
+    }
     if (a.m == 0 || a.n == 0) return DG_OK;
     const bool bf16 = a.kind == kBF16;
     if (a.a == nullptr || a.b == nullptr || a.d == nullptr) return dg_set_error("dg_gemm: null operand");
@@ -321,7 +336,9 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     if (cfg.bm == 0) return dg_set_error("dg_gemm: no tile shape fits this problem");
     if (!tile_allowed(a, cfg.bm, cfg.bn)) return dg_set_error("dg_gemm: block_m must divide the M-grouped alignment");
     // Direct register stores measured faster than staging the tile through LDS.
-    const int epi_kind = a.d_dtype == DG_DTYPE_F32 ? kEpiF32 : kEpiBf16;
+    const int epi_kind = a.d_dtype == DG_DTYPE_F32 ? kEpiF32
+                       : a.d_dtype == DG_DTYPE_FP8_E4M3 ? kEpiFp8
+                       : a.epilogue == DG_EPI_BF16_SR ? kEpiBf16SR : kEpiBf16;
     KernelFn fn = lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind);
     if (fn == nullptr) {
         char buf[160];
@@ -343,10 +360,12 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     p.lda = lda_b; p.ldb = ldb_b; p.ldd = a.ldd;
     p.bsa = a.batch_stride_a * esz_a; p.bsb = a.batch_stride_b * esz_b; p.bsd = a.batch_stride_d;
     p.sfa_ld = a.sfa_ld; p.sfb_ld = a.sfb_ld; p.sfa_bs = a.sfa_batch_stride; p.sfb_bs = a.sfb_batch_stride;
-    p.gemm_type = a.gemm_type; p.out_f32 = a.d_dtype == DG_DTYPE_F32; p.accumulate = a.accumulate != 0;
+    const int out_esz = a.d_dtype == DG_DTYPE_F32 ? 4 : a.d_dtype == DG_DTYPE_FP8_E4M3 ? 1 : 2;
+    p.gemm_type = a.gemm_type; p.out_esize = out_esz; p.accumulate = a.accumulate != 0;
     p.has_bias = a.bias != nullptr; p.alignment = a.alignment > 0 ? a.alignment : 256;
     p.alpha = a.alpha;
-    const int out_esz = p.out_f32 ? 4 : 2;
+    p.sfd = reinterpret_cast<uint8_t*>(a.sfd);
+    p.sfd_ld = a.sfd_ld;
     p.vec_store = (a.ldd % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.d) % (4 * out_esz)) == 0) &&
                   (a.gemm_type != kBatched && a.gemm_type != kMasked ? true : (a.batch_stride_d % 4 == 0));
     p.num_m_blocks = ceil_div(a.m, cfg.bm);

@@ -47,7 +47,7 @@ struct KParams {
     int64_t bsa, bsb;          // bytes
     int64_t bsd;               // elements of D
     int64_t sfa_ld, sfb_ld, sfa_bs, sfb_bs;   // int16 elements (ld even)
-    int gemm_type, out_f32, accumulate, has_bias, alignment, vec_store;
+    int gemm_type, out_esize, accumulate, has_bias, alignment, vec_store;   // out_esize: bytes per D element
     float alpha;
     int num_m_blocks, num_n_blocks;
     int kbytes_a, kbytes_b;    // bytes of one K row (multiple of 16)
@@ -59,11 +59,49 @@ struct KParams {
     int num_tiles;             // tiles of the launch (split-K grids are padded past it)
     float* ws;
     int* counters;
+    // FP8 output: per-(row, 32 columns) UE8M0 exponents, packed in pairs into int16
+    // sfd[(batch * n + col) / 64 * sfd_ld + row], lower byte = the even 32-column block.
+    uint8_t* sfd;
+    int64_t sfd_ld;
 };
 
 // Epilogue variants.
 constexpr int kEpiF32 = 1;       // fp32 D (bias / accumulate allowed)
 constexpr int kEpiBf16 = 2;      // bf16 D
+constexpr int kEpiBf16SR = 3;    // bf16 D, stochastic rounding (no bias / accumulate / alpha)
+constexpr int kEpiFp8 = 4;       // e4m3 D with per-(row, 32 columns) UE8M0 scales (n % 128 == 0)
+
+// Stochastic rounding of four consecutive fp32 outputs of a row (columns 4j .. 4j+3) to bf16.
+// The random bits come from a hash of the four fp32 bit patterns and the quartet index j
+// (tests/utils.py:70-92 of the reference pins the exact function, with zeros standing in for
+// columns past the end of the row): value v rounds up when its discarded low 16 bits exceed
+// 0xffff minus its 16 random bits; NaN becomes the canonical 0x7fc0.
+__device__ __forceinline__ void sr_bf16_quartet(const float* x, uint32_t j, uint16_t* out) {
+    uint32_t v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __builtin_bit_cast(uint32_t, x[i]);
+    uint32_t h = v[0] * 0x5671d42bu + v[1] * 0x9995e499u + v[2] * 0xace1b8a5u + v[3] * 0xe153538du + j;
+    h = (h ^ (h >> 23)) * 0x7feb352du;
+    h ^= h >> 16;
+    uint32_t h1 = h * 0x846ca68bu, h2 = h * 0xd35a2d97u;
+    h1 ^= h1 >> 11;
+    h2 ^= h2 >> 11;
+    const uint32_t rnd[4] = {h1 & 0xffffu, h1 >> 16, h2 & 0xffffu, h2 >> 16};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t up = (v[i] & 0xffffu) > (0xffffu - rnd[i]) ? 1u : 0u;
+        out[i] = (v[i] & 0x7fffffffu) > 0x7f800000u ? (uint16_t)0x7fc0 : (uint16_t)((v[i] >> 16) + up);
+    }
+}
+
+// UE8M0 exponent s of the scale 2^(s-127) for a block whose largest magnitude has bf16 bits
+// `x` (sign cleared): the smallest power of two with |max| <= 448 * 2^(s-127), at least 2^-22.
+// With x = (e << 7) | mant, |max| / 448 <= 2^(e-8) exactly when mant <= 0x60 (448 = 1.75 * 2^8),
+// so s = e - 8 + (mant > 0x60) = ((x + 31) >> 7) - 8; the floor of 2^-22 is the quantiser's
+// clamp of the block maximum at 1e-4 (tests/generators.py:80-81 of the reference).
+__device__ __forceinline__ uint32_t ue8m0_of_bf16_amax(uint32_t x) {
+    return max((x + 31u) >> 7, 113u) - 8u;
+}
 
 template <int N>
 struct Int { static constexpr int value = N; };
@@ -208,7 +246,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     const uint16_t* sfa = p.sfa;
     const uint16_t* sfb = p.sfb;
     uint8_t* d_base = p.d;
-    const int out_esize = p.out_f32 ? 4 : 2;
+    const int out_esize = p.out_esize;
     int group = 0;          // B operand group
     int valid_end = M;      // rows >= valid_end are padding (psum) / not written (masked)
     bool zero_tile = false;
@@ -266,7 +304,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
         for (int e = tid; e < rows * cols; e += NT) {
             const int rr = e / cols, cc = e % cols;
             const int64_t off = (int64_t)(m0 + rr) * p.ldd + n0 + cc;
-            if (p.out_f32) reinterpret_cast<float*>(d_base)[off] = 0.f;
+            if (out_esize == 4) reinterpret_cast<float*>(d_base)[off] = 0.f;
             else reinterpret_cast<uint16_t*>(d_base)[off] = 0;
         }
         return;
@@ -583,12 +621,14 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     // index would demote the accumulator array to scratch memory.
     const float alpha = p.alpha;
     constexpr bool kF32 = EPI == kEpiF32;
-    using OutT = std::conditional_t<kF32, float, uint16_t>;
+    constexpr bool kSR = EPI == kEpiBf16SR;
+    constexpr bool kFp8 = EPI == kEpiFp8;
+    using OutT = std::conditional_t<kF32, float, std::conditional_t<kFp8, uint8_t, uint16_t>>;
     OutT* dbase = reinterpret_cast<OutT*>(d_base);
     const OutT* bp = reinterpret_cast<const OutT*>(p.bias);
     const bool acc_old = p.accumulate, bias = p.has_bias, vec = p.vec_store;
     auto to_f = [](OutT x) -> float {
-        if constexpr (kF32) return x; else return bf16_to_f32(x);
+        if constexpr (kF32) return x; else if constexpr (kFp8) return 0.f; else return bf16_to_f32(x);
     };
     static_for<TM>([&](auto jm_c) {
         constexpr int jm = decltype(jm_c)::value;
@@ -605,6 +645,33 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
             float v[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) v[i] = acc[jn][jm][i] * alpha;
+            if constexpr (kFp8) {
+                // Quantise the bf16-rounded outputs per 32 columns of a row: this lane holds 16 of
+                // them, its partner lane (q ^ 1) the other 16.  The host guarantees n % 128 == 0, so
+                // a block is either entirely inside the row or entirely past it.
+                uint32_t amax = 0;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint16_t h = f32_to_bf16_rne(v[i]);
+                    v[i] = bf16_to_f32(h);
+                    amax = max(amax, (uint32_t)(h & 0x7fffu));
+                }
+                amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32));
+                const uint32_t sexp = ue8m0_of_bf16_amax(amax);
+                const float inv = __builtin_bit_cast(float, (254u - sexp) << 23);   // 2^(127 - s)
+                if (row_ok && nblk < N) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        int w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * g] * inv, v[4 * g + 1] * inv, 0, false);
+                        w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * g + 2] * inv, v[4 * g + 3] * inv, w, true);
+                        *reinterpret_cast<int*>(drow + nblk + 8 * g + 4 * q) = w;
+                    }
+                    if (q == 0) {
+                        const int64_t col = (int64_t)batch * N + nblk;
+                        p.sfd[((col >> 6) * p.sfd_ld + m) * 2 + ((col >> 5) & 1)] = (uint8_t)sexp;
+                    }
+                }
+            } else {
             const bool full = vec && nblk + 32 <= N;                   // wave-uniform
             if (full) {
                 if (bias) {
@@ -633,8 +700,15 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
                     uint32_t pk[4][2];
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
-                        pk[g][0] = pad_row ? 0u : pack_bf16x2(v[4 * g], v[4 * g + 1]);
-                        pk[g][1] = pad_row ? 0u : pack_bf16x2(v[4 * g + 2], v[4 * g + 3]);
+                        if constexpr (kSR) {
+                            uint16_t o[4];
+                            sr_bf16_quartet(v + 4 * g, (uint32_t)(nblk + 8 * g + 4 * q) >> 2, o);
+                            pk[g][0] = pad_row ? 0u : (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+                            pk[g][1] = pad_row ? 0u : (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+                        } else {
+                            pk[g][0] = pad_row ? 0u : pack_bf16x2(v[4 * g], v[4 * g + 1]);
+                            pk[g][1] = pad_row ? 0u : pack_bf16x2(v[4 * g + 2], v[4 * g + 3]);
+                        }
                     }
                     // v_permlane32_swap regroups the wave halves: afterwards the lower half
                     // (q = 0) holds columns 16..31 and the upper half (q = 1) columns 0..15 of
@@ -654,6 +728,20 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
                         *reinterpret_cast<i32x4*>(dp + 8) = i32x4{(int)pk[3][0], (int)pk[3][1], (int)pk[1][0], (int)pk[1][1]};
                     }
                 }
+            } else if (row_ok && kSR) {
+                // ragged / unaligned block, stochastic rounding: columns past the row hash as zeros
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int n = nblk + 8 * g + 4 * q;
+                    float x[4];
+                    uint16_t o[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) x[i] = n + i < N ? v[4 * g + i] : 0.f;
+                    sr_bf16_quartet(x, (uint32_t)n >> 2, o);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (n + i < N) drow[n + i] = pad_row ? (uint16_t)0 : o[i];
+                }
             } else if (row_ok) {
                 // ragged / unaligned block: element stores with bounds
 #pragma unroll
@@ -670,6 +758,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
                         }
                     }
             }
+            }   // !kFp8
         });
     });
 }

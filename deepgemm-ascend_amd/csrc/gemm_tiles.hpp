@@ -7,7 +7,7 @@ namespace dg {
 
 using KernelFn = void (*)(const KParams);
 
-// epi: kEpiF32 or kEpiBf16 (see gemm_kernel.hpp)
+// epi: kEpiF32, kEpiBf16, kEpiBf16SR or kEpiFp8 (see gemm_kernel.hpp)
 
 struct TileCfg {
     int bm, bn;
@@ -32,8 +32,16 @@ constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 template <int I, int KIND>
 KernelFn pick_epi(int epi) {
     constexpr TileCfg t = kTiles[I];
-    return epi == kEpiF32 ? &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiF32>
-                          : &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiBf16>;
+    switch (epi) {
+        case kEpiF32: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiF32>;
+        case kEpiBf16: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiBf16>;
+        case kEpiBf16SR: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiBf16SR>;
+        case kEpiFp8:
+            // FP8 output exists for e4m3 x e4m3 batched / dense GEMMs only (fp8_bmm)
+            if constexpr (KIND == kFP8FP8) return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiFp8>;
+            else return nullptr;
+        default: return nullptr;
+    }
 }
 
 template <int KIND, int I = 0>

@@ -15,7 +15,8 @@ _lib = None
 
 DG_KIND_FP8_FP8, DG_KIND_FP8_FP4, DG_KIND_FP4_FP4, DG_KIND_BF16 = 0, 1, 2, 3
 DG_GEMM_NORMAL, DG_GEMM_BATCHED, DG_GEMM_MGROUPED_PSUM, DG_GEMM_MGROUPED_IDX, DG_GEMM_MASKED, DG_GEMM_KGROUPED = 0, 1, 2, 3, 4, 5
-DG_DTYPE_BF16, DG_DTYPE_F32 = 0, 1
+DG_DTYPE_BF16, DG_DTYPE_F32, DG_DTYPE_FP8_E4M3 = 0, 1, 2
+DG_EPI_DEFAULT, DG_EPI_BF16_SR = 0, 1
 DG_SF_F32, DG_SF_I16 = 0, 1
 
 # Every symbol include/deep_gemm_amd.h declares.
@@ -39,6 +40,7 @@ class GemmArgs(ctypes.Structure):
         ('alignment', ctypes.c_int32), ('block_m', ctypes.c_int32), ('block_n', ctypes.c_int32),
         ('num_cus', ctypes.c_int32), ('split_k', ctypes.c_int32),
         ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_int64),
+        ('epilogue', ctypes.c_int32), ('sfd', ctypes.c_void_p), ('sfd_ld', ctypes.c_int64),
     ]
 
 

@@ -15,20 +15,17 @@ from .layout import _assert
 def fp8_bmm(a: Tuple[torch.Tensor, torch.Tensor], b: Tuple[torch.Tensor, torch.Tensor], d, c: Optional[torch.Tensor] = None,
             recipe=(1, 1, 32), compiled_dims: str = 'nk', epilogue=None) -> None:
     """Batched FP8 GEMM D[i] = A[i] @ B[i]^T (+ C[i]) (csrc/apis/einsum.hpp:22-71).
-    A [B, M, K] e4m3, B [B, N, K] e4m3, SFs fp32 or packed int16 in any major; D [B, M, N] bf16 / fp32."""
-    if isinstance(d, tuple):
-        raise RuntimeError('FP8 output (a (D, SFD) pair) is not supported: only bf16 / fp32 D')
-    _assert(epilogue is None, 'fp8_bmm supports the default epilogue only')
+    A [B, M, K] e4m3, B [B, N, K] e4m3, SFs fp32 or packed int16 in any major; D [B, M, N] bf16 /
+    fp32, or an (e4m3 D, SFD) pair / FP8Quantization(sfd) with SFD int16 [M, B * N / 64], M-major."""
     (a_, sfa), (b_, sfb) = a, b
-    _batched(a_, sfa, b_, sfb, d, c, recipe, bf16=False)
+    _batched(a_, sfa, b_, sfb, d, c, recipe, False, epilogue)
 
 
 def bf16_bmm(a: torch.Tensor, b: torch.Tensor, d: torch.Tensor, c: Optional[torch.Tensor] = None,
              compiled_dims: str = 'nk', epilogue=None) -> None:
     """Batched bf16 GEMM D[i] = A[i] @ B[i]^T (+ C[i]) (csrc/apis/einsum.hpp:73-97)."""
     _assert(d.dtype in (torch.float32, torch.bfloat16))
-    _assert(epilogue is None, 'bf16_bmm supports the default epilogue only')
-    _batched(a, None, b, None, d, c, None, bf16=True)
+    _batched(a, None, b, None, d, c, None, True, epilogue)
 
 
 def _perm(t: Optional[torch.Tensor], p):
@@ -56,15 +53,18 @@ def fp8_einsum(expr: str, a: Tuple[torch.Tensor, torch.Tensor], b: Tuple[torch.T
     permuted with their operands."""
     (a_, sfa), (b_, sfb) = a, b
     if expr == 'bhr,hdr->bhd':
-        # A=[b,h,r] B=[h,d,r] D=[b,h,d] -> (B,M,N,K) = (h,b,d,r)
-        fp8_bmm((a_.permute(1, 0, 2), sfa.permute(1, 0, 2)), (b_, sfb), d.permute(1, 0, 2), _perm(c, (1, 0, 2)),
+        # A=[b,h,r] B=[h,d,r] D=[b,h,d] -> (B,M,N,K) = (h,b,d,r); the output SF of an FP8 D stays as given
+        perm_d = (d[0].permute(1, 0, 2), d[1]) if isinstance(d, tuple) else d.permute(1, 0, 2)
+        fp8_bmm((a_.permute(1, 0, 2), sfa.permute(1, 0, 2)), (b_, sfb), perm_d, _perm(c, (1, 0, 2)),
                 recipe, 'nk', epilogue)
     elif expr == 'bhd,hdr->bhr':
         # A=[b,h,d] B=[h,d,r] D=[b,h,r] -> (h,b,r,d)
+        _assert(not isinstance(d, tuple))
         fp8_bmm((a_.permute(1, 0, 2), sfa.permute(1, 0, 2)), (b_.permute(0, 2, 1), sfb.permute(0, 2, 1)),
                 d.permute(1, 0, 2), _perm(c, (1, 0, 2)), recipe, 'nk', epilogue)
     elif expr == 'bhd,bhr->hdr':
         # A=[b,h,d] B=[b,h,r] D=[h,d,r] -> (h,d,r,b): batch h, contraction over b
+        _assert(not isinstance(d, tuple))
         fp8_bmm((a_.permute(1, 2, 0), sfa.permute(1, 2, 0)), (b_.permute(1, 2, 0), sfb.permute(1, 2, 0)),
                 d, c, recipe, 'mn', epilogue)
     else:

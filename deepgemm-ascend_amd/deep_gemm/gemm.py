@@ -140,7 +140,8 @@ def _fill_common(args, d, k_kernel, alpha, kind):
     args.kind = kind
     args.d = d.data_ptr()
     args.ldd = d.stride(-2)
-    args.d_dtype = _lib.DG_DTYPE_F32 if d.dtype == torch.float32 else _lib.DG_DTYPE_BF16
+    args.d_dtype = {torch.float32: _lib.DG_DTYPE_F32, torch.float8_e4m3fn: _lib.DG_DTYPE_FP8_E4M3}.get(
+        d.dtype, _lib.DG_DTYPE_BF16)
     args.alpha = 1.0 if alpha is None else float(alpha)
     args.k = k_kernel
     args.num_cus = get_num_sms()
@@ -150,13 +151,15 @@ def _fill_common(args, d, k_kernel, alpha, kind):
         args.block_m, args.block_n = (int(x) for x in forced.split('x'))
 
 
-def _early_return(m, n, k, d, c, is_cd_same, with_bias) -> bool:
+def _early_return(m, n, k, d, c, is_cd_same, with_bias, sfd=None) -> bool:
     """csrc/utils/layout.hpp:54-86."""
     if m == 0 or n == 0:
         return True
+    _assert(sfd is None or c is None)
     if is_cd_same:
         _assert(c.shape == d.shape and c.stride() == d.stride())
-    _assert(d.dtype in (torch.bfloat16, torch.float32))
+    _assert(d.dtype in (torch.bfloat16, torch.float32, torch.float8_e4m3fn))
+    _assert((d.dtype == torch.float8_e4m3fn) == (sfd is not None))
     if c is not None:
         _assert(c.stride(-1) == 1)
         _assert(d.dtype == c.dtype)
@@ -168,8 +171,20 @@ def _early_return(m, n, k, d, c, is_cd_same, with_bias) -> bool:
                 d.copy_(c.expand_as(d))
             else:
                 d.zero_()
+        if sfd is not None:
+            sfd.zero_()
         return True
     return False
+
+
+def _apply_epilogue(args, epi) -> None:
+    """Epilogue class -> dg_gemm_args fields (after _fill_common)."""
+    if isinstance(epi, _epi.BF16StochasticRounding):
+        args.epilogue = _lib.DG_EPI_BF16_SR
+    elif isinstance(epi, _epi.FP8Quantization):
+        args.d_dtype = _lib.DG_DTYPE_FP8_E4M3
+        args.sfd = epi.sfd.data_ptr()
+        args.sfd_ld = epi.sfd.stride(1)
 
 
 def _dense_gemm(a, sfa, b, sfb, d, c, recipe, recipe_a, recipe_b, disable_ue8m0_cast, alpha, epilogue,
@@ -226,6 +241,7 @@ def _dense_gemm(a, sfa, b, sfb, d, c, recipe, recipe_a, recipe_b, disable_ue8m0_
     args.m, args.n, args.num_groups = m, n, 1
     args.accumulate = 1 if is_cd_same else 0
     args.bias = c.data_ptr() if with_bias else None
+    _apply_epilogue(args, epi)
     _launch(args, d)
 
 
@@ -291,7 +307,6 @@ def _grouped_contiguous(a, sfa, b, sfb, d, grouped_layout, recipe, recipe_a, rec
         _assert(b.dtype == torch.float8_e4m3fn or _is_fp4(b))
     _assert(d.dtype in (torch.bfloat16, torch.float32))
     epi = _epi.resolve(epilogue, None, d)
-    _assert(isinstance(epi, _epi.Identity), 'grouped GEMMs only support the identity epilogue')
     _assert(_major_is_k(a))
     kb = _major_is_k(b)
     m, k = _logical_mn(a, True), _logical_k(a, True)
@@ -336,6 +351,7 @@ def _grouped_contiguous(a, sfa, b, sfb, d, grouped_layout, recipe, recipe_a, rec
     args.batch_stride_b = b_k.stride(0)
     args.grouped_layout = grouped_layout.data_ptr()
     args.m, args.n, args.num_groups = m, n, g
+    _apply_epilogue(args, epi)
     _launch(args, d)
 
 
@@ -424,20 +440,22 @@ def m_grouped_bf16_gemm_nt_masked(a, b, d, masked_m: torch.Tensor, expected_m: i
     _masked(a, None, b, None, d, masked_m, None, None, None, False, bf16=True)
 
 
-def _batched(a, sfa, b, sfb, d, c, recipe, bf16: bool):
+def _batched(a, sfa, b, sfb, d, c, recipe, bf16: bool, epilogue=None):
     """Batched GEMM D[i] = A[i] @ B[i]^T (+ C[i]): fp8_bmm / bf16_bmm (csrc/apis/einsum.hpp:37-97),
-    get_gemm_desc with GemmType::Batched (csrc/apis/gemm.hpp:60-197)."""
+    get_gemm_desc with GemmType::Batched (csrc/apis/gemm.hpp:60-197).  ``d`` may be an
+    (e4m3 D, SFD) pair (fp8_bmm only)."""
+    sfd = None
+    if isinstance(d, tuple):
+        _assert(not bf16, 'bf16_bmm has no FP8 output')
+        d, sfd = d
     if bf16:
         _assert(a.dtype == torch.bfloat16)
         _assert(b.dtype == torch.bfloat16)
+        _assert(d.dtype in (torch.float32, torch.bfloat16))
     else:
         _assert(a.dtype == torch.float8_e4m3fn)
         _assert(b.dtype == torch.float8_e4m3fn)
-    _assert(d.dtype in (torch.bfloat16, torch.float32))
     _assert(a.dim() == 3 and b.dim() == 3 and d.dim() == 3, 'batched GEMM takes A [B,M,K], B [B,N,K], D [B,M,N]')
-    _assert(a.stride(-1) == 1 or a.stride(-2) == 1)
-    _assert(b.stride(-1) == 1 or b.stride(-2) == 1)
-    _assert(d.stride(-1) == 1)
     ka, kb = _major_is_k(a), _major_is_k(b)
     bs, m, k = a.size(0), _logical_mn(a, ka), _logical_k(a, ka)
     n, k_b = _logical_mn(b, kb), _logical_k(b, kb)
@@ -445,12 +463,16 @@ def _batched(a, sfa, b, sfb, d, c, recipe, bf16: bool):
         raise RuntimeError(f"Conflicting shape dimension 'k': A gives {k}, B gives {k_b}")
     _assert(b.size(0) == bs and d.size(0) == bs and d.size(1) == m and d.size(2) == n,
             f'D shape {tuple(d.shape)} != ({bs}, {m}, {n})')
+    _assert(d.stride(-1) == 1)
     if bs == 0:
         return
+    epi = _epi.resolve(epilogue, c, d, None, sfd)
+    if isinstance(epi, _epi.FP8Quantization):
+        sfd = epi.sfd
     is_cd_same = c is not None and c.data_ptr() == d.data_ptr() and d.numel() > 0
     if c is not None:
         _assert(c.shape == d.shape and c.dtype == d.dtype and c.stride(-1) == 1)
-    if _early_return(m, n, k, d, c, is_cd_same, False):
+    if _early_return(m, n, k, d, c, is_cd_same, False, sfd):
         return
     args = _lib.GemmArgs()
     if bf16:
@@ -480,6 +502,7 @@ def _batched(a, sfa, b, sfb, d, c, recipe, bf16: bool):
     args.batch_stride_a, args.batch_stride_b, args.batch_stride_d = a_k.stride(0), b_k.stride(0), d.stride(0)
     args.m, args.n, args.num_groups = m, n, bs
     args.accumulate = 1 if c is not None else 0
+    _apply_epilogue(args, epi)
     _launch(args, d)
 
 
@@ -497,8 +520,7 @@ def _k_grouped(a, sfa, b, sfb, d, grouped_layout, c, recipe, use_psum_layout, ep
         _assert(a.dtype == torch.float8_e4m3fn or _is_fp4(a))
         _assert(b.dtype == torch.float8_e4m3fn or _is_fp4(b))
     _assert(d.dtype in (torch.bfloat16, torch.float32))
-    epi = _epi.resolve(epilogue, None, d)
-    _assert(isinstance(epi, _epi.Identity), 'K-grouped GEMMs only support the identity epilogue')
+    epi = _epi.resolve(epilogue, c, d)
     _assert(grouped_layout.is_contiguous() and grouped_layout.dtype == torch.int32 and grouped_layout.dim() == 1)
     g = grouped_layout.numel()
     ka, kb = _major_is_k(a_t), _major_is_k(b_t)
@@ -541,6 +563,7 @@ def _k_grouped(a, sfa, b, sfb, d, grouped_layout, c, recipe, use_psum_layout, ep
     args.grouped_layout = grouped_layout.data_ptr()
     args.m, args.n, args.num_groups = m, n, g
     args.accumulate = 1 if c is not None else 0
+    _apply_epilogue(args, epi)
     _launch(args, d)
 
 

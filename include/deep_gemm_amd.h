@@ -41,8 +41,20 @@ extern "C" {
                                     (k_grouped_fp8_gemm_tn_contiguous, csrc/apis/gemm.hpp:351-387);
                                     alignment a multiple of 64; accumulate allowed              */
 
-#define DG_DTYPE_BF16 0
-#define DG_DTYPE_F32  1
+#define DG_DTYPE_BF16     0
+#define DG_DTYPE_F32      1
+#define DG_DTYPE_FP8_E4M3 2   /* e4m3 D quantised per (row, 32 columns) with UE8M0 scales in sfd
+                                 (the FP8Quantization epilogue, csrc/jit_kernels/epilogue_class.hpp:77-107,
+                                 deep_gemm/include/deep_gemm/epilogue/operators.hpp:339-463):
+                                 DG_KIND_FP8_FP8, DG_GEMM_NORMAL / BATCHED, n % 128 == 0, no
+                                 accumulate / bias / alpha                                       */
+
+/* Output rounding of a bf16 D. */
+#define DG_EPI_DEFAULT 0      /* round to nearest even                                          */
+#define DG_EPI_BF16_SR 1      /* stochastic rounding keyed by a hash of each quartet of fp32
+                                 outputs (the BF16StochasticRounding epilogue,
+                                 deep_gemm/include/deep_gemm/epilogue/operators.hpp:224-337);
+                                 bf16 D, no accumulate / bias / alpha                           */
 
 #define DG_SF_F32 0   /* fp32 powers of two, one per gran_mn x gran_k block             */
 #define DG_SF_I16 1   /* packed UE8M0x2 int16, one per gran_mn x 64                       */
@@ -86,6 +98,11 @@ typedef struct dg_gemm_args {
                                   /* (dense / batched GEMMs with a workspace only)           */
     void *workspace;              /* device scratch for split-K, or NULL (no split)          */
     int64_t workspace_bytes;      /* its size; see dg_gemm_workspace_size()                  */
+    int32_t epilogue;             /* DG_EPI_*                                                */
+    int16_t *sfd;                 /* DG_DTYPE_FP8_E4M3 only: output SF, int16 pairs of UE8M0 bytes;
+                                     pair p = (batch * n + col) / 64 of row `row` at
+                                     sfd[p * sfd_ld + row], lower byte = the even 32 columns      */
+    int64_t sfd_ld;               /* >= m                                                    */
 } dg_gemm_args;
 
 /* Launch one GEMM.  Entry point replacing deep_gemm::launch_fp8_gemm /

@@ -13,10 +13,13 @@ It restates, in plain CPU torch / numpy, the reference's own reference math:
                  ``transform_sf_into_required_layout`` (``tests/test_layout.py:39-50``)
                  and the psum / m_indices helpers (``tests/generators.py:212-235``).
 * ``gemm``    -- dequantise-to-fp32 then matmul then cast (``tests/generators.py:320-322``),
-                 grouped and masked variants, and ``calc_diff`` (``tests/utils.py:36-43``).
+                 grouped, masked, batched, K-grouped and einsum variants, and ``calc_diff``
+                 (``tests/utils.py:36-43``).
+* ``epilogue`` -- stochastic bf16 rounding (``tests/utils.py:70-92``) and FP8 output
+                 quantisation (``tests/test_einsum.py:70-86``).
 
 Every function is pinned by ``tests/test_oracle.py`` against closed forms, library
 routines, brute force on tiny inputs and the committed fixtures in ``tests/golden/``.
 Parity status per function is listed in each module's docstring.
 """
-from . import quant, layout, gemm  # noqa: F401
+from . import quant, layout, gemm, epilogue  # noqa: F401

@@ -125,12 +125,37 @@ def test_mk_alignment_setter():
     deep_gemm.set_mk_alignment_for_contiguous_layout(old)
 
 
-def test_unsupported_epilogues_raise():
+def test_epilogue_checks_match_reference():
+    """csrc/jit_kernels/epilogue_class.hpp:66-128: stochastic rounding needs a direct bf16 D, FP8
+    quantization a direct e4m3 D with N % 128 == 0 and an M-major int16 SFD; the epilogue class,
+    alpha and the FP8 pair are exclusive; the dense API only takes bf16 / fp32 D."""
     a, b = _fp8((64, 128)), _fp8((32, 128))
-    d = torch.empty(64, 32, dtype=torch.bfloat16)
-    with pytest.raises(RuntimeError, match='not supported'):
-        deep_gemm.fp8_gemm_nt((a, torch.ones(64, 4)), (b, torch.ones(32, 4)), d,
-                              epilogue=deep_gemm.epilogue.BF16StochasticRounding())
+    sfa, sfb = torch.ones(64, 4), torch.ones(32, 4)
+    d32 = torch.empty(64, 32)
+    sr = deep_gemm.epilogue.BF16StochasticRounding()
+    with pytest.raises(RuntimeError, match='Stochastic rounding requires a direct BF16 output'):
+        deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d32, epilogue=sr)
+    with pytest.raises(RuntimeError, match='exclusive'):
+        deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d32, alpha=2.0, epilogue=sr)
+    a3, b3 = _fp8((2, 64, 128)), _fp8((2, 256, 128))
+    sfa3, sfb3 = torch.ones(2, 64, 4), torch.ones(2, 256, 4)
+    # FP8 D rows hold every batch: [M, B, N] storage viewed as [B, M, N] (batch stride == N)
+    d8 = torch.empty(64, 2, 256, dtype=torch.float8_e4m3fn).transpose(0, 1)
+    good = torch.empty_strided((64, 2 * 256 // 64), (1, 64), dtype=torch.int16)
+    bad = torch.empty(64, 2 * 256 // 64, dtype=torch.int16)
+    with pytest.raises(RuntimeError):
+        deep_gemm.fp8_bmm((a3, sfa3), (b3, sfb3), (d8, bad))
+    with pytest.raises(RuntimeError, match='multiple of 128'):
+        deep_gemm.fp8_bmm((a3, sfa3), (_fp8((2, 64, 128)), torch.ones(2, 64, 4)),
+                          (torch.empty(64, 2, 64, dtype=torch.float8_e4m3fn).transpose(0, 1),
+                           torch.empty_strided((64, 2), (1, 64), dtype=torch.int16)))
+    with pytest.raises(RuntimeError, match='exclusive'):
+        deep_gemm.fp8_bmm((a3, sfa3), (b3, sfb3), (d8, good), epilogue=deep_gemm.epilogue.FP8Quantization(good))
+    # K == 0: D and SFD are zero-filled on the host without a launch
+    d0 = torch.ones(64, 2, 256).to(torch.float8_e4m3fn).transpose(0, 1)
+    s0 = good.fill_(7)
+    deep_gemm.fp8_bmm((_fp8((2, 64, 0)), torch.ones(2, 64, 0)), (_fp8((2, 256, 0)), torch.ones(2, 256, 0)), (d0, s0))
+    assert int(d0.view(torch.uint8).count_nonzero()) == 0 and int(s0.count_nonzero()) == 0
 
 
 def test_import_is_lazy_and_fork_safe():

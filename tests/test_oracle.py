@@ -325,3 +325,75 @@ def test_einsum_ref_matches_loops(expr):
             env[kc] = kv
             s += float(a[tuple(env[x] for x in ta)]) * float(b[tuple(env[x] for x in tb)])
         assert abs(float(d[idx]) - s) < 1e-9
+
+
+# ----------------------------------------------------------------------------- epilogues
+from oracle import epilogue as oe   # noqa: E402
+
+
+def _sr_scalar(vals, j):
+    """The same hash, one quartet, in Python integers (independent of numpy's uint32 rules)."""
+    M = 0xffffffff
+    v = [int(x) & M for x in vals]
+    h = (v[0] * 0x5671d42b + v[1] * 0x9995e499 + v[2] * 0xace1b8a5 + v[3] * 0xe153538d + j) & M
+    h = ((h ^ (h >> 23)) * 0x7feb352d) & M
+    h ^= h >> 16
+    h1, h2 = (h * 0x846ca68b) & M, (h * 0xd35a2d97) & M
+    h1 ^= h1 >> 11
+    h2 ^= h2 >> 11
+    rnd = [h1 & 0xffff, h1 >> 16, h2 & 0xffff, h2 >> 16]
+    out = []
+    for x, r in zip(v, rnd):
+        if (x & 0x7fffffff) > 0x7f800000:
+            out.append(0x7fc0)
+        else:
+            out.append(((x >> 16) + ((x & 0xffff) > 0xffff - r)) & 0xffff)
+    return out
+
+
+def test_stochastic_round_matches_scalar_hash():
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(3, 10, generator=g) * 100
+    x[1, 3] = float('nan')
+    x[2, 0] = float('inf')
+    got = oe.stochastic_round_bf16(x).view(torch.int16).numpy().astype(np.int64) & 0xffff
+    bits = x.view(torch.int32).numpy().astype(np.int64) & 0xffffffff
+    for row in range(3):
+        padded = list(bits[row]) + [0, 0]
+        for j in range(3):
+            exp = _sr_scalar(padded[4 * j:4 * j + 4], j)
+            for i in range(4):
+                if 4 * j + i < 10:
+                    assert got[row, 4 * j + i] == exp[i]
+    assert got[1, 3] == 0x7fc0 and got[2, 0] == 0x7f80
+
+
+def test_stochastic_round_is_up_or_down_and_unbiased():
+    g = torch.Generator().manual_seed(13)
+    x = torch.rand(4096, 64, generator=g) + 1.0          # [1, 2): one bf16 ulp = 2^-7
+    out = oe.stochastic_round_bf16(x)
+    lo = (x.view(torch.int32) >> 16).to(torch.int32)
+    ob = out.view(torch.int16).to(torch.int32) & 0xffff
+    assert bool(((ob == lo) | (ob == lo + 1)).all())
+    # E[round(x)] = x: the mean error is far below the 2^-8 bias of truncation
+    err = (out.float() - x).double().mean().item()
+    assert abs(err) < 2e-5
+    exact = x.bfloat16().float()
+    assert torch.equal(oe.stochastic_round_bf16(exact).float(), exact)
+
+
+def test_quantize_fp8_output_packing():
+    g = torch.Generator().manual_seed(14)
+    d = (torch.randn(5, 256, generator=g) * torch.logspace(-3, 3, 256)).bfloat16()
+    data, sfd = oe.quantize_fp8_output(d)
+    assert sfd.shape == (5, 4) and sfd.stride() == (1, 5)
+    u = sfd.to(torch.int32) & 0xffff
+    for r in range(5):
+        for blk in range(8):
+            amax = float(d[r, 32 * blk:32 * blk + 32].float().abs().max())
+            e = quant.ceil_to_ue8m0(torch.tensor([max(amax, 1e-4) / 448.0])).view(torch.int32).item() >> 23
+            byte = (int(u[r, blk // 2]) >> (8 * (blk % 2))) & 0xff
+            assert byte == e
+            scale = 2.0 ** (e - 127)
+            ref = (d[r, 32 * blk:32 * blk + 32].float() / scale).to(torch.float8_e4m3fn)
+            assert torch.equal(data[r, 32 * blk:32 * blk + 32].view(torch.uint8), ref.view(torch.uint8))
