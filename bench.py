@@ -39,6 +39,9 @@ def parse():
     ap.add_argument('--m', type=int, default=M)
     ap.add_argument('--n', type=int, default=N)
     ap.add_argument('--k', type=int, default=K)
+    ap.add_argument('--suite', default=None,
+                    help='comma list of dense,bf16,fp4,grouped,kgrouped,einsum: one JSON line per shape '
+                         '(cold-L2 kernel times) instead of the north-star line')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a 256 MiB device copy (reference kernel for FETCH_SIZE / WRITE_SIZE scaling)')
     return ap.parse_args()
@@ -91,6 +94,179 @@ def cpu_baseline(a, sfa, b, sfb, m, n, k, seconds):
     }
 
 
+# ----------------------------------------------------------------------------- shape suite
+def _gpu_codes(shape, dev, gen):
+    """Random e4m3 codes (every non-NaN code) generated on the device."""
+    import torch
+    raw = torch.randint(0, 254, shape, dtype=torch.uint8, device=dev, generator=gen)
+    raw += (raw >= 0x7f).to(torch.uint8)
+    return raw.view(torch.float8_e4m3fn)
+
+
+def _gpu_sf(shape, dev, gen, lo=118, hi=122):
+    """fp32 power-of-two scales 2^(e-127), e in [lo, hi)."""
+    import torch
+    e = torch.randint(lo, hi, shape, dtype=torch.int32, device=dev, generator=gen)
+    return (e << 23).view(torch.float32)
+
+
+_FLUSH = None
+
+
+def _time_cold(fn, iters=20):
+    """Median kernel time (µs) with the operands evicted from L2 and the 256 MB MALL before every
+    launch (the reference times cold-L2 launches, tests/common.py:226-236); events bracket each
+    launch on its stream.  The eviction READS 1 GiB: a write-based flush leaves the MALL full of
+    dirty lines whose write-back then competes with the measured kernel (measured: a plain
+    streaming read drops from 4.5 to 2.4 TB/s after a 512 MB memset)."""
+    import torch
+    global _FLUSH
+    if _FLUSH is None:
+        _FLUSH = torch.ones(1 << 28, dtype=torch.float32, device='cuda')
+    fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    sinks = []
+    torch.cuda._sleep(int(2e7))
+    for e0, e1 in evs:
+        sinks.append(_FLUSH.sum())
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    ts = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in evs)
+    return ts[len(ts) // 2]
+
+
+def _line(group, workload, us, flops, nbytes, peak_tflops=PEAK_FP8_TFLOPS, **extra):
+    tflops = flops / (us * 1e-6) / 1e12
+    roof_us = max(flops / (peak_tflops * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)) * 1e6
+    out = {'suite': group, 'workload': workload, 'kernel_us': round(us, 2), 'tflops': round(tflops, 1),
+           'hbm_gbs': round(nbytes / (us * 1e-6) / 1e9, 1), 'bound': 'mfma' if flops / (peak_tflops * 1e12) * 1e6 >= roof_us - 1e-9 else 'hbm',
+           'roofline_us': round(roof_us, 2), 'roofline_frac': round(roof_us / us, 4),
+           'mfma_frac': round(tflops / peak_tflops, 4)}
+    out.update(extra)
+    print(json.dumps(out), flush=True)
+
+
+def _routed_counts(num_tokens=8192, num_experts=256, topk=8, local=32, seed=0):
+    """Per-expert token counts of one GPU's 32 experts: top-8 of N(0,1) logits over 256 experts."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.randn(num_tokens, num_experts, generator=g).topk(topk, dim=-1).indices.flatten()
+    return torch.bincount(idx, minlength=num_experts)[:local].tolist()
+
+
+def run_suite(groups):
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    gen = torch.Generator(device=dev).manual_seed(0)
+    NK = [(2112, 7168), (24576, 1536), (7168, 16384), (4096, 7168), (7168, 2048)]
+
+    def fp8_operand(rows, k, gran_mn, batch=None):
+        shape = (batch, rows, k) if batch else (rows, k)
+        sf_shape = ((batch,) if batch else ()) + (-(-rows // gran_mn), -(-k // 128))
+        return _gpu_codes(shape, dev, gen), _gpu_sf(sf_shape, dev, gen)
+
+    if 'dense' in groups:
+        for m in (1, 64, 128, 4096):
+            for n, k in NK:
+                a, sfa = fp8_operand(m, k, 1)
+                b, sfb = fp8_operand(n, k, 128)
+                sfa = deep_gemm.transform_sf_into_required_layout(sfa, m, k, (1, 128), is_sfa=True)
+                sfb = deep_gemm.transform_sf_into_required_layout(sfb, n, k, (128, 128), is_sfa=False)
+                d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+                us = _time_cold(lambda: deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d))
+                _line('dense', f'fp8_gemm_nt {m}x{n}x{k}', us, 2.0 * m * n * k,
+                      m * k + n * k + 2 * m * n + (m + n) * (k // 64) * 2)
+    if 'bf16' in groups:
+        for m in (128, 4096):
+            for n, k in NK:
+                a = (torch.randn(m, k, device=dev, generator=gen) * 0.1).bfloat16()
+                b = (torch.randn(n, k, device=dev, generator=gen) * 0.1).bfloat16()
+                d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+                us = _time_cold(lambda: deep_gemm.bf16_gemm_nt(a, b, d))
+                _line('bf16', f'bf16_gemm_nt {m}x{n}x{k}', us, 2.0 * m * n * k, 2 * (m * k + n * k + m * n),
+                      peak_tflops=2500.0)
+    if 'fp4' in groups:
+        for m in (128, 4096):
+            for n, k in ((7168, 2048), (4096, 7168)):
+                a, sfa = fp8_operand(m, k, 1)
+                b = torch.randint(-128, 128, (n, k // 2), dtype=torch.int8, device=dev, generator=gen)
+                sfb = _gpu_sf((n, k // 32), dev, gen, 125, 128)
+                sfa = deep_gemm.transform_sf_into_required_layout(sfa, m, k, (1, 128), is_sfa=True)
+                sfb = deep_gemm.transform_sf_into_required_layout(sfb, n, k, (1, 32), is_sfa=False)
+                d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+                us = _time_cold(lambda: deep_gemm.fp8_fp4_gemm_nt((a, sfa), (b, sfb), d))
+                _line('fp4', f'fp8_fp4_gemm_nt {m}x{n}x{k}', us, 2.0 * m * n * k,
+                      m * k + n * k // 2 + 2 * m * n + (m + n) * (k // 64) * 2)
+    if 'grouped' in groups:
+        counts = _routed_counts()
+        align = 128
+        deep_gemm.set_mk_alignment_for_contiguous_layout(align)
+        total, psum = 0, []
+        for c in counts:
+            psum.append(total + c)
+            total = -(-(total + c) // align) * align
+        valid = sum(counts)
+        for n, k in ((4096, 7168), (7168, 2048)):
+            g_ = len(counts)
+            a, sfa = fp8_operand(total, k, 1)
+            b, sfb = fp8_operand(n, k, 128, batch=g_)
+            layout = torch.tensor(psum, dtype=torch.int32, device=dev)
+            sfa = deep_gemm.transform_sf_into_required_layout(sfa, total, k, (1, 128), is_sfa=True, psum_layout=layout)
+            sfb = deep_gemm.transform_sf_into_required_layout(sfb, n, k, (128, 128), num_groups=g_, is_sfa=False)
+            d = torch.empty(total, n, dtype=torch.bfloat16, device=dev)
+            us = _time_cold(lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous((a, sfa), (b, sfb), d, layout))
+            _line('grouped', f'm_grouped_contiguous G=32 rows={total} (valid {valid}) N={n} K={k}', us,
+                  2.0 * valid * n * k, total * k + g_ * n * k + 2 * total * n, padded_tflops=round(
+                      2.0 * total * n * k / (us * 1e-6) / 1e12, 1))
+            mmax = 256
+            masked = torch.tensor([min(c, mmax) for c in counts], dtype=torch.int32, device=dev)
+            am, sfam = fp8_operand(mmax, k, 1, batch=g_)
+            sfam = deep_gemm.transform_sf_into_required_layout(sfam, mmax, k, (1, 128), num_groups=g_, is_sfa=True)
+            dm = torch.empty(g_, mmax, n, dtype=torch.bfloat16, device=dev)
+            em = int(sum(min(c, mmax) for c in counts) / g_)
+            us = _time_cold(lambda: deep_gemm.m_grouped_fp8_gemm_nt_masked((am, sfam), (b, sfb), dm, masked, em))
+            vm = sum(min(c, mmax) for c in counts)
+            _line('grouped', f'm_grouped_masked G=32 max_m={mmax} (valid {vm}) N={n} K={k}', us,
+                  2.0 * vm * n * k, vm * k + g_ * n * k + 2 * vm * n)
+        deep_gemm.set_mk_alignment_for_contiguous_layout(256)
+    if 'kgrouped' in groups:
+        import random
+        rng = random.Random(0)
+        for g_, m, n, ek in ((4, 4096, 7168, 8192), (4, 7168, 2048, 8192), (8, 4096, 7168, 4096),
+                             (8, 7168, 2048, 4096), (16, 4096, 7168, 2048), (16, 7168, 2048, 2048)):
+            ks = [max(1, int(ek * rng.uniform(0.7, 1.3))) for _ in range(g_)]
+            total, psum = 0, []
+            for kk in ks:
+                psum.append(total + kk)
+                total = -(-(total + kk) // 256) * 256
+            a = _gpu_codes((total, m), dev, gen)
+            b = _gpu_codes((total, n), dev, gen)
+            sfa = _gpu_sf((total // 32, m), dev, gen)
+            sfb = _gpu_sf((total // 32, n), dev, gen)
+            layout = torch.tensor(psum, dtype=torch.int32, device=dev)
+            d = torch.zeros(g_, m, n, dtype=torch.float32, device=dev)
+            fn = lambda: deep_gemm.k_grouped_fp8_gemm_tn_contiguous((a, sfa), (b, sfb), d, ks, layout, c=d)
+            us = _time_cold(fn)
+            sk = sum(ks)
+            _line('kgrouped', f'k_grouped_fp8_gemm_tn G={g_} M={m} N={n} sumK={sk} fp32 acc', us,
+                  2.0 * m * n * sk, total * (m + n) + 8 * g_ * m * n, includes='MN->K-major operand copy and SF transform')
+    if 'einsum' in groups:
+        h, r, dd = 8, 4096, 1024
+        for bsz in (4096, 8192):
+            a = _gpu_codes((h, bsz, r), dev, gen).permute(1, 0, 2)          # [b, h, r], r contiguous
+            sfa = _gpu_sf((h, bsz, r // 32), dev, gen).permute(1, 0, 2)
+            bw = _gpu_codes((h, dd, r), dev, gen)
+            sfb = _gpu_sf((h, dd, r // 32), dev, gen)
+            d = torch.empty(bsz, h, dd, dtype=torch.bfloat16, device=dev)
+            us = _time_cold(lambda: deep_gemm.fp8_einsum('bhr,hdr->bhd', (a, sfa), (bw, sfb), d))
+            _line('einsum', f"fp8_einsum bhr,hdr->bhd b={bsz} h={h} r={r} d={dd}", us, 2.0 * bsz * h * r * dd,
+                  bsz * h * r + h * dd * r + 2 * bsz * h * dd, includes='SF transform')
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
@@ -99,6 +275,9 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.suite:
+        run_suite(set(args.suite.split(',')))
         return
     import torch
     import deep_gemm

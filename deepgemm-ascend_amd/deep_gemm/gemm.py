@@ -71,7 +71,7 @@ def _to_kernel_operand(t: torch.Tensor, k: int) -> torch.Tensor:
         kbytes, align_elems, esize = k // 2, 32, 1
     else:
         if not k_major:
-            t = t.contiguous()
+            return _transpose_to_k_major(t, k)
         esize = t.element_size()
         kbytes, align_elems = k * esize, 16 // esize
     row_stride_bytes = t.stride(-2) * (1 if fp4 else esize)
@@ -84,6 +84,26 @@ def _to_kernel_operand(t: torch.Tensor, k: int) -> torch.Tensor:
     store_k = kpad // 2 if fp4 else kpad
     out = torch.zeros((*t.shape[:-1], store_k), dtype=t.dtype, device=t.device)
     out[..., :t.size(-1)] = t
+    return out
+
+
+def _transpose_to_k_major(t: torch.Tensor, k: int) -> torch.Tensor:
+    """MN-major [.., MN, K] view (stride(-2) == 1) -> new K-major [.., MN, align(K, 16 B)] tensor
+    (zero K padding), with the HIP transpose kernel."""
+    esize = t.element_size()
+    align_elems = 16 // esize
+    kpad = (k + align_elems - 1) // align_elems * align_elems
+    mn = t.size(-2)
+    if t.stride(-1) < mn:   # degenerate strides of a size-1 K axis: make the MN-major rows explicit
+        t = t.transpose(-2, -1).contiguous().transpose(-2, -1)
+    batches = t.size(0) if t.dim() == 3 else 1
+    out = torch.empty((*t.shape[:-2], mn, kpad), dtype=t.dtype, device=t.device)
+    if out.numel() == 0 or get_dry_run():
+        return out
+    lib = _lib.load()
+    _lib.check(lib.dg_transpose_to_k_major(
+        t.data_ptr(), esize, batches, t.stride(0) if t.dim() == 3 else 0, t.stride(-1), k, mn,
+        out.data_ptr(), mn * kpad, kpad, kpad, _stream(t)), lib)
     return out
 
 

@@ -144,6 +144,19 @@ int dg_transform_k_grouped_sf(const void *src, int32_t src_kind, int64_t stride_
                               int32_t gran_k, const int32_t *psum, int32_t num_groups, int32_t alignment,
                               int16_t *dst, int32_t *err_flag, void *stream);
 
+/*
+ * MN-major -> K-major operand copy.  The reference's kernels read MN-major operands in place
+ * (its TMA / fractal loaders, deep_gemm/include/deep_gemm/ascend/copy.hpp); this build's GEMM
+ * streams K-major rows, so an MN-major A / B (the tn / nn / tt layouts, K-grouped wgrad operands,
+ * einsum views) is transposed once with this entry point before dg_gemm.
+ * src element (b, k, mn) at src[b*src_batch_stride + k*src_ld + mn] (elements of elem_bytes = 1
+ * or 2); dst element (b, mn, k) at dst[b*dst_batch_stride + mn*dst_ld + k] for k < k_padded,
+ * zero for k >= k.  dst rows and batches 16-byte aligned.
+ */
+int dg_transpose_to_k_major(const void *src, int32_t elem_bytes, int32_t batches, int64_t src_batch_stride,
+                            int64_t src_ld, int32_t k, int32_t mn, void *dst, int64_t dst_batch_stride,
+                            int64_t dst_ld, int32_t k_padded, void *stream);
+
 /* Number of compute units of `device` (the reference's get_num_sms, csrc/apis/runtime.hpp:13-19). */
 int dg_device_num_cus(int32_t device);
 

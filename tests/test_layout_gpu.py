@@ -100,3 +100,29 @@ def test_transform_sf_invalid_flag(monkeypatch):
     sf = torch.full((8, 4), 1.5, device='cuda')
     with pytest.raises(RuntimeError, match='Invalid float32 SF'):
         deep_gemm.transform_sf_into_required_layout(sf, 8, 128, (1, 1, 32), is_sfa=True)
+
+
+@pytest.mark.parametrize('dtype', [torch.float8_e4m3fn, torch.bfloat16])
+@pytest.mark.parametrize('batch,k,mn', [(0, 64, 64), (0, 2048, 7168), (0, 100, 37), (3, 130, 257), (2, 1, 5), (0, 7, 300)])
+def test_transpose_to_k_major(dtype, batch, k, mn):
+    """MN-major -> K-major operand copy: bit-exact against torch's transpose, zero K padding."""
+    from deep_gemm.gemm import _transpose_to_k_major
+    g = torch.Generator().manual_seed(k + mn)
+    shape = (batch, k, mn) if batch else (k, mn)
+    raw = torch.randint(0, 255, shape, generator=g, dtype=torch.uint8)
+    src = raw.view(torch.float8_e4m3fn) if dtype != torch.bfloat16 else torch.randn(shape, generator=g).bfloat16()
+    # the caller's MN-major [.., MN, K] view of a [.., K, MN] tensor, with a padded K-row stride
+    big = torch.zeros((*shape[:-1], mn + 24), dtype=src.dtype) if dtype == torch.bfloat16 else \
+        torch.zeros((*shape[:-1], mn + 24), dtype=torch.uint8).view(src.dtype)
+    big[..., :mn] = src
+    view = big.cuda()[..., :mn].transpose(-2, -1)
+    out = _transpose_to_k_major(view, k)
+    torch.cuda.synchronize()
+    esize = src.element_size()
+    kpad = -(-k // (16 // esize)) * (16 // esize)
+    assert out.shape == (*shape[:-2], mn, kpad) and out.is_contiguous()
+    bits = torch.int16 if esize == 2 else torch.uint8
+    expect = src.transpose(-2, -1).contiguous().view(bits)
+    got = out.cpu().view(bits)
+    assert torch.equal(got[..., :k], expect)
+    assert int(got[..., k:].count_nonzero()) == 0
