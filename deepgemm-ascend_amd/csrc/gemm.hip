@@ -149,12 +149,12 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     // fp32 D of the same call, with the same K split and summation order.)
     const double hbm_bytes = esz * ((double)a.m + a.n) * a.k * groups + 2.0 * a.m * a.n * groups;
     double best = 1e300;
-    Plan pick = {{0, 0, 0, 0, 0, 0}, 1, ns};
+    Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0}, 1, ns};
     for (int i = 0; i < kNumTiles; ++i) {
         const TileCfg& tc = kTiles[i];
         if (!tile_allowed(a, tc.bm, tc.bn)) continue;
         const int64_t tiles = plan_tiles(a, tc);
-        const int max_split = allow_split && tiles <= kMaxSplitTiles ? std::min(16, std::max(1, ns / 4)) : 1;
+        const int max_split = allow_split && tile_splittable(tc) && tiles <= kMaxSplitTiles ? std::min(16, std::max(1, ns / 4)) : 1;
         for (int sp = 1; sp <= max_split; ++sp) {
             const int sps = ceil_div(ns, sp);
             const int s_eff = ceil_div(ns, sps);
@@ -202,10 +202,10 @@ Plan choose(const dg_gemm_args& a, int cus, bool allow_split) {
     const int ns = ceil_div(a.k, k_stage_elems(a.kind));
     allow_split = allow_split && split_capable(a);
     if (a.block_m > 0 && a.block_n > 0) {
-        TileCfg t = {a.block_m, a.block_n, 0, 0, 0, 0, 0};
+        TileCfg t = {a.block_m, a.block_n, 0, 0, 0, 0, 0, 0};
         for (const TileCfg& c : kTiles)
             if (c.bm == a.block_m && c.bn == a.block_n) t = c;
-        int sp = allow_split && a.split_k > 1 && plan_tiles(a, t) <= kMaxSplitTiles ? std::min(a.split_k, std::max(1, ns)) : 1;
+        int sp = allow_split && tile_splittable(t) && a.split_k > 1 && plan_tiles(a, t) <= kMaxSplitTiles ? std::min(a.split_k, std::max(1, ns)) : 1;
         const int sps = ceil_div(ns, sp);
         return {t, ceil_div(ns, sps), sps};
     }
@@ -225,7 +225,7 @@ Plan choose(const dg_gemm_args& a, int cus, bool allow_split) {
             g_memo.emplace(key, pl);
         }
     }
-    if (allow_split && a.split_k > 1 && plan_tiles(a, pl.tile) <= kMaxSplitTiles) {
+    if (allow_split && tile_splittable(pl.tile) && a.split_k > 1 && plan_tiles(a, pl.tile) <= kMaxSplitTiles) {
         // forced split count (tuning), on the heuristic's tile shape
         const int sps = ceil_div(ns, std::min(a.split_k, std::max(1, ns)));
         pl.split = ceil_div(ns, sps);

@@ -122,15 +122,25 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((v & 0xf) | ((v >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-// Slot swizzle inside one LDS row of SPR 16-byte slots (64-byte rows: 4 slots, 32-byte rows:
-// 2 slots).  Chosen so the 16 rows one ds_read_b128 phase touches (lanes r = 0..15 at a
-// fixed lane group) land on distinct 16-byte bank groups both for a 64 x 4-byte and a
-// 32 x 4-byte bank organisation.  Only row bits >= 1 are read, and a 4 KB block of slots
-// shifts rows by a multiple of 64, so a lane's swizzled slot is the same in every block.
+// Slot swizzle inside one LDS row of SPR 16-byte slots (128-byte rows: 8 slots, 64-byte: 4,
+// 32-byte: 2).  gfx950's LDS has 64 banks of 4 bytes and serves a ds_read_b128 in four phases
+// of 16 lanes; measured (per-lane-pair bank-conflict counts), the phases of lanes 0..31 are
+// {0-3, 12-15, 20-27} and {4-11, 16-19, 28-31} (lanes 32..63 alike).  With j = row / 4 those
+// are the rows of even and of odd popcount(j % 8).  A phase is conflict-free when its 16 lanes
+// (16 rows, one slot each) hit 16 distinct 16-byte bank groups of the 256-byte bank period:
+//   64-byte rows:  row % 4 picks the quarter, so the slot must differ over the four j of each
+//                  parity class: j % 4 does;
+//   128-byte rows: row % 2 picks the half, so the slot must differ over the eight rows of each
+//                  (parity class, row % 2): 2 (j % 4) + (row / 2) % 2 does;
+//   32-byte rows:  row % 8 picks the eighth, so rows r and r + 8 / r + 24 of a class must
+//                  differ: (row / 8) % 2 does.
+// Row steps of a load item are multiples of 32, so a lane's swizzled slot is the same for
+// every item.
 template <int SPR>
 __device__ __forceinline__ int slot_swizzle(int row) {
-    if constexpr (SPR == 4) return ((row >> 1) ^ (row >> 3)) & 3;
-    else return ((row >> 2) ^ (row >> 3)) & 1;
+    if constexpr (SPR == 8) return (((row >> 2) & 3) << 1) | ((row >> 1) & 1);
+    else if constexpr (SPR == 4) return (row >> 2) & 3;
+    else return (row >> 3) & 1;
 }
 
 // Buffer resource over [base, base + bytes); every field is forced wave-uniform (SGPRs) so no
@@ -178,34 +188,60 @@ __device__ __forceinline__ void swizzle_tile(int t, int nm, int nn, int gm, int&
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KIND, int EPI>
+template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int KIND, int EPI>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
     constexpr bool kBf16 = KIND == kBF16;
     constexpr int kFmtA = kAFp4 ? kFmtE2M1 : kFmtE4M3;
     constexpr int kFmtB = kBFp4 ? kFmtE2M1 : kFmtE4M3;
-    constexpr int KS = kBf16 ? 32 : 64;                  // K elements per stage
-    constexpr int RBA = kAFp4 ? 32 : 64;                 // bytes of one row per stage
-    constexpr int RBB = kBFp4 ? 32 : 64;
+    // A stage holds KM sub-steps of one MFMA K-step each (64 fp8 / fp4 or 32 bf16 elements).
+    // KM = 2 makes fp8 / bf16 rows 128 bytes per stage: every global load then fetches whole
+    // 128-byte lines (measured 1.5x the LDS-fill rate of 64-byte row pieces).
+    static_assert(KM == 1 || KM == 2, "sub-steps per stage");
+    constexpr int KS = (kBf16 ? 32 : 64) * KM;           // K elements per stage
+    constexpr int RBA = (kAFp4 ? 32 : 64) * KM;          // bytes of one row per stage
+    constexpr int RBB = (kBFp4 ? 32 : 64) * KM;
     constexpr int SPRA = RBA / 16, SPRB = RBB / 16;
+    // With three or more ring slots the next stage has landed while this one computes, so its
+    // first fragments are read ahead across the stage barrier.  A two-slot ring (128-K stages of
+    // the largest tiles, KM = 2) syncs late instead: once a stage's last fragments are in
+    // registers, before its last MFMA group, the waves wait for the next stage, meet at the
+    // barrier, refill the slot just drained and read the next stage's first fragments while
+    // that group's MFMAs run -- so no stage starts on an empty MFMA pipe.
+    constexpr bool kCross = NSTAGE >= 3;
+    constexpr bool kLate = NSTAGE == 2;
+    // Late-sync rings issue the next stage's loads spread over the first sub-step's MFMA groups
+    // (kSpread) or all at the sync point.
+    constexpr bool kSpread = false;
+    static_assert(!kLate || KM == 2, "two-slot rings need 128-byte stages");
     constexpr int NT = NW * 64;                          // threads per workgroup
     // The last LW waves issue every global->LDS load; with LW < NW the other waves only read
     // LDS and run MFMAs, so a stall in the load-issue path never blocks a whole SIMD.
     constexpr int LT = LW * 64, FW = NW - LW;            // loader threads, first loader wave
     static_assert(LW == NW || (NW == 8 && LW == 4), "loader waves");
     constexpr int WGN = NW / WGM;
-    constexpr int WM = BM / WGM, WN = BN / WGN;          // wave tile
+    constexpr int WM = BM / WGM;                         // wave tile rows
+    constexpr int WN = (BN / WGN + 31) / 32 * 32;        // wave tile columns (32-column blocks)
     constexpr int TM = WM / 32, TN = WN / 32;            // 32x32 MFMA blocks per wave
-    static_assert((NW == 4 || NW == 8) && WGM * WGN == NW && TM >= 1 && TN >= 1 && TM * 32 == WM && TN * 32 == WN, "wave tiling");
+    // Ragged wave tiling: the last wave column holds TN_LAST < TN blocks (256x224 = 4 + 3
+    // blocks of 32 columns).  Those waves are exactly the loader waves (waves 4..7 with 4 waves
+    // along M), and each SIMD runs one wave of each column, so every SIMD still issues the
+    // same number of MFMAs per stage while the loader waves carry fewer.
+    constexpr int TN_LAST = (BN - (WGN - 1) * WN) / 32;
+    constexpr bool kRagged = TN_LAST != TN;
+    static_assert((NW == 4 || NW == 8) && WGM * WGN == NW && TM >= 1 && TN >= 1 && TM * 32 == WM &&
+                      TN_LAST >= 1 && (WGN - 1) * WN + TN_LAST * 32 == BN, "wave tiling");
+    static_assert(!kRagged || (NW == 8 && LW == 4 && WGM == 4 && WGN == 2), "ragged tiling needs the loader waves as its last column");
     constexpr int A_BYTES = BM * RBA, B_BYTES = BN * RBB;
-    constexpr int SCA = kBf16 ? 0 : (BM * 2 + 255) / 256 * 256;   // one packed int16 per row
+    constexpr int SCA = kBf16 ? 0 : (BM * 2 + 255) / 256 * 256;   // one packed int16 per row and sub-step
     constexpr int SCB = kBf16 ? 0 : (BN * 2 + 255) / 256 * 256;
+    constexpr int SCU = SCA + SCB;                                 // scale bytes of one sub-step
     constexpr int NSCA = kBf16 ? 0 : (BM + 127) / 128, NSCB = kBf16 ? 0 : (BN + 127) / 128;
     // 256 idle bytes per stage that take the dead SF loads of waves without an SF row to fetch
     constexpr int SPARE = (!kBf16 && NSCA + NSCB < LW) ? 256 : 0;
-    constexpr int STAGE = A_BYTES + B_BYTES + SCA + SCB + SPARE;
-    static_assert(NSTAGE >= 3 && NSTAGE * STAGE <= 160 * 1024, "LDS budget");
+    constexpr int STAGE = A_BYTES + B_BYTES + KM * SCU + SPARE;
+    static_assert(NSTAGE >= 2 && NSTAGE * STAGE <= 160 * 1024, "LDS budget");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * STAGE];
 
     const int tid = threadIdx.x;
@@ -321,13 +357,14 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(b_base + (int64_t)n0 * ldb, (int64_t)rows_b * ldb);
     const int kbytes_a = p.gemm_type == kKGrouped ? k_len * (kAFp4 ? 1 : (kBf16 ? 4 : 2)) / 2 : p.kbytes_a;
     const int kbytes_b = p.gemm_type == kKGrouped ? k_len * (kBFp4 ? 1 : (kBf16 ? 4 : 2)) / 2 : p.kbytes_b;
-    // The ring walks an even number of virtual stages so the main loop is a pair of iterations
-    // with static register sets; an odd stage count gets one leading dead stage (all-zero
-    // operands and scales, so it adds nothing to the accumulators).
+    // With KM = 1 the ring walks an even number of virtual stages so the main loop is a pair of
+    // iterations with static register sets; an odd stage count gets one leading dead stage
+    // (all-zero operands and scales, so it adds nothing to the accumulators).  With KM = 2 the
+    // two sub-steps of every stage own the two register sets.
     // K stages of this workgroup: [c0, c0 + num_stages) of the whole K loop.
     const int c0 = split * p.split_stages;
     const int num_stages = p.split_k > 1 ? min(p.split_stages, ceil_div(k_len, KS) - c0) : ceil_div(k_len, KS);
-    const int shift = num_stages & 1;
+    const int shift = KM == 1 ? (num_stages & 1) : 0;
     const int num_virtual = num_stages + shift;
     const int nk64 = ceil_div(k_len, 64);
 
@@ -337,12 +374,12 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     // offset rides in the scalar soffset, so the per-lane voffset is stage-invariant.
     constexpr int SLA = BM * SPRA, SLB = BN * SPRB;                    // 16-byte slots per stage
     constexpr int NLA = (SLA + LT - 1) / LT, NLB = (SLB + LT - 1) / LT;  // per-thread loads
-    // Packed SF rows: one buffer_load_dword ... lds per 128 rows of the tile, issued by waves
-    // 0 .. NSCA-1 (A) and NSCA .. NSCA+NSCB-1 (B).
+    // Packed SF rows: one buffer_load_dword ... lds per 128 rows of the tile and sub-step,
+    // issued by waves 0 .. NSCA-1 (A) and NSCA .. NSCA+NSCB-1 (B).
     static_assert(NSCA + NSCB <= LW, "scale loads per stage");
-    constexpr int NL = NLA + NLB + (kBf16 ? 0 : 1);
+    constexpr int NL = NLA + NLB + (kBf16 ? 0 : KM);
     // Loads that every wave issues per stage (the waits below count the smallest number).
-    constexpr int kMinLoadsPerStage = (SLA / LT) + (SLB / LT) + (kBf16 ? 0 : 1);
+    constexpr int kMinLoadsPerStage = (SLA / LT) + (SLB / LT) + (kBf16 ? 0 : KM);
 
     // Per-lane byte offset of the thread's first 16-byte slot of the A / B stage and the K piece
     // it covers; load item `it` adds it * LT / SPR rows through the scalar offset.
@@ -374,7 +411,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
         sc_voff = (sc_live && row < (is_a ? rows_a : rows_b)) ? (uint32_t)(row * 2) : kOOBOffset;
         sc_step = __builtin_amdgcn_readfirstlane((int)((is_a ? p.sfa_ld : p.sfb_ld) * 2));
         sc_lds = __builtin_amdgcn_readfirstlane(sc_live ? A_BYTES + B_BYTES + (is_a ? 0 : SCA) + w * 256
-                                                        : A_BYTES + B_BYTES + SCA + SCB);
+                                                        : A_BYTES + B_BYTES + KM * SCU);
     }
     constexpr int kDeadOffset = 0x40000000;   // scalar offset that moves every lane out of range
 
@@ -400,9 +437,13 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
                 kIsA ? rs_a : rs_b, (lds_void*)(sbase + (kIsA ? 0 : A_BYTES) + (it * LT + lwave * 64) * 16), 16,
                 voff, __builtin_amdgcn_readfirstlane(live ? soff : kDeadOffset), 0, 0);
         } else if constexpr (!kBf16) {
-            // packed-SF row of stage c (its k64 index is c)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_sc, (lds_void*)(sbase + sc_lds), 4, sc_voff,
-                                                     __builtin_amdgcn_readfirstlane((live & sc_live) ? c * sc_step : kDeadOffset),
+            // packed-SF row of sub-step u of stage c (its k64 index is c * KM + u); a dead load
+            // lands in the spare word, whatever u
+            constexpr int u = IDX - NLA - NLB;
+            const bool on = live & sc_live;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_sc, (lds_void*)(sbase + sc_lds + (sc_live ? u * SCU : 0)), 4,
+                                                     sc_voff,
+                                                     __builtin_amdgcn_readfirstlane(on ? (c * KM + u) * sc_step : kDeadOffset),
                                                      0, 0);
         }
     };
@@ -415,22 +456,23 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
         constexpr int SPR = decltype(spr_tag)::value;
         return R * (SPR * 16) + ((slot ^ slot_swizzle<SPR>(R)) << 4);
     };
-    // 32 bytes (fp8: K [16q,+16) and [32+16q,+16); bf16: k-steps 0 and 1) or 16 bytes (fp4).
-    auto load_frag = [&](const uint8_t* base, int R, auto spr_tag) -> i32x8 {
+    // Sub-step u of row R: 32 bytes (fp8: K [16q,+16) and [32+16q,+16) of the sub-step; bf16:
+    // its k-steps 0 and 1) or 16 bytes (fp4).  A sub-step spans 64 row bytes (32 for fp4).
+    auto load_frag = [&](const uint8_t* base, int R, auto spr_tag, auto u_tag) -> i32x8 {
         constexpr int SPR = decltype(spr_tag)::value;
-        const i32x4 lo = *reinterpret_cast<const i32x4*>(base + frag_addr(R, q, spr_tag));
-        if constexpr (SPR == 4) {
-            const i32x4 hi = *reinterpret_cast<const i32x4*>(base + frag_addr(R, 2 + q, spr_tag));
+        constexpr int u = decltype(u_tag)::value;
+        constexpr int P = SPR / KM;                      // 16-byte slots per sub-step
+        const i32x4 lo = *reinterpret_cast<const i32x4*>(base + frag_addr(R, u * P + q, spr_tag));
+        if constexpr (P == 4) {
+            const i32x4 hi = *reinterpret_cast<const i32x4*>(base + frag_addr(R, u * P + 2 + q, spr_tag));
             return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         } else {
             return i32x8{lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
         }
     };
-    // UE8M0 byte of K-block q of row R (one packed int16 per row in the stage's scale area).
-    auto load_scale = [&](const uint8_t* sc, int R) -> int {
-        const uint32_t v = *reinterpret_cast<const uint16_t*>(sc + R * 2);
-        return (int)((v >> (8 * q)) & 0xffu);
-    };
+    // UE8M0 byte of K-block q of row R (one packed int16 per row in the sub-step's scale area,
+    // K-block 0 in the low byte): a byte read, consumed by the MFMA as it is.
+    auto load_scale = [&](const uint8_t* sc, int R) -> int { return sc[R * 2 + q]; };
 
     f32x16 acc[TN][TM];
 #pragma unroll
@@ -438,51 +480,71 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
 
-    // Register sets `buf` = 0 / 1 alternate between stages: A-side fragments and scales of the
-    // whole wave tile plus the first B-side block, all read one stage ahead.
+    // Register sets `buf` = 0 / 1 alternate between sub-steps (KM = 1: between stages): A-side
+    // fragments and scales of the whole wave tile plus the first B-side block, all read one
+    // sub-step ahead.
     i32x8 fa[2][TM];
     int sa[2][TM];
     i32x8 fb0[2];
     int sb0[2];
-    auto load_ahead = [&](int s, auto part_tag) {
+    auto load_ahead = [&](int s, auto part_tag, auto u_tag) {
         constexpr int part = decltype(part_tag)::value;   // TM: the B block, else A block `part`
+        constexpr int u = decltype(u_tag)::value;
         const uint8_t* st = smem + s * STAGE;
+        const uint8_t* sc = st + A_BYTES + B_BYTES + u * SCU;
         if constexpr (part < TM) {
             const int R = wm * WM + part * 32 + r;
-            return std::pair<i32x8, int>(load_frag(st, R, Int<SPRA>{}),
-                                         kBf16 ? 0 : load_scale(st + A_BYTES + B_BYTES, R));
+            return std::pair<i32x8, int>(load_frag(st, R, Int<SPRA>{}, u_tag), kBf16 ? 0 : load_scale(sc, R));
         } else {
             const int R = wn * WN + r;
-            return std::pair<i32x8, int>(load_frag(st + A_BYTES, R, Int<SPRB>{}),
-                                         kBf16 ? 0 : load_scale(st + A_BYTES + B_BYTES + SCA, R));
+            return std::pair<i32x8, int>(load_frag(st + A_BYTES, R, Int<SPRB>{}, u_tag),
+                                         kBf16 ? 0 : load_scale(sc + SCA, R));
         }
     };
-    auto prefetch = [&](int s, auto buf_tag, auto part_tag) {
+    auto prefetch = [&](int s, auto buf_tag, auto part_tag, auto u_tag) {
         constexpr int buf = decltype(buf_tag)::value;
         constexpr int part = decltype(part_tag)::value;
-        const auto v = load_ahead(s, part_tag);
+        const auto v = load_ahead(s, part_tag, u_tag);
         if constexpr (part < TM) { fa[buf][part] = v.first; sa[buf][part] = v.second; }
         else { fb0[buf] = v.first; sb0[buf] = v.second; }
     };
 
-    // One stage of MFMAs from ring slot s with the registers of set `buf`; reads the ahead
-    // registers of the next stage (slot sn) into the other set and issues the loads of stage cl
+    // Sub-step u of the stage in ring slot s with the registers of set `buf`.  Reads the ahead
+    // registers of the next sub-step (u + 1 of this slot, or sub-step 0 of slot sn when the ring
+    // crosses stages) into the other set, and -- in sub-step 0 -- issues the loads of stage cl
     // into slot sl, all interleaved with the MFMA groups (one group = the TM blocks of one jn).
-    constexpr int kLPG = (NL + TN - 1) / TN;
-    auto compute = [&](int s, auto buf_tag, auto loads_tag, int sn, int cl, int sl, bool load_live) {
+    // TNX = the wave's number of 32-column blocks (TN, or TN_LAST in the last wave column).
+    auto compute = [&](int s, auto u_tag, auto buf_tag, auto loads_tag, auto tnx_tag, int sn, int cl, int sl,
+                       bool load_live) {
+        constexpr int u = decltype(u_tag)::value;
         constexpr int buf = decltype(buf_tag)::value;
-        constexpr bool kLoads = decltype(loads_tag)::value != 0;
+        constexpr bool kLoadWave = decltype(loads_tag)::value != 0;
+        constexpr bool kLoads = kLoadWave && u == 0 && (!kLate || kSpread);
+        constexpr int TNX = decltype(tnx_tag)::value;
+        constexpr int kLPG = (NL + TNX - 1) / TNX;
+        constexpr bool kAhead = u + 1 < KM || kCross;
         const uint8_t* sB = smem + s * STAGE + A_BYTES;
-        const uint8_t* sSB = smem + s * STAGE + A_BYTES + B_BYTES + SCA;
+        const uint8_t* sSB = smem + s * STAGE + A_BYTES + B_BYTES + u * SCU + SCA;
         i32x8 fb_cur = fb0[buf];
         int sb_cur = sb0[buf];
-        static_for<TN>([&](auto jn_c) {
+        static_for<TNX>([&](auto jn_c) {
             constexpr int jn = decltype(jn_c)::value;
             i32x8 fb_next = fb_cur;
             int sb_next = sb_cur;
-            if constexpr (jn + 1 < TN) {
-                fb_next = load_frag(sB, wn * WN + (jn + 1) * 32 + r, Int<SPRB>{});
+            if constexpr (jn + 1 < TNX) {
+                fb_next = load_frag(sB, wn * WN + (jn + 1) * 32 + r, Int<SPRB>{}, u_tag);
                 if constexpr (!kBf16) sb_next = load_scale(sSB, wn * WN + (jn + 1) * 32 + r);
+            }
+            if constexpr (kLate && u + 1 == KM && jn + 1 == TNX) {
+                // late sync: this stage's slot s is no longer read by anyone after the barrier
+                // and stage cl - 1 has landed; refill s with stage cl and read stage cl - 1's
+                // first fragments (slot sn) into the sub-step-0 registers
+                wait_vmcnt<0>();
+                stage_barrier();
+                static_for<TM + 1>([&](auto part_c) { prefetch(sn, Int<0>{}, part_c, Int<0>{}); });
+                // (the reads go out before this group's MFMAs, which then cover their latency)
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (kLoadWave && !kSpread) issue_stage(cl, sl, load_live);
             }
             static_for<TM>([&](auto jm_c) {
                 constexpr int jm = decltype(jm_c)::value;
@@ -500,14 +562,19 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
                         fb_cur, fa[buf][jm], acc[jn][jm], kFmtB, kFmtA, 0, sb_cur, 0, sa[buf][jm]);
                 }
             });
-            // ahead registers of the next stage: A block jm goes with group jm * TN / TM, the
-            // first B block with the last group (slot sn is always readable; a stage past the
-            // end reads stale bytes that are never used)
-            static_for<TM + 1>([&](auto part_c) {
-                constexpr int part = decltype(part_c)::value;
-                constexpr int grp = part < TM ? part * TN / TM : TN - 1;
-                if constexpr (grp == jn) prefetch(sn, Int<buf ^ 1>{}, Int<part>{});
-            });
+            // ahead registers of the next sub-step: A block jm goes with group jm * TNX / TM, the
+            // first B block with the last group (a cross-stage read of slot sn past the last
+            // stage reads stale bytes that are never used)
+            if constexpr (kAhead) {
+                static_for<TM + 1>([&](auto part_c) {
+                    constexpr int part = decltype(part_c)::value;
+                    constexpr int grp = part < TM ? part * TNX / TM : TNX - 1;
+                    if constexpr (grp == jn) {
+                        if constexpr (u + 1 < KM) prefetch(s, Int<buf ^ 1>{}, Int<part>{}, Int<u + 1>{});
+                        else prefetch(sn, Int<buf ^ 1>{}, Int<part>{}, Int<0>{});
+                    }
+                });
+            }
             static_for<kLPG>([&](auto li) {
                 constexpr int idx = jn * kLPG + decltype(li)::value;
                 if constexpr (kLoads && idx < NL) issue_item(Int<idx>{}, cl, sl, load_live);
@@ -519,39 +586,61 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     };
 
     // ------------------------------------------------------------------ main loop
-    // Prologue: stages 0 .. NSTAGE-2 in flight, stage 0 visible, its ahead registers loaded.
-    static_for<NSTAGE - 1>([&](auto i) {
+    // Prologue: stages 0 .. NSTAGE-2 in flight; with a cross-stage ring, stage 0 visible and its
+    // ahead registers loaded.
+    // (A two-slot ring fills both slots.)
+    constexpr int kPro = kLate && !kSpread ? 2 : NSTAGE - 1;
+    static_for<kPro>([&](auto i) {
         constexpr int st = decltype(i)::value;
         if (is_loader) issue_stage(c0 + st - shift, st, st >= shift && st < num_virtual);
     });
-    wait_vmcnt<(NSTAGE - 2) * kMinLoadsPerStage>();
-    stage_barrier();
-    static_for<TM + 1>([&](auto part_c) { prefetch(0, Int<0>{}, part_c); });
-
-    // Stage c + 1 must have landed before the barrier of iteration c (its ahead registers are
-    // read during stage c); the loads of stages c + 2 .. c + NSTAGE - 2 may stay in flight.
-    // The barrier also certifies that every wave finished reading stage c - 1 (its B side in
-    // iteration c - 1, its ahead registers in iteration c - 2), so its slot can take stage
-    // c + NSTAGE - 1.
-    auto iteration = [&](int c, auto buf_tag, auto loads_tag) {
-        wait_vmcnt<(NSTAGE - 3) * kMinLoadsPerStage>();
+    if constexpr (kCross || kLate) {
+        wait_vmcnt<(kPro - 1) * kMinLoadsPerStage>();
         stage_barrier();
-        const int cl = c + NSTAGE - 1;
-        compute(c % NSTAGE, buf_tag, loads_tag, (c + 1) % NSTAGE, c0 + cl - shift, cl % NSTAGE, cl < num_virtual);
+        static_for<TM + 1>([&](auto part_c) { prefetch(0, Int<0>{}, part_c, Int<0>{}); });
+    }
+
+    // Cross-stage ring: stage c + 1 must have landed before the barrier of iteration c (its ahead
+    // registers are read during stage c); the loads of stages c + 2 .. c + NSTAGE - 2 may stay in
+    // flight.  The barrier also certifies that every wave finished reading stage c - 1 (its B
+    // side in iteration c - 1, its ahead registers in iteration c - 2), so its slot can take
+    // stage c + NSTAGE - 1.  Otherwise stage c must have landed (stages c + 1 .. c + NSTAGE - 2
+    // may be in flight), the barrier certifies that stage c - 1 is no longer read, and the
+    // stage's first fragments are read after it.  A late-sync ring has no barrier here: it met
+    // before the previous stage's last MFMA group (see compute).
+    auto iteration = [&](int c, auto pbuf_tag, auto loads_tag, auto tnx_tag) {
+        if constexpr (!kLate) {
+            wait_vmcnt<(NSTAGE - (kCross ? 3 : 2)) * kMinLoadsPerStage>();
+            stage_barrier();
+        }
+        const int cl = c + (kLate && !kSpread ? 2 : NSTAGE - 1);
+        constexpr int buf0 = KM == 1 ? decltype(pbuf_tag)::value : 0;
+        if constexpr (!kCross && !kLate)
+            static_for<TM + 1>([&](auto part_c) { prefetch(c % NSTAGE, Int<buf0>{}, part_c, Int<0>{}); });
+        static_for<KM>([&](auto u_c) {
+            constexpr int u = decltype(u_c)::value;
+            constexpr int buf = KM == 1 ? decltype(pbuf_tag)::value : u;
+            compute(c % NSTAGE, u_c, Int<buf>{}, loads_tag, tnx_tag, (c + 1) % NSTAGE, c0 + cl - shift, cl % NSTAGE,
+                    cl < num_virtual);
+        });
     };
     // Loader and non-loader waves run separate copies of the loop, each branch-free.
-    auto main_loop = [&](auto loads_tag) {
-        for (int c = 0; c < num_virtual; c += 2) {
-            iteration(c, Int<0>{}, loads_tag);
-            iteration(c + 1, Int<1>{}, loads_tag);
+    auto main_loop = [&](auto loads_tag, auto tnx_tag) {
+        if constexpr (KM == 1) {
+            for (int c = 0; c < num_virtual; c += 2) {
+                iteration(c, Int<0>{}, loads_tag, tnx_tag);
+                iteration(c + 1, Int<1>{}, loads_tag, tnx_tag);
+            }
+        } else {
+            for (int c = 0; c < num_virtual; ++c) iteration(c, Int<0>{}, loads_tag, tnx_tag);
         }
     };
-    if (LW == NW || is_loader) main_loop(Int<1>{});
-    else main_loop(Int<0>{});
+    if (LW == NW || is_loader) main_loop(Int<1>{}, Int<TN_LAST>{});   // loaders = the last wave column
+    else main_loop(Int<0>{}, Int<TN>{});
     __builtin_amdgcn_s_waitcnt(0);
 
     // ------------------------------------------------------------------ split-K reduction
-    if (p.split_k > 1) {
+    if (!kRagged && p.split_k > 1) {   // (the host never splits a ragged tile)
         // This workgroup's partial tile, in accumulator-register order (coalesced 16-byte
         // stores and loads; the reducing workgroup uses the same lane mapping).
         float* const tile_ws = p.ws + (int64_t)tile_id * p.split_k * (BM * BN);
@@ -640,6 +729,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
         OutT* drow = dbase + (int64_t)m * p.ldd;
         static_for<TN>([&](auto jn_c) {
             constexpr int jn = decltype(jn_c)::value;
+            if (kRagged && jn >= TN_LAST && wn == WGN - 1) return;   // no such block in this wave
             const int nblk = n0 + wn * WN + jn * 32;                  // wave-uniform
             // the lane holds columns nblk + 8 g + 4 q + {0..3} in elements 4 g + {0..3}
             float v[16];

@@ -15,30 +15,37 @@ struct TileCfg {
     int nw;       // waves per workgroup: 8 = two per SIMD, so one wave's MFMAs issue while the
                   // other waits on loads; 4 where a 4-wave tile needs more than 256 registers
     int lw;       // waves that issue the global->LDS loads (nw, or 4 of 8)
-    int stages;   // depth of the LDS ring (64-K stages; deeper for small tiles to keep more
-                  // bytes in flight per CU)
-    int stage_cycles;   // measured cycles per 64-K stage with every CU busy (fp8, MI355X)
+    int stages;   // depth of the LDS ring (deeper for small tiles to keep more bytes in flight
+                  // per CU)
+    int km;       // MFMA K-steps per stage: 2 = 128-byte fp8 rows (whole-line loads), 1 = 64
+    int stage_cycles;   // measured cycles per 64 K with every CU busy (fp8, MI355X)
 };
 
 // Measured on MI355X at M=4096, N=7168, K=2048 (fp8): 256x256/8 waves (4 loaders) 63 us, 256x224/4 waves
 // 75 us, 128x128/4 waves 76 us; at M=128, N=7168, K=7168: 64x128 35 us, 128x128 44 us.
 constexpr TileCfg kTiles[] = {
-    {256, 256, 4, 8, 4, 4, 1380}, {256, 224, 4, 4, 4, 4, 1743}, {256, 128, 4, 8, 8, 4, 937},
-    {128, 256, 2, 8, 8, 4, 985},  {128, 128, 2, 4, 4, 4, 1056}, {64, 128, 2, 4, 4, 8, 588},
-    {32, 128, 1, 4, 4, 8, 643},
+    {256, 256, 4, 8, 4, 2, 2, 1380}, {256, 224, 4, 8, 4, 2, 2, 1250}, {256, 128, 4, 8, 8, 4, 1, 937},
+    {128, 256, 2, 8, 8, 4, 1, 985},  {128, 128, 2, 4, 4, 4, 1, 1056}, {64, 128, 2, 4, 4, 8, 1, 588},
+    {32, 128, 1, 4, 4, 8, 1, 643},
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
+
+// Split-K runs on tiles with 64-K stages whose waves split N into equal 32-column multiples (a
+// ragged tile -- 256x224 over two wave columns: 128 + 96 -- keeps no split-K partial layout).
+constexpr bool tile_splittable(const TileCfg& t) {
+    return t.nw == 0 || (t.km == 1 && (t.bn / (t.nw / t.wgm)) % 32 == 0);
+}
 
 template <int I, int KIND>
 KernelFn pick_epi(int epi) {
     constexpr TileCfg t = kTiles[I];
     switch (epi) {
-        case kEpiF32: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiF32>;
-        case kEpiBf16: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiBf16>;
-        case kEpiBf16SR: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiBf16SR>;
+        case kEpiF32: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, KIND, kEpiF32>;
+        case kEpiBf16: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, KIND, kEpiBf16>;
+        case kEpiBf16SR: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, KIND, kEpiBf16SR>;
         case kEpiFp8:
             // FP8 output exists for e4m3 x e4m3 batched / dense GEMMs only (fp8_bmm)
-            if constexpr (KIND == kFP8FP8) return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, KIND, kEpiFp8>;
+            if constexpr (KIND == kFP8FP8) return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, KIND, kEpiFp8>;
             else return nullptr;
         default: return nullptr;
     }
