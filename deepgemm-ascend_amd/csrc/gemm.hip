@@ -149,7 +149,7 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     // fp32 D of the same call, with the same K split and summation order.)
     const double hbm_bytes = esz * ((double)a.m + a.n) * a.k * groups + 2.0 * a.m * a.n * groups;
     double best = 1e300;
-    Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0}, 1, ns};
+    Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0, 0}, 1, ns};
     for (int i = 0; i < kNumTiles; ++i) {
         const TileCfg& tc = kTiles[i];
         if (!tile_allowed(a, tc.bm, tc.bn)) continue;
@@ -160,13 +160,14 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
             const int s_eff = ceil_div(ns, sps);
             if (sp > 1 && s_eff != sp) continue;
             // The splits of a tile run on one XCD (kXcds of them, cus / kXcds CUs each).
-            const int64_t rounds = sp == 1 ? ceil_div64(tiles, cus)
+            const int64_t rounds = sp == 1 ? ceil_div64(tiles, (int64_t)cus * tc.occ)
                                            : ceil_div64(ceil_div64(tiles, kXcds) * sp, std::max(1, cus / kXcds));
             if (sp > 1 && rounds > 1) break;
             // Waves of workgroups x (their K stages at the tile's measured stage time + the
             // fixed cost of a tile: pipeline fill and the epilogue's stores), plus the split
             // reduction (measured ~10K cycles: partial stores, arrival count, partial reads).
-            double t = (double)rounds * ((double)sps * tc.stage_cycles + 6000.0 + tc.bm * tc.bn / 8.0);
+            // (co-resident workgroups share the CU's MFMAs but overlap each other's fixed costs)
+            double t = (double)rounds * ((double)tc.occ * sps * tc.stage_cycles + 6000.0 + tc.bm * tc.bn / 8.0);
             double bytes = hbm_bytes;
             if (sp > 1) {
                 t += 10000.0 + 500.0 * sp;
@@ -202,7 +203,7 @@ Plan choose(const dg_gemm_args& a, int cus, bool allow_split) {
     const int ns = ceil_div(a.k, k_stage_elems(a.kind));
     allow_split = allow_split && split_capable(a);
     if (a.block_m > 0 && a.block_n > 0) {
-        TileCfg t = {a.block_m, a.block_n, 0, 0, 0, 0, 0, 0};
+        TileCfg t = {a.block_m, a.block_n, 0, 0, 0, 0, 0, 0, 0};
         for (const TileCfg& c : kTiles)
             if (c.bm == a.block_m && c.bn == a.block_n) t = c;
         int sp = allow_split && tile_splittable(t) && a.split_k > 1 && plan_tiles(a, t) <= kMaxSplitTiles ? std::min(a.split_k, std::max(1, ns)) : 1;
@@ -371,7 +372,8 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     p.num_m_blocks = ceil_div(a.m, cfg.bm);
     p.num_n_blocks = ceil_div(a.n, cfg.bn);
     p.kbytes_a = (int)kbytes_a; p.kbytes_b = (int)kbytes_b;
-    p.group_m = 4;
+    static const int group_m_env = std::getenv("DG_GROUP_M") ? std::atoi(std::getenv("DG_GROUP_M")) : 0;   // tuning
+    p.group_m = group_m_env > 0 ? group_m_env : 4;
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
     const int64_t tiles = (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
     if (tiles <= 0) return DG_OK;

@@ -188,8 +188,9 @@ __device__ __forceinline__ void swizzle_tile(int t, int nm, int nn, int gm, int&
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int KIND, int EPI>
-__global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
+// OCC = workgroups per CU the kernel is compiled for (its waves per SIMD bound its registers).
+template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI>
+__global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KParams p) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
     constexpr bool kBf16 = KIND == kBF16;
@@ -241,7 +242,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const KParams p) {
     // 256 idle bytes per stage that take the dead SF loads of waves without an SF row to fetch
     constexpr int SPARE = (!kBf16 && NSCA + NSCB < LW) ? 256 : 0;
     constexpr int STAGE = A_BYTES + B_BYTES + KM * SCU + SPARE;
-    static_assert(NSTAGE >= 2 && NSTAGE * STAGE <= 160 * 1024, "LDS budget");
+    static_assert(NSTAGE >= 2 && NSTAGE * STAGE * OCC <= 160 * 1024, "LDS budget");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * STAGE];
 
     const int tid = threadIdx.x;

@@ -18,15 +18,18 @@ struct TileCfg {
     int stages;   // depth of the LDS ring (deeper for small tiles to keep more bytes in flight
                   // per CU)
     int km;       // MFMA K-steps per stage: 2 = 128-byte fp8 rows (whole-line loads), 1 = 64
+    int occ;      // workgroups per CU (2: LDS ring and registers sized for two co-resident
+                  // workgroups, whose prologues and epilogues then overlap each other's main loops)
     int stage_cycles;   // measured cycles per 64 K with every CU busy (fp8, MI355X)
 };
 
-// Measured on MI355X at M=4096, N=7168, K=2048 (fp8): 256x256/8 waves (4 loaders) 63 us, 256x224/4 waves
-// 75 us, 128x128/4 waves 76 us; at M=128, N=7168, K=7168: 64x128 35 us, 128x128 44 us.
+// Measured on MI355X (fp8, cold L2): 4096x7168x2048 256x224 70 us, 256x256 72 us; M-grouped contiguous (32
+// experts, ~257 rows each, alignment 128) N=4096 K=7168: 128x256 as 8 waves / one workgroup per CU 572 us, as
+// 4 waves / two workgroups per CU 509 us; skinny M=128, N=7168, K=16384: 128x128 split 4 57 us.
 constexpr TileCfg kTiles[] = {
-    {256, 256, 4, 8, 4, 2, 2, 1380}, {256, 224, 4, 8, 4, 2, 2, 1250}, {256, 128, 4, 8, 8, 4, 1, 937},
-    {128, 256, 2, 8, 8, 4, 1, 985},  {128, 128, 2, 4, 4, 4, 1, 1056}, {64, 128, 2, 4, 4, 8, 1, 588},
-    {32, 128, 1, 4, 4, 8, 1, 643},
+    {256, 256, 4, 8, 4, 2, 2, 1, 1380}, {256, 224, 4, 8, 4, 2, 2, 1, 1250}, {256, 128, 4, 8, 8, 4, 1, 1, 937},
+    {128, 256, 2, 4, 4, 3, 1, 2, 985},  {128, 128, 2, 4, 4, 4, 1, 1, 1056}, {64, 128, 2, 4, 4, 6, 1, 2, 588},
+    {32, 128, 1, 4, 4, 6, 1, 2, 643},
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -40,12 +43,12 @@ template <int I, int KIND>
 KernelFn pick_epi(int epi) {
     constexpr TileCfg t = kTiles[I];
     switch (epi) {
-        case kEpiF32: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, KIND, kEpiF32>;
-        case kEpiBf16: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, KIND, kEpiBf16>;
-        case kEpiBf16SR: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, KIND, kEpiBf16SR>;
+        case kEpiF32: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiF32>;
+        case kEpiBf16: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiBf16>;
+        case kEpiBf16SR: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiBf16SR>;
         case kEpiFp8:
             // FP8 output exists for e4m3 x e4m3 batched / dense GEMMs only (fp8_bmm)
-            if constexpr (KIND == kFP8FP8) return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, KIND, kEpiFp8>;
+            if constexpr (KIND == kFP8FP8) return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiFp8>;
             else return nullptr;
         default: return nullptr;
     }
