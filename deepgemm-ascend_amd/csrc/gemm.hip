@@ -82,7 +82,8 @@ struct Plan {
     int split_stages;   // K stages per range
 };
 
-int k_stage_elems(int kind) { return kind == kBF16 ? 32 : 64; }
+// K elements of one kernel stage of tile t
+int k_stage_elems(int kind, const TileCfg& t) { return (kind == kBF16 ? 32 : 64) * std::max(1, t.km); }
 
 // Split-K is offered to dense / batched GEMMs whose tiles alone cannot fill the CUs.
 bool split_capable(const dg_gemm_args& a) { return a.gemm_type == kNormal || a.gemm_type == kBatched; }
@@ -122,7 +123,7 @@ bool skinny_plan(const dg_gemm_args& a, int cus, bool allow_split, Plan& out) {
     if (t64 == nullptr || t128 == nullptr) return false;
     const TileCfg& tc = plan_tiles(a, *t64) > cus && a.m > 64 ? *t128 : *t64;
     const int64_t tiles = plan_tiles(a, tc);
-    const int ns = ceil_div(a.k, k_stage_elems(a.kind));
+    const int ns = ceil_div(a.k, k_stage_elems(a.kind, tc));
     int sp = 1;
     if (allow_split && a.k > 2048 && tiles <= kMaxSplitTiles) {
         sp = (a.k + 1024) / 2048;
@@ -142,17 +143,17 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
     // (K-grouped: each tile contracts one group's share of K)
     const int k_tile = a.gemm_type == kKGrouped ? ceil_div(a.k, std::max(1, a.num_groups)) : a.k;
-    const int ns = ceil_div(k_tile, k_stage_elems(a.kind));
     // HBM floor: operands once, D once (8 TB/s at ~2.1 GHz is ~3800 bytes per cycle).
     const double esz = a.kind == kBF16 ? 2.0 : 1.0;
     // (The plan must not depend on D's dtype: a bf16 D is then exactly the RNE rounding of the
     // fp32 D of the same call, with the same K split and summation order.)
     const double hbm_bytes = esz * ((double)a.m + a.n) * a.k * groups + 2.0 * a.m * a.n * groups;
     double best = 1e300;
-    Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0, 0}, 1, ns};
+    Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0, 0}, 1, 1};
     for (int i = 0; i < kNumTiles; ++i) {
         const TileCfg& tc = kTiles[i];
         if (!tile_allowed(a, tc.bm, tc.bn)) continue;
+        const int ns = ceil_div(k_tile, k_stage_elems(a.kind, tc));
         const int64_t tiles = plan_tiles(a, tc);
         const int max_split = allow_split && tile_splittable(tc) && tiles <= kMaxSplitTiles ? std::min(16, std::max(1, ns / 4)) : 1;
         for (int sp = 1; sp <= max_split; ++sp) {
@@ -167,7 +168,7 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
             // fixed cost of a tile: pipeline fill and the epilogue's stores), plus the split
             // reduction (measured ~10K cycles: partial stores, arrival count, partial reads).
             // (co-resident workgroups share the CU's MFMAs but overlap each other's fixed costs)
-            double t = (double)rounds * ((double)tc.occ * sps * tc.stage_cycles + 6000.0 + tc.bm * tc.bn / 8.0);
+            double t = (double)rounds * ((double)tc.occ * sps * tc.km * tc.stage_cycles + 6000.0 + tc.bm * tc.bn / 8.0);
             double bytes = hbm_bytes;
             if (sp > 1) {
                 t += 10000.0 + 500.0 * sp;
@@ -200,12 +201,12 @@ std::mutex g_memo_mu;
 std::unordered_map<MemoKey, Plan, MemoHash> g_memo;
 
 Plan choose(const dg_gemm_args& a, int cus, bool allow_split) {
-    const int ns = ceil_div(a.k, k_stage_elems(a.kind));
     allow_split = allow_split && split_capable(a);
     if (a.block_m > 0 && a.block_n > 0) {
         TileCfg t = {a.block_m, a.block_n, 0, 0, 0, 0, 0, 0, 0};
         for (const TileCfg& c : kTiles)
             if (c.bm == a.block_m && c.bn == a.block_n) t = c;
+        const int ns = ceil_div(a.k, k_stage_elems(a.kind, t));
         int sp = allow_split && tile_splittable(t) && a.split_k > 1 && plan_tiles(a, t) <= kMaxSplitTiles ? std::min(a.split_k, std::max(1, ns)) : 1;
         const int sps = ceil_div(ns, sp);
         return {t, ceil_div(ns, sps), sps};
@@ -228,6 +229,7 @@ Plan choose(const dg_gemm_args& a, int cus, bool allow_split) {
     }
     if (allow_split && tile_splittable(pl.tile) && a.split_k > 1 && plan_tiles(a, pl.tile) <= kMaxSplitTiles) {
         // forced split count (tuning), on the heuristic's tile shape
+        const int ns = ceil_div(a.k, k_stage_elems(a.kind, pl.tile));
         const int sps = ceil_div(ns, std::min(a.split_k, std::max(1, ns)));
         pl.split = ceil_div(ns, sps);
         pl.split_stages = sps;

@@ -33,11 +33,9 @@ constexpr TileCfg kTiles[] = {
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-// Split-K runs on tiles with 64-K stages whose waves split N into equal 32-column multiples (a
-// ragged tile -- 256x224 over two wave columns: 128 + 96 -- keeps no split-K partial layout).
-constexpr bool tile_splittable(const TileCfg& t) {
-    return t.nw == 0 || (t.km == 1 && (t.bn / (t.nw / t.wgm)) % 32 == 0);
-}
+// Split-K runs on tiles whose waves split N into equal 32-column multiples (a ragged tile --
+// 256x224 over two wave columns: 128 + 96 -- keeps no split-K partial layout).
+constexpr bool tile_splittable(const TileCfg& t) { return t.nw == 0 || (t.bn / (t.nw / t.wgm)) % 32 == 0; }
 
 template <int I, int KIND>
 KernelFn pick_epi(int epi) {

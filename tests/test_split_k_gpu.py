@@ -109,3 +109,19 @@ def test_split_k_fp8_fp4(split_env):
     deep_gemm.fp8_fp4_gemm_nt((a, sfa), (b, sfb), d)
     torch.cuda.synchronize()
     assert calc_diff(d.cpu(), og.gemm_nt(a_deq, b_deq)) < THRESH
+
+
+@pytest.mark.parametrize('tile', ['256x256', '128x256', '128x128', '64x128'])
+@pytest.mark.parametrize('split', [2, 3])
+def test_split_k_tiles(split_env, monkeypatch, tile, split):
+    """Forced split on every splittable tile shape, including the 128-K-stage two-slot ring, with a
+    K that ends inside a stage."""
+    m, n, k = 300, 512, 1984
+    print(f'split_k={split} tile={tile} m={m} n={n} k={k}', flush=True)
+    monkeypatch.setenv('DG_FORCE_BLOCK', tile)
+    os.environ['DG_SPLIT_K'] = str(split)
+    a, sfa, a_deq, b, sfb, b_deq = _case(m, n, k, seed=40 + split)
+    d = torch.empty(m, n, dtype=torch.float32, device='cuda')
+    deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d)
+    torch.cuda.synchronize()
+    assert calc_diff(d.cpu(), og.gemm_nt(a_deq, b_deq, torch.float32)) < THRESH
