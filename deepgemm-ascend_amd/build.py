@@ -54,7 +54,7 @@ def build(jobs: int = 0, verbose: bool = False) -> Path:
             f.result()
     tmp = LIB.with_suffix('.so.tmp')
     # -z defs: a kernel whose host stub was silently dropped fails here, not at load time
-    cmd = [hipcc(), f'--offload-arch={ARCH}', '-shared', '-fPIC', '-Wl,-z,defs', *map(str, objs), '-o', str(tmp)]
+    cmd = [hipcc(), f'--offload-arch={ARCH}', '-shared', '-fPIC', '-Wl,-z,defs', *map(str, objs), '-lhiprtc', '-o', str(tmp)]
     if verbose:
         print(' '.join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

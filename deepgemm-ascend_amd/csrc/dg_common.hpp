@@ -1,8 +1,20 @@
 // Shared device/host definitions for the gfx950 block-scaled GEMM family.
 #pragma once
 
+// (The runtime compiler, hipRTC, brings its own HIP definitions and fixed-width types.)
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#else
+using __hip_internal::int8_t;
+using __hip_internal::uint8_t;
+using __hip_internal::int16_t;
+using __hip_internal::uint16_t;
+using __hip_internal::int32_t;
+using __hip_internal::uint32_t;
+using __hip_internal::int64_t;
+using __hip_internal::uint64_t;
+#endif
 
 namespace dg {
 

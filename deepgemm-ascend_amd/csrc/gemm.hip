@@ -271,7 +271,9 @@ extern "C" int dg_gemm_workspace_size(const dg_gemm_args* args, int64_t* bytes) 
     return DG_OK;
 }
 
-extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
+namespace {
+
+int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only) {
     using namespace dg;
     if (args == nullptr) return dg_set_error("dg_gemm: null args");
     const dg_gemm_args& a = *args;
@@ -342,8 +344,8 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
     const int epi_kind = a.d_dtype == DG_DTYPE_F32 ? kEpiF32
                        : a.d_dtype == DG_DTYPE_FP8_E4M3 ? kEpiFp8
                        : a.epilogue == DG_EPI_BF16_SR ? kEpiBf16SR : kEpiBf16;
-    KernelFn fn = lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind);
-    if (fn == nullptr) {
+    KernelFn fn = a.jit ? nullptr : lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind);
+    if (fn == nullptr && !a.jit) {
         char buf[160];
         snprintf(buf, sizeof(buf), "dg_gemm: no compiled kernel for kind=%d block=%dx%d", a.kind, cfg.bm, cfg.bn);
         dg_set_error(buf);
@@ -390,6 +392,7 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
         p.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.workspace) + kCounterBytes);
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (a.jit) return jit_run(a, cfg, epi_kind, plan.split, p, grid, st, compile_only);
     hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3((unsigned)tile_threads(cfg.bm, cfg.bn)), 0, st, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
@@ -397,4 +400,15 @@ extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) {
         return DG_ELAUNCH;
     }
     return DG_OK;
+}
+
+}  // namespace
+
+extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) { return gemm_impl(args, stream, false); }
+
+extern "C" int dg_jit_compile(const dg_gemm_args* args) {
+    if (args == nullptr) return dg_set_error("dg_jit_compile: null args");
+    dg_gemm_args a = *args;
+    a.jit = 1;
+    return gemm_impl(&a, nullptr, true);
 }

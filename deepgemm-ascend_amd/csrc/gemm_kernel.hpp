@@ -27,8 +27,6 @@
 // ends with groups of four consecutive n of one output row m.
 #pragma once
 
-#include <type_traits>
-#include <utility>
 #include "dg_common.hpp"
 
 namespace dg {
@@ -106,14 +104,33 @@ __device__ __forceinline__ uint32_t ue8m0_of_bf16_amax(uint32_t x) {
 template <int N>
 struct Int { static constexpr int value = N; };
 
+// Compile-time loop f(Int<0>), ..., f(Int<N-1>) (the kernel sources use no standard-library
+// header, so the runtime compiler needs nothing beyond them).
+template <int... Is>
+struct IntSeq {};
+template <int N, int... Is>
+struct MakeSeq : MakeSeq<N - 1, N - 1, Is...> {};
+template <int... Is>
+struct MakeSeq<0, Is...> { using type = IntSeq<Is...>; };
 template <typename F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+__device__ __forceinline__ void static_for_impl(F&& f, IntSeq<Is...>) {
     (f(Int<Is>{}), ...);
 }
 template <int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
+    static_for_impl(f, typename MakeSeq<N>::type{});
 }
+
+template <bool C, typename T, typename F>
+struct Cond { using type = T; };
+template <typename T, typename F>
+struct Cond<false, T, F> { using type = F; };
+
+template <typename A, typename B>
+struct Pair {
+    A first;
+    B second;
+};
 
 // s_waitcnt that bounds only the vector-memory counter.
 template <int VM>
@@ -188,9 +205,13 @@ __device__ __forceinline__ void swizzle_tile(int t, int nm, int nn, int gm, int&
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// OCC = workgroups per CU the kernel is compiled for (its waves per SIMD bound its registers).
-template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI>
-__global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KParams p) {
+// The kernel body.  OCC = workgroups per CU the kernel is compiled for (its waves per SIMD bound
+// its registers).  CT / CS / CM / CN / CK fix the GEMM type, the K split and M / N / K at compile
+// time (-1 / 0 = read from the arguments): the ahead-of-time menu reads everything from the
+// arguments, the JIT compiles one body per problem (csrc/jit.hip).
+template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI, int CT = -1,
+          int CS = 0, int CM = 0, int CN = 0, int CK = 0>
+__device__ __forceinline__ void gemm_body(const KParams& p) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
     constexpr bool kBf16 = KIND == kBF16;
@@ -254,29 +275,31 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
     const int r = lane & 31, q = lane >> 5;
 
     // ------------------------------------------------------------------ tile selection
-    const int nm = p.num_m_blocks, nn = p.num_n_blocks;
+    const int gemm_type = CT >= 0 ? CT : p.gemm_type;
+    const int split_k = CS > 0 ? CS : p.split_k;
+    const int nm = CM > 0 ? ceil_div(CM, BM) : p.num_m_blocks, nn = CN > 0 ? ceil_div(CN, BN) : p.num_n_blocks;
     int t, split = 0;
-    if (p.split_k > 1) {
+    if (split_k > 1) {
         // Split-K launch: grid = 8 * ceil(tiles / 8) * split_k, and workgroup b serves tile
         // (b / 8 / split_k) * 8 + b % 8, split (b / 8) % split_k, so all splits of a tile share
         // b % 8 -- the XCD (and L2) the dispatcher places them on.
         const int b = blockIdx.x, r = b >> 3;
-        t = (r / p.split_k) * 8 + (b & 7);
-        split = r % p.split_k;
+        t = (r / split_k) * 8 + (b & 7);
+        split = r % split_k;
         if (t >= p.num_tiles) return;
     } else {
         t = xcd_remap(blockIdx.x, gridDim.x);
     }
     const int tile_id = t;
     int batch = 0;
-    if (p.gemm_type == kBatched || p.gemm_type == kMasked || p.gemm_type == kKGrouped) {
+    if (gemm_type == kBatched || gemm_type == kMasked || gemm_type == kKGrouped) {
         batch = t / (nm * nn);
         t -= batch * nm * nn;
     }
     int mb, nb;
     swizzle_tile(t, nm, nn, p.group_m, mb, nb);
     const int m0 = mb * BM, n0 = nb * BN;
-    const int M = p.m, N = p.n;
+    const int M = CM > 0 ? CM : p.m, N = CN > 0 ? CN : p.n;
 
     const uint8_t* a_base = p.a;
     const uint8_t* b_base = p.b;
@@ -287,9 +310,9 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
     int group = 0;          // B operand group
     int valid_end = M;      // rows >= valid_end are padding (psum) / not written (masked)
     bool zero_tile = false;
-    int k_len = p.k;        // K extent of this tile's contraction
+    int k_len = CK > 0 ? CK : p.k;   // K extent of this tile's contraction
 
-    if (p.gemm_type == kKGrouped) {
+    if (gemm_type == kKGrouped) {
         // K-grouped: group g contracts K rows [align(psum[g-1]), psum[g]) of A and B into D[g].
         const int ks = batch == 0 ? 0 : align_up(p.layout[batch - 1], p.alignment);
         k_len = __builtin_amdgcn_readfirstlane(max(0, p.layout[batch] - ks));
@@ -303,16 +326,16 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
         d_base += (int64_t)batch * p.bsd * out_esize;
     }
 
-    if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
+    if (gemm_type == kBatched || gemm_type == kMasked) {
         group = batch;
         a_base += (int64_t)batch * p.bsa;
         d_base += (int64_t)batch * p.bsd * out_esize;
         if (!kBf16) sfa += (int64_t)batch * p.sfa_bs;
-        if (p.gemm_type == kMasked) {
+        if (gemm_type == kMasked) {
             valid_end = min(M, p.layout[batch]);
             if (m0 >= valid_end) return;   // whole tile beyond masked_m: nothing to write
         }
-    } else if (p.gemm_type == kMGroupedPsum) {
+    } else if (gemm_type == kMGroupedPsum) {
         int found = -1;
         for (int base = 0; base < p.num_groups; base += 64) {
             const int gi = base + lane;
@@ -328,7 +351,7 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
             valid_end = min(M, p.layout[found]);
             if (valid_end <= m0) zero_tile = true;
         }
-    } else if (p.gemm_type == kMGroupedIdx) {
+    } else if (gemm_type == kMGroupedIdx) {
         group = __builtin_amdgcn_readfirstlane(p.layout[m0]);
         if (group < 0) zero_tile = true;
     }
@@ -346,7 +369,7 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
         }
         return;
     }
-    if (p.gemm_type != kNormal && p.gemm_type != kKGrouped) {
+    if (gemm_type != kNormal && gemm_type != kKGrouped) {
         b_base += (int64_t)group * p.bsb;
         if (!kBf16) sfb += (int64_t)group * p.sfb_bs;
     }
@@ -356,15 +379,16 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
     const int64_t lda = p.lda, ldb = p.ldb;
     const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(a_base + (int64_t)m0 * lda, (int64_t)rows_a * lda);
     const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(b_base + (int64_t)n0 * ldb, (int64_t)rows_b * ldb);
-    const int kbytes_a = p.gemm_type == kKGrouped ? k_len * (kAFp4 ? 1 : (kBf16 ? 4 : 2)) / 2 : p.kbytes_a;
-    const int kbytes_b = p.gemm_type == kKGrouped ? k_len * (kBFp4 ? 1 : (kBf16 ? 4 : 2)) / 2 : p.kbytes_b;
+    // (bytes of one K row: storage bytes per two K elements x K / 2)
+    const int kbytes_a = gemm_type == kKGrouped || CK > 0 ? k_len * (kAFp4 ? 1 : (kBf16 ? 4 : 2)) / 2 : p.kbytes_a;
+    const int kbytes_b = gemm_type == kKGrouped || CK > 0 ? k_len * (kBFp4 ? 1 : (kBf16 ? 4 : 2)) / 2 : p.kbytes_b;
     // With KM = 1 the ring walks an even number of virtual stages so the main loop is a pair of
     // iterations with static register sets; an odd stage count gets one leading dead stage
     // (all-zero operands and scales, so it adds nothing to the accumulators).  With KM = 2 the
     // two sub-steps of every stage own the two register sets.
     // K stages of this workgroup: [c0, c0 + num_stages) of the whole K loop.
     const int c0 = split * p.split_stages;
-    const int num_stages = p.split_k > 1 ? min(p.split_stages, ceil_div(k_len, KS) - c0) : ceil_div(k_len, KS);
+    const int num_stages = split_k > 1 ? min(p.split_stages, ceil_div(k_len, KS) - c0) : ceil_div(k_len, KS);
     const int shift = KM == 1 ? (num_stages & 1) : 0;
     const int num_virtual = num_stages + shift;
     const int nk64 = ceil_div(k_len, 64);
@@ -495,11 +519,11 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
         const uint8_t* sc = st + A_BYTES + B_BYTES + u * SCU;
         if constexpr (part < TM) {
             const int R = wm * WM + part * 32 + r;
-            return std::pair<i32x8, int>(load_frag(st, R, Int<SPRA>{}, u_tag), kBf16 ? 0 : load_scale(sc, R));
+            return Pair<i32x8, int>{load_frag(st, R, Int<SPRA>{}, u_tag), kBf16 ? 0 : load_scale(sc, R)};
         } else {
             const int R = wn * WN + r;
-            return std::pair<i32x8, int>(load_frag(st + A_BYTES, R, Int<SPRB>{}, u_tag),
-                                         kBf16 ? 0 : load_scale(sc + SCA, R));
+            return Pair<i32x8, int>{load_frag(st + A_BYTES, R, Int<SPRB>{}, u_tag),
+                                         kBf16 ? 0 : load_scale(sc + SCA, R)};
         }
     };
     auto prefetch = [&](int s, auto buf_tag, auto part_tag, auto u_tag) {
@@ -641,10 +665,10 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
     __builtin_amdgcn_s_waitcnt(0);
 
     // ------------------------------------------------------------------ split-K reduction
-    if (!kRagged && p.split_k > 1) {   // (the host never splits a ragged tile)
+    if (!kRagged && split_k > 1) {   // (the host never splits a ragged tile)
         // This workgroup's partial tile, in accumulator-register order (coalesced 16-byte
         // stores and loads; the reducing workgroup uses the same lane mapping).
-        float* const tile_ws = p.ws + (int64_t)tile_id * p.split_k * (BM * BN);
+        float* const tile_ws = p.ws + (int64_t)tile_id * split_k * (BM * BN);
         auto part = [&](int sp, int jn, int jm) {
             return tile_ws + (int64_t)sp * (BM * BN) + (((wave * TN + jn) * TM + jm) * 64 + lane) * 16;
         };
@@ -678,15 +702,15 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
                                            __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         const int prev = *flag;
-        if ((prev & 0xffff) != p.split_k - 1) return;
+        if ((prev & 0xffff) != split_k - 1) return;
         if (!home || (prev >> 16) != 0) __threadfence();
         // Sum the partials in split order, whichever split arrived last, so a launch's result
         // does not depend on workgroup timing.
         static_for<TN>([&](auto i) {
             static_for<TM>([&](auto j) { acc[decltype(i)::value][decltype(j)::value] = f32x16{}; });
         });
-        const __amdgpu_buffer_rsrc_t rs_ws = make_rsrc(tile_ws, (int64_t)p.split_k * (BM * BN) * 4);
-        for (int sp = 0; sp < p.split_k; ++sp) {
+        const __amdgpu_buffer_rsrc_t rs_ws = make_rsrc(tile_ws, (int64_t)split_k * (BM * BN) * 4);
+        for (int sp = 0; sp < split_k; ++sp) {
             static_for<TN>([&](auto jn_c) {
                 constexpr int jn = decltype(jn_c)::value;
                 static_for<TM>([&](auto jm_c) {
@@ -713,7 +737,7 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
     constexpr bool kF32 = EPI == kEpiF32;
     constexpr bool kSR = EPI == kEpiBf16SR;
     constexpr bool kFp8 = EPI == kEpiFp8;
-    using OutT = std::conditional_t<kF32, float, std::conditional_t<kFp8, uint8_t, uint16_t>>;
+    using OutT = typename Cond<kF32, float, typename Cond<kFp8, uint8_t, uint16_t>::type>::type;
     OutT* dbase = reinterpret_cast<OutT*>(d_base);
     const OutT* bp = reinterpret_cast<const OutT*>(p.bias);
     const bool acc_old = p.accumulate, bias = p.has_bias, vec = p.vec_store;
@@ -723,10 +747,10 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
     static_for<TM>([&](auto jm_c) {
         constexpr int jm = decltype(jm_c)::value;
         const int m = m0 + wm * WM + jm * 32 + r;
-        const bool row_ok = m < M && !(p.gemm_type == kMasked && m >= valid_end);
+        const bool row_ok = m < M && !(gemm_type == kMasked && m >= valid_end);
         bool pad_row = false;
-        if (p.gemm_type == kMGroupedPsum) pad_row = m >= valid_end;
-        else if (p.gemm_type == kMGroupedIdx) pad_row = row_ok && p.layout[m] != group;
+        if (gemm_type == kMGroupedPsum) pad_row = m >= valid_end;
+        else if (gemm_type == kMGroupedIdx) pad_row = row_ok && p.layout[m] != group;
         OutT* drow = dbase + (int64_t)m * p.ldd;
         static_for<TN>([&](auto jn_c) {
             constexpr int jn = decltype(jn_c)::value;
@@ -852,6 +876,12 @@ __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KPara
             }   // !kFp8
         });
     });
+}
+
+// The ahead-of-time kernel of one tile shape: everything from the arguments.
+template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI>
+__global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KParams p) {
+    gemm_body<BM, BN, WGM, NW, LW, NSTAGE, KM, OCC, KIND, EPI>(p);
 }
 
 }  // namespace dg

@@ -2,6 +2,7 @@
 #pragma once
 
 #include "gemm_kernel.hpp"
+#include "../../include/deep_gemm_amd.h"
 
 namespace dg {
 
@@ -68,6 +69,11 @@ inline int tile_threads(int bm, int bn) {
         if (t.bm == bm && t.bn == bn) return t.nw * 64;
     return 0;
 }
+
+// Run-time compiled kernel of one launch plan (csrc/jit.hip): compile or fetch it and, unless
+// compile_only, launch it on `st`.
+int jit_run(const dg_gemm_args& a, const TileCfg& cfg, int epi, int split, const KParams& p, int64_t grid,
+            hipStream_t st, bool compile_only);
 
 KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi);
 KernelFn lookup_kernel_fp8fp4(int bm, int bn, int epi);

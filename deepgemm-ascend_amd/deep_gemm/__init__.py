@@ -21,7 +21,7 @@ from .runtime import (  # noqa: E402
     get_mk_alignment_for_contiguous_layout,
     get_theoretical_mk_alignment_for_contiguous_layout,
     use_deterministic_algorithms, get_deterministic_algorithms,
-    set_dry_run, get_dry_run, init,
+    set_dry_run, get_dry_run, set_jit, get_jit, init,
 )
 from .layout import (transform_sf_into_required_layout, transform_k_grouped_sf_into_required_layout,  # noqa: E402
                      get_recipe)

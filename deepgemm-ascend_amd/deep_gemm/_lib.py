@@ -18,10 +18,12 @@ DG_GEMM_NORMAL, DG_GEMM_BATCHED, DG_GEMM_MGROUPED_PSUM, DG_GEMM_MGROUPED_IDX, DG
 DG_DTYPE_BF16, DG_DTYPE_F32, DG_DTYPE_FP8_E4M3 = 0, 1, 2
 DG_EPI_DEFAULT, DG_EPI_BF16_SR = 0, 1
 DG_SF_F32, DG_SF_I16 = 0, 1
+DG_COMPILED_M, DG_COMPILED_N, DG_COMPILED_K = 1, 2, 4
 
 # Every symbol include/deep_gemm_amd.h declares.
 EXPORTED_SYMBOLS = ('dg_gemm', 'dg_transform_sf', 'dg_transform_k_grouped_sf', 'dg_transpose_to_k_major', 'dg_device_num_cus', 'dg_select_config',
-                    'dg_gemm_workspace_size', 'dg_last_error', 'dg_version')
+                    'dg_gemm_workspace_size', 'dg_last_error', 'dg_version', 'dg_jit_compile', 'dg_jit_set_include_dir',
+                    'dg_jit_stats')
 
 
 class GemmArgs(ctypes.Structure):
@@ -41,6 +43,7 @@ class GemmArgs(ctypes.Structure):
         ('num_cus', ctypes.c_int32), ('split_k', ctypes.c_int32),
         ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_int64),
         ('epilogue', ctypes.c_int32), ('sfd', ctypes.c_void_p), ('sfd_ld', ctypes.c_int64),
+        ('jit', ctypes.c_int32), ('compiled_dims', ctypes.c_int32),
     ]
 
 
@@ -89,11 +92,27 @@ def load(path=None) -> ctypes.CDLL:
         lib.dg_select_config.restype = ctypes.c_int
         lib.dg_gemm_workspace_size.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(ctypes.c_int64)]
         lib.dg_gemm_workspace_size.restype = ctypes.c_int
+        lib.dg_jit_compile.argtypes = [ctypes.POINTER(GemmArgs)]
+        lib.dg_jit_compile.restype = ctypes.c_int
+        lib.dg_jit_set_include_dir.argtypes = [ctypes.c_char_p]
+        lib.dg_jit_set_include_dir.restype = ctypes.c_int
+        lib.dg_jit_stats.argtypes = [ctypes.POINTER(ctypes.c_int64)] * 3
+        lib.dg_jit_stats.restype = ctypes.c_int
+        # kernel headers the run-time compiler reads: csrc/ beside this package
+        lib.dg_jit_set_include_dir(str(Path(__file__).resolve().parent.parent / 'csrc').encode())
         lib.dg_last_error.restype = ctypes.c_char_p
         lib.dg_version.restype = ctypes.c_char_p
         if path is None:
             _lib = lib
         return lib
+
+
+def jit_stats(lib=None):
+    """(hipRTC compilations, disk-cache reads, launches of an already loaded kernel) since load."""
+    lib = lib or load()
+    vals = [ctypes.c_int64() for _ in range(3)]
+    check(lib.dg_jit_stats(*[ctypes.byref(v) for v in vals]), lib)
+    return tuple(v.value for v in vals)
 
 
 def check(rc: int, lib=None) -> None:

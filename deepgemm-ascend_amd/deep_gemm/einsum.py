@@ -18,14 +18,14 @@ def fp8_bmm(a: Tuple[torch.Tensor, torch.Tensor], b: Tuple[torch.Tensor, torch.T
     A [B, M, K] e4m3, B [B, N, K] e4m3, SFs fp32 or packed int16 in any major; D [B, M, N] bf16 /
     fp32, or an (e4m3 D, SFD) pair / FP8Quantization(sfd) with SFD int16 [M, B * N / 64], M-major."""
     (a_, sfa), (b_, sfb) = a, b
-    _batched(a_, sfa, b_, sfb, d, c, recipe, False, epilogue)
+    _batched(a_, sfa, b_, sfb, d, c, recipe, False, epilogue, dims=compiled_dims)
 
 
 def bf16_bmm(a: torch.Tensor, b: torch.Tensor, d: torch.Tensor, c: Optional[torch.Tensor] = None,
              compiled_dims: str = 'nk', epilogue=None) -> None:
     """Batched bf16 GEMM D[i] = A[i] @ B[i]^T (+ C[i]) (csrc/apis/einsum.hpp:73-97)."""
     _assert(d.dtype in (torch.float32, torch.bfloat16))
-    _batched(a, None, b, None, d, c, None, True, epilogue)
+    _batched(a, None, b, None, d, c, None, True, epilogue, dims=compiled_dims)
 
 
 def _perm(t: Optional[torch.Tensor], p):

@@ -21,7 +21,7 @@ from . import _lib
 from . import epilogue as _epi
 from .layout import (transform_sf_into_required_layout, transform_k_grouped_sf_into_required_layout, get_recipe,
                      operand_recipes, _assert)
-from .runtime import get_num_sms, get_mk_alignment_for_contiguous_layout, get_dry_run
+from .runtime import get_num_sms, get_mk_alignment_for_contiguous_layout, get_dry_run, get_jit
 
 PACKED_FP4 = torch.int8   # the reference's kPackedFP4 (csrc/utils/dtype.hpp:9)
 _FP4_TYPES = (torch.int8, getattr(torch, 'float4_e2m1fn_x2', torch.int8))
@@ -141,6 +141,11 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
 
 def _launch(args: _lib.GemmArgs, d: torch.Tensor) -> None:
     if get_dry_run():
+        # the reference's dry run compiles the kernel without loading or launching it
+        # (csrc/jit_kernels/fp8_gemm.hpp:75-78); ahead-of-time kernels need nothing
+        if args.jit:
+            lib = _lib.load()
+            _lib.check(lib.dg_jit_compile(args), lib)
         return
     lib = _lib.load()
     stream = _stream(d)
@@ -156,7 +161,7 @@ def _launch(args: _lib.GemmArgs, d: torch.Tensor) -> None:
     _lib.check(lib.dg_gemm(args, stream), lib)
 
 
-def _fill_common(args, d, k_kernel, alpha, kind):
+def _fill_common(args, d, k_kernel, alpha, kind, dims: str = 'nk'):
     args.kind = kind
     args.d = d.data_ptr()
     args.ldd = d.stride(-2)
@@ -166,6 +171,11 @@ def _fill_common(args, d, k_kernel, alpha, kind):
     args.k = k_kernel
     args.num_cus = get_num_sms()
     args.alignment = get_mk_alignment_for_contiguous_layout()
+    # run-time compiled kernels (set_jit): the GEMM type and K split, plus the `compiled_dims` sizes,
+    # become compile-time constants (the reference's compiled_dims, csrc/jit_kernels/fp8_gemm.hpp:42-44)
+    args.jit = 1 if get_jit() else 0
+    args.compiled_dims = (_lib.DG_COMPILED_M if 'm' in dims else 0) | (_lib.DG_COMPILED_N if 'n' in dims else 0) | \
+        (_lib.DG_COMPILED_K if 'k' in dims else 0)
     forced = os.environ.get('DG_FORCE_BLOCK')   # e.g. "256x224": tuning override of the heuristic
     if forced:
         args.block_m, args.block_n = (int(x) for x in forced.split('x'))
@@ -208,7 +218,7 @@ def _apply_epilogue(args, epi) -> None:
 
 
 def _dense_gemm(a, sfa, b, sfb, d, c, recipe, recipe_a, recipe_b, disable_ue8m0_cast, alpha, epilogue,
-                bf16: bool):
+                bf16: bool, dims: str = 'nk'):
     """fp8_fp4_gemm / bf16_gemm after the nt/nn/tn/tt transposes (csrc/apis/gemm.hpp:225-256, 424-453)."""
     _assert(d.dtype in (torch.bfloat16, torch.float32))
     if bf16:
@@ -254,7 +264,7 @@ def _dense_gemm(a, sfa, b, sfb, d, c, recipe, recipe_a, recipe_b, disable_ue8m0_
         # keep both operands on the same padded K
         a_k = _pad_k(a_k, k_kernel)
         b_k = _pad_k(b_k, k_kernel)
-    _fill_common(args, d, k_kernel, alpha_v, kind)
+    _fill_common(args, d, k_kernel, alpha_v, kind, dims)
     args.gemm_type = _lib.DG_GEMM_NORMAL
     args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
     args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
@@ -285,7 +295,7 @@ def _make_fp8_fp4_gemm(trans_a: bool, trans_b: bool, default_dims: str):
         if trans_b:
             b_, sfb = b_.transpose(0, 1), sfb.transpose(0, 1)
         _dense_gemm(a_, sfa, b_, sfb, d, c, recipe, recipe_a, recipe_b, disable_ue8m0_cast, alpha, epilogue,
-                    bf16=False)
+                    bf16=False, dims=compiled_dims)
     return fn
 
 
@@ -304,7 +314,7 @@ def _make_bf16_gemm(trans_a: bool, trans_b: bool, default_dims: str):
            compiled_dims: str = default_dims, alpha: Optional[float] = None, epilogue=None) -> None:
         a_ = a.transpose(0, 1) if trans_a else a
         b_ = b.transpose(0, 1) if trans_b else b
-        _dense_gemm(a_, None, b_, None, d, c, None, None, None, False, alpha, epilogue, bf16=True)
+        _dense_gemm(a_, None, b_, None, d, c, None, None, None, False, alpha, epilogue, bf16=True, dims=compiled_dims)
     return fn
 
 
@@ -317,7 +327,7 @@ for _f, _name in ((bf16_gemm_nt, 'nt'), (bf16_gemm_nn, 'nn'), (bf16_gemm_tn, 'tn
 
 
 def _grouped_contiguous(a, sfa, b, sfb, d, grouped_layout, recipe, recipe_a, recipe_b, disable_ue8m0_cast,
-                        use_psum_layout, epilogue, bf16: bool):
+                        use_psum_layout, epilogue, bf16: bool, dims: str = 'nk'):
     """m_grouped_fp8_fp4_gemm_contiguous / m_grouped_bf16_gemm_contiguous (csrc/apis/gemm.hpp:289-324, 470-499)."""
     if bf16:
         _assert(a.dtype == torch.bfloat16)
@@ -363,7 +373,7 @@ def _grouped_contiguous(a, sfa, b, sfb, d, grouped_layout, recipe, recipe_a, rec
     b_k = _to_kernel_operand(b, k)
     k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
     a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
-    _fill_common(args, d, k_kernel, None, kind)
+    _fill_common(args, d, k_kernel, None, kind, dims)
     args.alignment = alignment
     args.gemm_type = _lib.DG_GEMM_MGROUPED_PSUM if use_psum_layout else _lib.DG_GEMM_MGROUPED_IDX
     args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
@@ -383,7 +393,7 @@ def _make_m_grouped_fp8_fp4(trans_b: bool):
         if trans_b:
             b_, sfb = b_.transpose(1, 2), sfb.transpose(1, 2)
         _grouped_contiguous(a_, sfa, b_, sfb, d, grouped_layout, recipe, recipe_a, recipe_b, disable_ue8m0_cast,
-                            use_psum_layout, epilogue, bf16=False)
+                            use_psum_layout, epilogue, bf16=False, dims=compiled_dims)
     return fn
 
 
@@ -399,7 +409,7 @@ def _make_m_grouped_bf16(trans_b: bool):
            epilogue=None) -> None:
         b_ = b.transpose(1, 2) if trans_b else b
         _grouped_contiguous(a, None, b_, None, d, grouped_layout, None, None, None, False, use_psum_layout,
-                            epilogue, bf16=True)
+                            epilogue, bf16=True, dims=compiled_dims)
     return fn
 
 
@@ -407,7 +417,7 @@ m_grouped_bf16_gemm_nt_contiguous = _make_m_grouped_bf16(False)
 m_grouped_bf16_gemm_nn_contiguous = _make_m_grouped_bf16(True)
 
 
-def _masked(a, sfa, b, sfb, d, masked_m, recipe, recipe_a, recipe_b, disable_ue8m0_cast, bf16: bool):
+def _masked(a, sfa, b, sfb, d, masked_m, recipe, recipe_a, recipe_b, disable_ue8m0_cast, bf16: bool, dims: str = 'nk'):
     """Masked grouped GEMM, upstream DeepGEMM semantics: D[g, :masked_m[g]] = A[g, :masked_m[g]] @ B[g]^T.
     The reference has no masked kernel (csrc/apis/gemm.hpp:606,630)."""
     _assert(a.dim() == 3 and b.dim() == 3 and d.dim() == 3, 'masked GEMM takes A [G,M,K], B [G,N,K], D [G,M,N]')
@@ -438,7 +448,7 @@ def _masked(a, sfa, b, sfb, d, masked_m, recipe, recipe_a, recipe_b, disable_ue8
     b_k = _to_kernel_operand(b, k)
     k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
     a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
-    _fill_common(args, d, k_kernel, None, kind)
+    _fill_common(args, d, k_kernel, None, kind, dims)
     args.gemm_type = _lib.DG_GEMM_MASKED
     args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
     args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
@@ -452,15 +462,15 @@ def m_grouped_fp8_fp4_gemm_nt_masked(a, b, d, masked_m: torch.Tensor, expected_m
                                      recipe_a=None, recipe_b=None, compiled_dims: str = 'nk',
                                      disable_ue8m0_cast: bool = False) -> None:
     (a_, sfa), (b_, sfb) = a, b
-    _masked(a_, sfa, b_, sfb, d, masked_m, recipe, recipe_a, recipe_b, disable_ue8m0_cast, bf16=False)
+    _masked(a_, sfa, b_, sfb, d, masked_m, recipe, recipe_a, recipe_b, disable_ue8m0_cast, bf16=False, dims=compiled_dims)
 
 
 def m_grouped_bf16_gemm_nt_masked(a, b, d, masked_m: torch.Tensor, expected_m: int,
                                   compiled_dims: str = 'nk') -> None:
-    _masked(a, None, b, None, d, masked_m, None, None, None, False, bf16=True)
+    _masked(a, None, b, None, d, masked_m, None, None, None, False, bf16=True, dims=compiled_dims)
 
 
-def _batched(a, sfa, b, sfb, d, c, recipe, bf16: bool, epilogue=None):
+def _batched(a, sfa, b, sfb, d, c, recipe, bf16: bool, epilogue=None, dims: str = 'nk'):
     """Batched GEMM D[i] = A[i] @ B[i]^T (+ C[i]): fp8_bmm / bf16_bmm (csrc/apis/einsum.hpp:37-97),
     get_gemm_desc with GemmType::Batched (csrc/apis/gemm.hpp:60-197).  ``d`` may be an
     (e4m3 D, SFD) pair (fp8_bmm only)."""
@@ -515,7 +525,7 @@ def _batched(a, sfa, b, sfb, d, c, recipe, bf16: bool, epilogue=None):
     b_k = _to_kernel_operand(b, k)
     k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
     a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
-    _fill_common(args, d, k_kernel, None, kind)
+    _fill_common(args, d, k_kernel, None, kind, dims)
     args.gemm_type = _lib.DG_GEMM_BATCHED
     args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
     args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
@@ -526,7 +536,7 @@ def _batched(a, sfa, b, sfb, d, c, recipe, bf16: bool, epilogue=None):
     _launch(args, d)
 
 
-def _k_grouped(a, sfa, b, sfb, d, grouped_layout, c, recipe, use_psum_layout, epilogue, bf16: bool):
+def _k_grouped(a, sfa, b, sfb, d, grouped_layout, c, recipe, use_psum_layout, epilogue, bf16: bool, dims: str = 'mn'):
     """K-grouped contiguous GEMM, D[g] = A[Kg]^T @ B[Kg] (+ C[g]) with A [Ktot, M], B [Ktot, N]
     (the `tn` layout) and K split by a psum layout: k_grouped_fp8_gemm_tn_contiguous
     (csrc/apis/gemm.hpp:351-387) and k_grouped_bf16_gemm_tn_contiguous (:515-...)."""
@@ -574,7 +584,7 @@ def _k_grouped(a, sfa, b, sfb, d, grouped_layout, c, recipe, use_psum_layout, ep
     b_k = _to_kernel_operand(b_t, k)
     k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
     a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
-    _fill_common(args, d, k_kernel, None, kind)
+    _fill_common(args, d, k_kernel, None, kind, dims)
     args.alignment = alignment
     args.gemm_type = _lib.DG_GEMM_KGROUPED
     args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
@@ -592,7 +602,7 @@ def k_grouped_fp8_gemm_tn_contiguous(a, b, d, ks_cpu, grouped_layout, c=None, re
     """K-grouped contiguous low-precision GEMM (csrc/apis/gemm.hpp:326-387): A [Ktot, M], B [Ktot, N], D [G, M, N].
     ``ks_cpu`` is a hint only (the reference uses it for its cost model)."""
     (a_, sfa), (b_, sfb) = a, b
-    _k_grouped(a_, sfa, b_, sfb, d, grouped_layout, c, recipe, use_psum_layout, epilogue, bf16=False)
+    _k_grouped(a_, sfa, b_, sfb, d, grouped_layout, c, recipe, use_psum_layout, epilogue, bf16=False, dims=compiled_dims)
 
 
 def k_grouped_fp8_gemm_nt_contiguous(a, b, d, ks_cpu, grouped_layout, c=None, recipe=(1, 1, 32),
@@ -609,7 +619,7 @@ def k_grouped_fp8_gemm_nt_contiguous(a, b, d, ks_cpu, grouped_layout, c=None, re
 def k_grouped_bf16_gemm_tn_contiguous(a, b, d, ks_cpu, grouped_layout, c=None, compiled_dims: str = 'mn',
                                       use_psum_layout: bool = True, epilogue=None) -> None:
     """K-grouped contiguous bf16 GEMM (csrc/apis/gemm.hpp:515-...)."""
-    _k_grouped(a, None, b, None, d, grouped_layout, c, None, use_psum_layout, epilogue, bf16=True)
+    _k_grouped(a, None, b, None, d, grouped_layout, c, None, use_psum_layout, epilogue, bf16=True, dims=compiled_dims)
 
 
 def select_config(m: int, n: int, k: int, kind: int = _lib.DG_KIND_FP8_FP8, gemm_type: int = _lib.DG_GEMM_NORMAL,

@@ -5,6 +5,7 @@ The M-grouped contiguous alignment defaults to 256 like the reference and may be
 any positive multiple of 32 (128 is the common MoE choice); the grouped kernels then use a
 block_m that divides it.
 """
+import os
 import threading
 
 _state = threading.local()
@@ -12,6 +13,7 @@ _lock = threading.Lock()
 _num_sms = 0
 _mk_alignment = 256
 _dry_run = False
+_jit = os.environ.get('DG_JIT', '0') not in ('', '0')
 _deterministic = False
 _device_cus = {}
 
@@ -63,6 +65,17 @@ def set_dry_run(value: bool) -> None:
 
 def get_dry_run() -> bool:
     return _dry_run
+
+
+def set_jit(enabled: bool) -> None:
+    """Launch kernels compiled at run time for each problem (hipRTC, cached under DG_JIT_CACHE_DIR)
+    instead of the ahead-of-time tile menu; the initial value comes from DG_JIT (default off)."""
+    global _jit
+    _jit = bool(enabled)
+
+
+def get_jit() -> bool:
+    return _jit
 
 
 def use_deterministic_algorithms(enabled: bool) -> None:

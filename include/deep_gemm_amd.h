@@ -103,11 +103,32 @@ typedef struct dg_gemm_args {
                                      pair p = (batch * n + col) / 64 of row `row` at
                                      sfd[p * sfd_ld + row], lower byte = the even 32 columns      */
     int64_t sfd_ld;               /* >= m                                                    */
+    int32_t jit;                  /* 1: launch a kernel compiled at run time for this problem
+                                     (see dg_jit_compile); 0: the ahead-of-time tile menu       */
+    int32_t compiled_dims;        /* jit only: DG_COMPILED_* sizes fixed at compile time (the
+                                     reference's compiled_dims, csrc/jit_kernels/fp8_gemm.hpp:
+                                     42-44); the GEMM type and K split always are              */
 } dg_gemm_args;
+
+#define DG_COMPILED_M 1
+#define DG_COMPILED_N 2
+#define DG_COMPILED_K 4
 
 /* Launch one GEMM.  Entry point replacing deep_gemm::launch_fp8_gemm /
  * launch_fp4_gemm / launch_fp8_dequant_gemm / launch_bf16_gemm (see dg_gemm_args). */
 int dg_gemm(const dg_gemm_args *args, void *stream);
+
+/* Runtime compilation (replaces the reference's deep-jit runtime, csrc/jit/jit.hpp:16-92, and
+ * the compile-without-load of its dry-run mode, csrc/jit_kernels/fp8_gemm.hpp:75-78).
+ * dg_jit_compile builds -- or finds in the DG_JIT_CACHE_DIR caches -- the kernel dg_gemm would
+ * launch for `args` with jit = 1, without launching it (nothing touches the device).  Kernels are
+ * compiled in-process with hipRTC for gfx950 from the headers in the include directory
+ * (default: csrc/ next to the library's directory). */
+int dg_jit_compile(const dg_gemm_args *args);
+int dg_jit_set_include_dir(const char *dir);
+/* Counters since load: hipRTC compilations, code objects read from the disk cache, launches of
+ * an already loaded kernel. */
+int dg_jit_stats(int64_t *compiled, int64_t *disk_hits, int64_t *memory_hits);
 
 /*
  * Scale-factor layout transform.  Replaces launch_transform_sf
