@@ -705,12 +705,16 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         if ((prev & 0xffff) != split_k - 1) return;
         if (!home || (prev >> 16) != 0) __threadfence();
         // Sum the partials in split order, whichever split arrived last, so a launch's result
-        // does not depend on workgroup timing.
+        // does not depend on workgroup timing.  Small wave tiles keep the loads of partial sp + 1
+        // in flight while partial sp is added (two register sets), so the reduction costs about
+        // one L2 round trip instead of split_k of them.
         static_for<TN>([&](auto i) {
             static_for<TM>([&](auto j) { acc[decltype(i)::value][decltype(j)::value] = f32x16{}; });
         });
         const __amdgpu_buffer_rsrc_t rs_ws = make_rsrc(tile_ws, (int64_t)split_k * (BM * BN) * 4);
-        for (int sp = 0; sp < split_k; ++sp) {
+        f32x4 pb[TM * TN <= 4 ? 2 : 1][TN][TM][4];
+        auto load_part = [&](int sp, auto set_tag) {
+            constexpr int set = decltype(set_tag)::value;
             static_for<TN>([&](auto jn_c) {
                 constexpr int jn = decltype(jn_c)::value;
                 static_for<TM>([&](auto jm_c) {
@@ -718,14 +722,40 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
                     // sc0 loads miss this CU's L1 (which may hold stale lines) and read the L2
                     const uint32_t off = (uint32_t)((part(sp, jn, jm) - tile_ws) * 4);
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const f32x4 v = __builtin_bit_cast(
+                    for (int g = 0; g < 4; ++g)
+                        pb[set][jn][jm][g] = __builtin_bit_cast(
                             f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_ws, off + 16 * g, 0, kCacheSc0));
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[jn][jm][4 * g + i] += v[i];
-                    }
                 });
             });
+        };
+        auto add_part = [&](auto set_tag) {
+            constexpr int set = decltype(set_tag)::value;
+            static_for<TN>([&](auto jn_c) {
+                constexpr int jn = decltype(jn_c)::value;
+                static_for<TM>([&](auto jm_c) {
+                    constexpr int jm = decltype(jm_c)::value;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[jn][jm][4 * g + i] += pb[set][jn][jm][g][i];
+                });
+            });
+        };
+        if constexpr (TM * TN <= 4) {
+            // (a partial index past the last one re-reads partial 0: in range, never added)
+            load_part(0, Int<0>{});
+            for (int sp = 0; sp < split_k; sp += 2) {
+                load_part(sp + 1 < split_k ? sp + 1 : 0, Int<1>{});
+                add_part(Int<0>{});
+                load_part(sp + 2 < split_k ? sp + 2 : 0, Int<0>{});
+                if (sp + 1 < split_k) add_part(Int<1>{});
+            }
+        } else {
+            // (large wave tiles: no registers for a second set)
+            for (int sp = 0; sp < split_k; ++sp) {
+                load_part(sp, Int<0>{});
+                add_part(Int<0>{});
+            }
         }
         if (tid == 0) __hip_atomic_store(p.counters + tile_id, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
