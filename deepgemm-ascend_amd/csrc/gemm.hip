@@ -79,7 +79,9 @@ bool tile_allowed(const dg_gemm_args& a, int bm, int bn) {
 struct Plan {
     TileCfg tile;
     int split;          // K ranges per tile (1 = no split)
-    int split_stages;   // K stages per range
+    int split_stages;   // K stages per range (skinny kernel: 64-K blocks per range)
+    int skinny_nw;      // > 0: the skinny-M kernel with this many waves (tile = 32 mt x 32 nb)
+    int skinny_d;       // its ring depth
 };
 
 // K elements of one kernel stage of tile t
@@ -132,12 +134,54 @@ bool skinny_plan(const dg_gemm_args& a, int cus, bool allow_split, Plan& out) {
         sp = std::max(1, std::min(sp, 16));
     }
     const int sps = ceil_div(ns, sp);
-    out = {tc, ceil_div(ns, sps), sps};
+    out = {tc, ceil_div(ns, sps), sps, 0, 0};
+    return true;
+}
+
+// DG_SKINNY (tuning override): "0" = never use the skinny-M kernel, "mt,nb,nw,d[,split]" = use
+// that configuration wherever M fits it.
+struct SkinnyEnv {
+    int mode;   // -1 default, 0 off, 1 forced configuration
+    int mt, nb, nw, d, split;
+};
+SkinnyEnv skinny_env() {
+    SkinnyEnv e = {-1, 0, 0, 0, 0, 0};
+    const char* s = std::getenv("DG_SKINNY");
+    if (s == nullptr || *s == '\0') return e;
+    if (std::strcmp(s, "0") == 0) { e.mode = 0; return e; }
+    if (std::sscanf(s, "%d,%d,%d,%d,%d", &e.mt, &e.nb, &e.nw, &e.d, &e.split) >= 4) e.mode = 1;
+    return e;
+}
+
+// Decode shapes (M <= 16, dense or batched) stream B through the skinny-M kernel: one
+// workgroup per 32-column strip, its four waves splitting K, and a K split across workgroups
+// only while the strips alone leave CUs idle (each range keeps at least four 64-K blocks per
+// wave).  Measured on MI355X (fp8, M = 1, kernel us, tile kernel in brackets): 2112x7168 8.5
+// (15.0), 7168x2048 5.6 (13.5), 24576x1536 10.4 (11.7), 7168x16384 26.5 (32.1), 4096x7168
+// 9.9 (15.8).  Larger M loads A rows straight to registers and loses to the tile kernel.
+bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const SkinnyEnv& env, Plan& out) {
+    if (env.mode == 0 || !(a.gemm_type == kNormal || a.gemm_type == kBatched)) return false;
+    int mt = 1, nb = 1, nw = 4, d = 2;
+    if (env.mode == 1) { mt = env.mt; nb = env.nb; nw = env.nw; d = env.d; }
+    else if (a.m > 16) return false;
+    if (a.m > 32 * mt || lookup_skinny(a.kind, mt, nb, nw, d, kEpiBf16) == nullptr) return false;
+    const int groups = a.gemm_type == kBatched ? a.num_groups : 1;
+    const int64_t strips = (int64_t)ceil_div(a.n, 32 * nb) * groups;
+    const int nk64 = std::max(1, ceil_div(a.k, 64));
+    int sp = 1;
+    if (allow_split && strips <= kMaxSplitTiles) {
+        if (env.mode == 1 && env.split > 0) sp = env.split;
+        else sp = (int)std::min<int64_t>(std::max<int64_t>(1, cus / strips), std::max(1, nk64 / (4 * nw)));
+        sp = std::max(1, std::min(sp, std::min(16, nk64)));
+    }
+    const int ss = ceil_div(nk64, sp);
+    out = {{32 * mt, 32 * nb, 0, nw, 0, 0, 0, 0, 0}, ceil_div(nk64, ss), ss, nw, d};
     return true;
 }
 
 Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     Plan skinny;
+    if (skinny_kernel_plan(a, cus, allow_split, skinny_env(), skinny)) return skinny;
     if (skinny_plan(a, cus, allow_split, skinny)) return skinny;
     allow_split = false;   // wide problems fill the CUs with tiles
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
@@ -149,7 +193,7 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     // fp32 D of the same call, with the same K split and summation order.)
     const double hbm_bytes = esz * ((double)a.m + a.n) * a.k * groups + 2.0 * a.m * a.n * groups;
     double best = 1e300;
-    Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0, 0}, 1, 1};
+    Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0, 0}, 1, 1, 0, 0};
     for (int i = 0; i < kNumTiles; ++i) {
         const TileCfg& tc = kTiles[i];
         if (!tile_allowed(a, tc.bm, tc.bn)) continue;
@@ -177,7 +221,7 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
             t = std::max(t, bytes / 3800.0);
             if (t < best * 0.97) {
                 best = t;
-                pick = {tc, sp, sps};
+                pick = {tc, sp, sps, 0, 0};
             }
         }
     }
@@ -186,6 +230,7 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
 
 struct MemoKey {
     int kind, type, m, n, k, g, cus, align, allow_split;
+    SkinnyEnv skinny;
     bool operator==(const MemoKey& o) const { return memcmp(this, &o, sizeof(*this)) == 0; }
 };
 struct MemoHash {
@@ -209,13 +254,14 @@ Plan choose(const dg_gemm_args& a, int cus, bool allow_split) {
         const int ns = ceil_div(a.k, k_stage_elems(a.kind, t));
         int sp = allow_split && tile_splittable(t) && a.split_k > 1 && plan_tiles(a, t) <= kMaxSplitTiles ? std::min(a.split_k, std::max(1, ns)) : 1;
         const int sps = ceil_div(ns, sp);
-        return {t, ceil_div(ns, sps), sps};
+        return {t, ceil_div(ns, sps), sps, 0, 0};
     }
     MemoKey key;
     memset(&key, 0, sizeof(key));
     key.kind = a.kind; key.type = a.gemm_type; key.m = a.m; key.n = a.n; key.k = a.k;
     key.g = a.num_groups; key.cus = cus; key.align = a.alignment;
     key.allow_split = allow_split && a.split_k != 1;
+    key.skinny = skinny_env();
     Plan pl;
     {
         std::lock_guard<std::mutex> lk(g_memo_mu);
@@ -226,6 +272,16 @@ Plan choose(const dg_gemm_args& a, int cus, bool allow_split) {
             pl = select_plan(a, cus, key.allow_split);
             g_memo.emplace(key, pl);
         }
+    }
+    if (pl.skinny_nw > 0) {
+        if (allow_split && a.split_k > 1 && plan_tiles(a, pl.tile) <= kMaxSplitTiles) {
+            // forced split count (tuning), in 64-K blocks
+            const int nk64 = std::max(1, ceil_div(a.k, 64));
+            const int ss = ceil_div(nk64, std::min(a.split_k, nk64));
+            pl.split = ceil_div(nk64, ss);
+            pl.split_stages = ss;
+        }
+        return pl;
     }
     if (allow_split && tile_splittable(pl.tile) && a.split_k > 1 && plan_tiles(a, pl.tile) <= kMaxSplitTiles) {
         // forced split count (tuning), on the heuristic's tile shape
@@ -344,8 +400,14 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only) {
     const int epi_kind = a.d_dtype == DG_DTYPE_F32 ? kEpiF32
                        : a.d_dtype == DG_DTYPE_FP8_E4M3 ? kEpiFp8
                        : a.epilogue == DG_EPI_BF16_SR ? kEpiBf16SR : kEpiBf16;
-    KernelFn fn = a.jit ? nullptr : lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind);
-    if (fn == nullptr && !a.jit) {
+    // (the skinny-M kernel is not specialised per problem: the JIT setting leaves it ahead-of-time)
+    const bool skinny = plan.skinny_nw > 0;
+    const bool jit = a.jit && !skinny;
+    if (skinny && compile_only) return DG_OK;
+    KernelFn fn = jit ? nullptr
+                : skinny ? lookup_skinny(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_nw, plan.skinny_d, epi_kind)
+                         : lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind);
+    if (fn == nullptr && !jit) {
         char buf[160];
         snprintf(buf, sizeof(buf), "dg_gemm: no compiled kernel for kind=%d block=%dx%d", a.kind, cfg.bm, cfg.bn);
         dg_set_error(buf);
@@ -392,8 +454,9 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only) {
         p.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.workspace) + kCounterBytes);
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (a.jit) return jit_run(a, cfg, epi_kind, plan.split, p, grid, st, compile_only);
-    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3((unsigned)tile_threads(cfg.bm, cfg.bn)), 0, st, p);
+    if (jit) return jit_run(a, cfg, epi_kind, plan.split, p, grid, st, compile_only);
+    const int threads = skinny ? plan.skinny_nw * 64 : tile_threads(cfg.bm, cfg.bn);
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3((unsigned)threads), 0, st, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         dg_set_error(hipGetErrorString(e));

@@ -205,6 +205,144 @@ __device__ __forceinline__ void swizzle_tile(int t, int nm, int nn, int gm, int&
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Epilogue of one 32x32 accumulator block: lane (r, q) holds output row m (the caller's
+// row_ok / pad_row flags describe it) and columns nblk + 8 g + 4 q + {0..3} in elements
+// 4 g + {0..3}; alpha, bias, accumulate, the D dtype (EPI) and stochastic rounding / FP8
+// quantisation are applied here and the block is stored to D (d_base already offset by batch).
+template <int EPI>
+__device__ __forceinline__ void epilogue_block(const KParams& p, const f32x16& acc, uint8_t* d_base, int m,
+                                               bool row_ok, bool pad_row, int nblk, int N, int batch, int q) {
+    const float alpha = p.alpha;
+    constexpr bool kF32 = EPI == kEpiF32;
+    constexpr bool kSR = EPI == kEpiBf16SR;
+    constexpr bool kFp8 = EPI == kEpiFp8;
+    using OutT = typename Cond<kF32, float, typename Cond<kFp8, uint8_t, uint16_t>::type>::type;
+    OutT* drow = reinterpret_cast<OutT*>(d_base) + (int64_t)m * p.ldd;
+    const OutT* bp = reinterpret_cast<const OutT*>(p.bias);
+    const bool acc_old = p.accumulate, bias = p.has_bias, vec = p.vec_store;
+    auto to_f = [](OutT x) -> float {
+        if constexpr (kF32) return x; else if constexpr (kFp8) return 0.f; else return bf16_to_f32(x);
+    };
+    // the lane holds columns nblk + 8 g + 4 q + {0..3} in elements 4 g + {0..3}
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = acc[i] * alpha;
+    if constexpr (kFp8) {
+        // Quantise the bf16-rounded outputs per 32 columns of a row: this lane holds 16 of
+        // them, its partner lane (q ^ 1) the other 16.  The host guarantees n % 128 == 0, so
+        // a block is either entirely inside the row or entirely past it.
+        uint32_t amax = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint16_t h = f32_to_bf16_rne(v[i]);
+            v[i] = bf16_to_f32(h);
+            amax = max(amax, (uint32_t)(h & 0x7fffu));
+        }
+        amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32));
+        const uint32_t sexp = ue8m0_of_bf16_amax(amax);
+        const float inv = __builtin_bit_cast(float, (254u - sexp) << 23);   // 2^(127 - s)
+        if (row_ok && nblk < N) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                int w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * g] * inv, v[4 * g + 1] * inv, 0, false);
+                w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * g + 2] * inv, v[4 * g + 3] * inv, w, true);
+                *reinterpret_cast<int*>(drow + nblk + 8 * g + 4 * q) = w;
+            }
+            if (q == 0) {
+                const int64_t col = (int64_t)batch * N + nblk;
+                p.sfd[((col >> 6) * p.sfd_ld + m) * 2 + ((col >> 5) & 1)] = (uint8_t)sexp;
+            }
+        }
+    } else {
+    const bool full = vec && nblk + 32 <= N;                   // wave-uniform
+    if (full) {
+        if (bias) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[4 * g + i] += to_f(bp[nblk + 8 * g + 4 * q + i]);
+        }
+        if (acc_old && row_ok) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[4 * g + i] += to_f(drow[nblk + 8 * g + 4 * q + i]);
+        }
+        if constexpr (kF32) {
+            if (row_ok) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    f32x4 o = {v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+                    if (pad_row) o = f32x4{0.f, 0.f, 0.f, 0.f};
+                    *reinterpret_cast<f32x4*>(drow + nblk + 8 * g + 4 * q) = o;
+                }
+            }
+        } else {
+            // pk[g] = columns 8 g + 4 q + {0..3} as two bf16 pairs
+            uint32_t pk[4][2];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                if constexpr (kSR) {
+                    uint16_t o[4];
+                    sr_bf16_quartet(v + 4 * g, (uint32_t)(nblk + 8 * g + 4 * q) >> 2, o);
+                    pk[g][0] = pad_row ? 0u : (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+                    pk[g][1] = pad_row ? 0u : (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+                } else {
+                    pk[g][0] = pad_row ? 0u : pack_bf16x2(v[4 * g], v[4 * g + 1]);
+                    pk[g][1] = pad_row ? 0u : pack_bf16x2(v[4 * g + 2], v[4 * g + 3]);
+                }
+            }
+            // v_permlane32_swap regroups the wave halves: afterwards the lower half
+            // (q = 0) holds columns 16..31 and the upper half (q = 1) columns 0..15 of
+            // the block, i.e. 32 contiguous bytes per lane.
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const auto s02 = __builtin_amdgcn_permlane32_swap(pk[2][h], pk[0][h], false, false);
+                const auto s13 = __builtin_amdgcn_permlane32_swap(pk[3][h], pk[1][h], false, false);
+                pk[2][h] = s02[0]; pk[0][h] = s02[1];
+                pk[3][h] = s13[0]; pk[1][h] = s13[1];
+            }
+            if (row_ok) {
+                // q = 0: pk2 = 16..19, pk0 = 20..23, pk3 = 24..27, pk1 = 28..31
+                // q = 1: pk2 = 0..3,   pk0 = 4..7,   pk3 = 8..11,  pk1 = 12..15
+                uint16_t* dp = drow + nblk + (q ? 0 : 16);
+                *reinterpret_cast<i32x4*>(dp) = i32x4{(int)pk[2][0], (int)pk[2][1], (int)pk[0][0], (int)pk[0][1]};
+                *reinterpret_cast<i32x4*>(dp + 8) = i32x4{(int)pk[3][0], (int)pk[3][1], (int)pk[1][0], (int)pk[1][1]};
+            }
+        }
+    } else if (row_ok && kSR) {
+        // ragged / unaligned block, stochastic rounding: columns past the row hash as zeros
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int n = nblk + 8 * g + 4 * q;
+            float x[4];
+            uint16_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = n + i < N ? v[4 * g + i] : 0.f;
+            sr_bf16_quartet(x, (uint32_t)n >> 2, o);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (n + i < N) drow[n + i] = pad_row ? (uint16_t)0 : o[i];
+        }
+    } else if (row_ok) {
+        // ragged / unaligned block: element stores with bounds
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int n = nblk + 8 * g + 4 * q + i;
+                if (n < N) {
+                    float x = v[4 * g + i];
+                    if (bias) x += to_f(bp[n]);
+                    if (acc_old) x += to_f(drow[n]);
+                    if constexpr (kF32) drow[n] = pad_row ? 0.f : x;
+                    else drow[n] = pad_row ? (uint16_t)0 : f32_to_bf16_rne(x);
+                }
+            }
+    }
+    }   // !kFp8
+}
+
 // The kernel body.  OCC = workgroups per CU the kernel is compiled for (its waves per SIMD bound
 // its registers).  CT / CS / CM / CN / CK fix the GEMM type, the K split and M / N / K at compile
 // time (-1 / 0 = read from the arguments): the ahead-of-time menu reads everything from the
@@ -668,19 +806,26 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     if (!kRagged && split_k > 1) {   // (the host never splits a ragged tile)
         // This workgroup's partial tile, in accumulator-register order (coalesced 16-byte
         // stores and loads; the reducing workgroup uses the same lane mapping).
+        // Lanes of rows past M (skinny M) take an offset past the buffer's end: the hardware
+        // drops their stores and returns zeros for their loads, so no partial bytes move for them.
         float* const tile_ws = p.ws + (int64_t)tile_id * split_k * (BM * BN);
-        auto part = [&](int sp, int jn, int jm) {
-            return tile_ws + (int64_t)sp * (BM * BN) + (((wave * TN + jn) * TM + jm) * 64 + lane) * 16;
+        const __amdgpu_buffer_rsrc_t rs_ws = make_rsrc(tile_ws, (int64_t)split_k * (BM * BN) * 4);
+        auto part_off = [&](int sp, int jn, int jm) -> uint32_t {
+            const int m = m0 + wm * WM + jm * 32 + r;
+            return m < M ? (uint32_t)(sp * (BM * BN) + (((wave * TN + jn) * TM + jm) * 64 + lane) * 16) * 4u
+                         : 0x80000000u;
         };
         static_for<TN>([&](auto jn_c) {
             constexpr int jn = decltype(jn_c)::value;
             static_for<TM>([&](auto jm_c) {
                 constexpr int jm = decltype(jm_c)::value;
-                float* dst = part(split, jn, jm);
+                const uint32_t off = part_off(split, jn, jm);
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
-                    *reinterpret_cast<f32x4*>(dst + 4 * g) =
-                        f32x4{acc[jn][jm][4 * g], acc[jn][jm][4 * g + 1], acc[jn][jm][4 * g + 2], acc[jn][jm][4 * g + 3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4, f32x4{acc[jn][jm][4 * g], acc[jn][jm][4 * g + 1], acc[jn][jm][4 * g + 2],
+                                                        acc[jn][jm][4 * g + 3]}),
+                        rs_ws, off + 16 * g, 0, 0);
             });
         });
         // Publish the partial and count arrivals; only the last workgroup of the tile goes on.
@@ -711,7 +856,6 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         static_for<TN>([&](auto i) {
             static_for<TM>([&](auto j) { acc[decltype(i)::value][decltype(j)::value] = f32x16{}; });
         });
-        const __amdgpu_buffer_rsrc_t rs_ws = make_rsrc(tile_ws, (int64_t)split_k * (BM * BN) * 4);
         f32x4 pb[TM * TN <= 4 ? 2 : 1][TN][TM][4];
         auto load_part = [&](int sp, auto set_tag) {
             constexpr int set = decltype(set_tag)::value;
@@ -720,7 +864,7 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
                 static_for<TM>([&](auto jm_c) {
                     constexpr int jm = decltype(jm_c)::value;
                     // sc0 loads miss this CU's L1 (which may hold stale lines) and read the L2
-                    const uint32_t off = (uint32_t)((part(sp, jn, jm) - tile_ws) * 4);
+                    const uint32_t off = part_off(sp, jn, jm);
 #pragma unroll
                     for (int g = 0; g < 4; ++g)
                         pb[set][jn][jm][g] = __builtin_bit_cast(
@@ -763,17 +907,6 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     // ------------------------------------------------------------------ epilogue
     // All accumulator indexing is in compile-time-unrolled loops (static_for): a runtime
     // index would demote the accumulator array to scratch memory.
-    const float alpha = p.alpha;
-    constexpr bool kF32 = EPI == kEpiF32;
-    constexpr bool kSR = EPI == kEpiBf16SR;
-    constexpr bool kFp8 = EPI == kEpiFp8;
-    using OutT = typename Cond<kF32, float, typename Cond<kFp8, uint8_t, uint16_t>::type>::type;
-    OutT* dbase = reinterpret_cast<OutT*>(d_base);
-    const OutT* bp = reinterpret_cast<const OutT*>(p.bias);
-    const bool acc_old = p.accumulate, bias = p.has_bias, vec = p.vec_store;
-    auto to_f = [](OutT x) -> float {
-        if constexpr (kF32) return x; else if constexpr (kFp8) return 0.f; else return bf16_to_f32(x);
-    };
     static_for<TM>([&](auto jm_c) {
         constexpr int jm = decltype(jm_c)::value;
         const int m = m0 + wm * WM + jm * 32 + r;
@@ -781,129 +914,10 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         bool pad_row = false;
         if (gemm_type == kMGroupedPsum) pad_row = m >= valid_end;
         else if (gemm_type == kMGroupedIdx) pad_row = row_ok && p.layout[m] != group;
-        OutT* drow = dbase + (int64_t)m * p.ldd;
         static_for<TN>([&](auto jn_c) {
             constexpr int jn = decltype(jn_c)::value;
             if (kRagged && jn >= TN_LAST && wn == WGN - 1) return;   // no such block in this wave
-            const int nblk = n0 + wn * WN + jn * 32;                  // wave-uniform
-            // the lane holds columns nblk + 8 g + 4 q + {0..3} in elements 4 g + {0..3}
-            float v[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = acc[jn][jm][i] * alpha;
-            if constexpr (kFp8) {
-                // Quantise the bf16-rounded outputs per 32 columns of a row: this lane holds 16 of
-                // them, its partner lane (q ^ 1) the other 16.  The host guarantees n % 128 == 0, so
-                // a block is either entirely inside the row or entirely past it.
-                uint32_t amax = 0;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const uint16_t h = f32_to_bf16_rne(v[i]);
-                    v[i] = bf16_to_f32(h);
-                    amax = max(amax, (uint32_t)(h & 0x7fffu));
-                }
-                amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32));
-                const uint32_t sexp = ue8m0_of_bf16_amax(amax);
-                const float inv = __builtin_bit_cast(float, (254u - sexp) << 23);   // 2^(127 - s)
-                if (row_ok && nblk < N) {
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        int w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * g] * inv, v[4 * g + 1] * inv, 0, false);
-                        w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * g + 2] * inv, v[4 * g + 3] * inv, w, true);
-                        *reinterpret_cast<int*>(drow + nblk + 8 * g + 4 * q) = w;
-                    }
-                    if (q == 0) {
-                        const int64_t col = (int64_t)batch * N + nblk;
-                        p.sfd[((col >> 6) * p.sfd_ld + m) * 2 + ((col >> 5) & 1)] = (uint8_t)sexp;
-                    }
-                }
-            } else {
-            const bool full = vec && nblk + 32 <= N;                   // wave-uniform
-            if (full) {
-                if (bias) {
-#pragma unroll
-                    for (int g = 0; g < 4; ++g)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) v[4 * g + i] += to_f(bp[nblk + 8 * g + 4 * q + i]);
-                }
-                if (acc_old && row_ok) {
-#pragma unroll
-                    for (int g = 0; g < 4; ++g)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) v[4 * g + i] += to_f(drow[nblk + 8 * g + 4 * q + i]);
-                }
-                if constexpr (kF32) {
-                    if (row_ok) {
-#pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            f32x4 o = {v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
-                            if (pad_row) o = f32x4{0.f, 0.f, 0.f, 0.f};
-                            *reinterpret_cast<f32x4*>(drow + nblk + 8 * g + 4 * q) = o;
-                        }
-                    }
-                } else {
-                    // pk[g] = columns 8 g + 4 q + {0..3} as two bf16 pairs
-                    uint32_t pk[4][2];
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        if constexpr (kSR) {
-                            uint16_t o[4];
-                            sr_bf16_quartet(v + 4 * g, (uint32_t)(nblk + 8 * g + 4 * q) >> 2, o);
-                            pk[g][0] = pad_row ? 0u : (uint32_t)o[0] | ((uint32_t)o[1] << 16);
-                            pk[g][1] = pad_row ? 0u : (uint32_t)o[2] | ((uint32_t)o[3] << 16);
-                        } else {
-                            pk[g][0] = pad_row ? 0u : pack_bf16x2(v[4 * g], v[4 * g + 1]);
-                            pk[g][1] = pad_row ? 0u : pack_bf16x2(v[4 * g + 2], v[4 * g + 3]);
-                        }
-                    }
-                    // v_permlane32_swap regroups the wave halves: afterwards the lower half
-                    // (q = 0) holds columns 16..31 and the upper half (q = 1) columns 0..15 of
-                    // the block, i.e. 32 contiguous bytes per lane.
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const auto s02 = __builtin_amdgcn_permlane32_swap(pk[2][h], pk[0][h], false, false);
-                        const auto s13 = __builtin_amdgcn_permlane32_swap(pk[3][h], pk[1][h], false, false);
-                        pk[2][h] = s02[0]; pk[0][h] = s02[1];
-                        pk[3][h] = s13[0]; pk[1][h] = s13[1];
-                    }
-                    if (row_ok) {
-                        // q = 0: pk2 = 16..19, pk0 = 20..23, pk3 = 24..27, pk1 = 28..31
-                        // q = 1: pk2 = 0..3,   pk0 = 4..7,   pk3 = 8..11,  pk1 = 12..15
-                        uint16_t* dp = drow + nblk + (q ? 0 : 16);
-                        *reinterpret_cast<i32x4*>(dp) = i32x4{(int)pk[2][0], (int)pk[2][1], (int)pk[0][0], (int)pk[0][1]};
-                        *reinterpret_cast<i32x4*>(dp + 8) = i32x4{(int)pk[3][0], (int)pk[3][1], (int)pk[1][0], (int)pk[1][1]};
-                    }
-                }
-            } else if (row_ok && kSR) {
-                // ragged / unaligned block, stochastic rounding: columns past the row hash as zeros
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int n = nblk + 8 * g + 4 * q;
-                    float x[4];
-                    uint16_t o[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) x[i] = n + i < N ? v[4 * g + i] : 0.f;
-                    sr_bf16_quartet(x, (uint32_t)n >> 2, o);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (n + i < N) drow[n + i] = pad_row ? (uint16_t)0 : o[i];
-                }
-            } else if (row_ok) {
-                // ragged / unaligned block: element stores with bounds
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int n = nblk + 8 * g + 4 * q + i;
-                        if (n < N) {
-                            float x = v[4 * g + i];
-                            if (bias) x += to_f(bp[n]);
-                            if (acc_old) x += to_f(drow[n]);
-                            if constexpr (kF32) drow[n] = pad_row ? 0.f : x;
-                            else drow[n] = pad_row ? (uint16_t)0 : f32_to_bf16_rne(x);
-                        }
-                    }
-            }
-            }   // !kFp8
+            epilogue_block<EPI>(p, acc[jn][jm], d_base, m, row_ok, pad_row, n0 + wn * WN + jn * 32, N, batch, q);
         });
     });
 }

@@ -1,0 +1,387 @@
+// Skinny-M GEMM kernel for gfx950 (decode shapes: the whole of M fits one 32 MT-row tile).
+//
+// Same contract as gemm_kernel (D = alpha * A . B^T (+ bias | + D), per-32-K UE8M0 scales, the
+// epilogue variants of epilogue_block), specialised for M <= 32 MT, where the GEMM is a stream
+// of B through the CUs and the tile kernel's LDS ring cannot keep enough bytes in flight.
+//
+// A workgroup owns one 32 NB-column strip of D (all M rows).  Its NW waves split the strip's K
+// range between them in contiguous runs of groups of G 64-K blocks.  Each wave has a private ring of D group slots
+// in LDS that it fills with whole-line global->LDS loads (buffer_load ... lds: one instruction
+// moves 8 rows x 128 bytes) and reads back in the MFMA operand layout (ds_read_b128, the
+// tile kernel's bank swizzle); no other wave touches the ring, so the main loop has no
+// workgroup barrier, only vmcnt waits.  The few rows of A and the scales go straight to
+// registers through the same ring.  While group i runs its MFMAs, groups i + 1 .. i + D - 1
+// are in flight.  At the end the waves' partial tiles meet in LDS and are summed in wave
+// order (deterministic).  Long K with few strips is also cut across workgroups (split-K
+// through a workspace, as in gemm_kernel: the last workgroup of a strip sums the partials in
+// split order).
+//
+// MFMA operand layout (see gemm_kernel.hpp): for each 64-K block lane (r, q) needs, of row r,
+// the 16-byte pieces at bytes 32 j + 16 q (j < 2 for e4m3, j < 1 for e2m1; bf16: j < 4, one
+// per 32x32x16 K-step) and the UE8M0 byte q of the row's packed scale pair (int16 per row and
+// 64-K block, the low byte for K [0, 32)).
+#pragma once
+
+#include "gemm_kernel.hpp"
+
+namespace dg {
+
+// Ring geometry of a skinny kernel configuration (host and device).
+struct SkinnyShape {
+    int g;       // 64-K blocks per group (a group row is 128 bytes for e4m3 / bf16, 64 for e2m1 B)
+    int rg;      // bytes of one B row in a group slot
+    int loads;   // vector-memory instructions per group: B rows (1 KB each), A pieces, scale dwords
+};
+__host__ __device__ constexpr SkinnyShape skinny_shape(int kind, int mt, int nb) {
+    const int g = kind == kBF16 ? 1 : 2;
+    const int rbb = kind == kBF16 ? 128 : (kind == kFP8FP8 ? 64 : 32);
+    const int rg = g * rbb;
+    const int pa = kind == kBF16 ? 4 : (kind == kFP4FP4 ? 1 : 2);
+    return {g, rg, nb * 32 * rg / 1024 + mt * g * pa + (kind == kBF16 ? 0 : g * (nb + mt))};
+}
+
+// x >> sh, kept at its place in the instruction stream (volatile), so the compiler cannot move
+// it to where the loaded x has not been waited for yet.
+__device__ __forceinline__ int shift_at_use(int x, int sh) {
+    int y;
+    asm volatile("v_lshrrev_b32 %0, %1, %2" : "=v"(y) : "v"(sh), "v"(x));
+    return y;
+}
+
+template <int KIND, int MT, int NB, int NW, int D, int EPI>
+__global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const KParams p) {
+    constexpr bool kAFp4 = KIND == kFP4FP4;
+    constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
+    constexpr bool kBf16 = KIND == kBF16;
+    constexpr int kFmtA = kAFp4 ? kFmtE2M1 : kFmtE4M3;
+    constexpr int kFmtB = kBFp4 ? kFmtE2M1 : kFmtE4M3;
+    constexpr int BM = 32 * MT, BN = 32 * NB;
+    constexpr int RBA = kBf16 ? 128 : (kAFp4 ? 32 : 64);   // bytes of one row per 64-K block
+    constexpr int RBB = kBf16 ? 128 : (kBFp4 ? 32 : 64);
+    constexpr int PA = RBA / 32, PB = RBB / 32;            // 16-byte pieces per lane and block
+    constexpr SkinnyShape kShape = skinny_shape(KIND, MT, NB);
+    constexpr int G = kShape.g, RG = kShape.rg;
+    constexpr int SPR = RG / 16;                            // 16-byte slots of a B row
+    constexpr int RPI = 64 / SPR;                           // B rows per load instruction
+    constexpr int NDMA = BN / RPI;                          // load instructions per group slot
+    constexpr int SLOT = BN * RG;                           // bytes of one group slot
+    constexpr int NBLK = NB * MT;                           // 32x32 output blocks
+    constexpr int kLoads = kShape.loads;
+    static_assert(kLoads == NDMA + MT * G * PA + (kBf16 ? 0 : G * (NB + MT)), "loads per group");
+    static_assert(D >= 2 && (D - 1) * kLoads <= 63, "vmcnt range");
+    constexpr int RING = NW * D * SLOT, RED = NW * NBLK * 4096;
+    static_assert(RING <= 128 * 1024 && RED <= 128 * 1024, "LDS budget");
+    // the wave rings, reused for the wave reduction after the main loop
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[RING > RED ? RING : RED];
+    f32x4* const red = reinterpret_cast<f32x4*>(smem);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 31, q = lane >> 5;
+
+    // ------------------------------------------------------------------ strip and K range
+    const int split_k = p.split_k;
+    int t, split = 0;
+    if (split_k > 1) {
+        // grid = 8 * ceil(strips / 8) * split_k; all splits of a strip share blockIdx % 8 (XCD)
+        const int b = blockIdx.x, rr = b >> 3;
+        t = (rr / split_k) * 8 + (b & 7);
+        split = rr % split_k;
+        if (t >= p.num_tiles) return;
+    } else {
+        t = blockIdx.x;
+    }
+    const int tile_id = t;
+    const int nn = p.num_n_blocks;
+    int batch = 0;
+    if (p.gemm_type == kBatched) {
+        batch = t / nn;
+        t -= batch * nn;
+    }
+    const int n0 = t * BN;
+    const int M = p.m, N = p.n;
+    const uint8_t* a_base = p.a;
+    const uint8_t* b_base = p.b + (int64_t)n0 * p.ldb;
+    const uint16_t* sfa = p.sfa;
+    const uint16_t* sfb = p.sfb;
+    uint8_t* d_base = p.d;
+    if (p.gemm_type == kBatched) {
+        a_base += (int64_t)batch * p.bsa;
+        b_base += (int64_t)batch * p.bsb;
+        d_base += (int64_t)batch * p.bsd * p.out_esize;
+        if (!kBf16) {
+            sfa += (int64_t)batch * p.sfa_bs;
+            sfb += (int64_t)batch * p.sfb_bs;
+        }
+    }
+    const int rows_a = min(BM, M), rows_b = min(BN, N - n0);
+    const int nk64 = ceil_div(p.k, 64);
+    const int kb0 = split * p.split_stages;
+    const int kb1 = split_k > 1 ? min(nk64, kb0 + p.split_stages) : nk64;
+    // The workgroup's groups are dealt to its waves in contiguous runs (measured: contiguous
+    // per-wave K ranges stream long rows faster than groups interleaved over the waves).
+    const int ng = ceil_div(max(kb1 - kb0, 0), G);                 // groups of the workgroup
+    const int gpw = ceil_div(ng, NW);
+    const int gw0 = w * gpw;                                        // first group of this wave
+    const int ngw = max(0, min(ng, gw0 + gpw) - gw0);               // groups of this wave
+
+    const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(a_base, (int64_t)rows_a * p.lda);
+    const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(b_base, (int64_t)rows_b * p.ldb);
+    __amdgpu_buffer_rsrc_t rs_sa, rs_sb;
+    if constexpr (!kBf16) {
+        rs_sa = make_rsrc(sfa, (int64_t)nk64 * p.sfa_ld * 2);
+        rs_sb = make_rsrc(sfb + n0, ((int64_t)nk64 * p.sfb_ld - n0) * 2);
+    }
+    // Per-lane row offsets (rows past the operand read zeros) and scale-dword offsets: the packed
+    // scales of rows 2i and 2i + 1 share one dword (the leading dimension is even), so a lane
+    // loads the aligned dword of its row pair and shifts its byte ((row % 2) * 2 + q) down at
+    // use; the MFMA reads the low byte of the scale register.  (Byte loads would need a
+    // zero-extension that the compiler hoists to the top of the loop, which makes it wait for
+    // the ring's loads in flight.)
+    uint32_t va[MT], vsa[MT], vsb[NB];
+    const int sc_shift = 8 * ((r & 1) * 2 + q);
+#pragma unroll
+    for (int jm = 0; jm < MT; ++jm) {
+        const int row = jm * 32 + r;
+        va[jm] = row < rows_a ? (uint32_t)(row * p.lda) + 16 * q : kOOBOffset;
+        vsa[jm] = row < rows_a ? (uint32_t)((row & ~1) * 2) : kOOBOffset;
+    }
+#pragma unroll
+    for (int jn = 0; jn < NB; ++jn) {
+        const int row = jn * 32 + r;
+        vsb[jn] = row < rows_b ? (uint32_t)((row & ~1) * 2) : kOOBOffset;
+    }
+    // B load instruction i of a group: lane l fills LDS slot l % SPR of row i RPI + l / SPR with
+    // the row's 16-byte piece (slot ^ swizzle(row)) of the group.
+    int lk[NDMA];
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+        const int row = i * RPI + lane / SPR;
+        lk[i] = ((lane % SPR) ^ slot_swizzle<SPR>(row)) * 16;
+    }
+    uint32_t vrow[NDMA];   // (rows past the strip's end: out of range, zeros)
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+        const int row = i * RPI + lane / SPR;
+        vrow[i] = row < rows_b ? (uint32_t)(row * p.ldb + lk[i]) : kOOBOffset;
+    }
+    uint8_t* const ring = smem + w * (D * SLOT);
+    const int kbytes_a = p.kbytes_a, kbytes_b = p.kbytes_b;
+    const int sfa_step = (int)p.sfa_ld * 2, sfb_step = (int)p.sfb_ld * 2;
+
+    // ------------------------------------------------------------------ register ring
+    i32x4 fa[D][G][MT][PA];
+    int sa[D][G][MT], sb[D][G][NB];
+    // Group gi of this wave (64-K blocks kb0 + (gw0 + gi) G + j) into ring slot S; a group past
+    // the wave's range (or a block past K) loads zeros with no memory traffic.
+    auto load_group = [&](auto slot_tag, int gi) {
+        constexpr int S = decltype(slot_tag)::value;
+        const bool live = gi < ngw;
+        const int kbg = kb0 + (gw0 + gi) * G;
+        {
+            // B rows of the group: whole lines into the wave's ring slot S (a piece past K or past
+            // the strip's rows reads zeros)
+            const int left = live && kbg < kb1 ? kbytes_b - kbg * RBB : 0;
+            const int kend = (kb1 - kbg) * RBB;   // (a group straddling the split's end stops there)
+#pragma unroll
+            for (int i = 0; i < NDMA; ++i) {
+                const uint32_t v = lk[i] < left && lk[i] < kend ? vrow[i] : kOOBOffset;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, (lds_void*)(ring + S * SLOT + i * 1024), 16, v,
+                                                         __builtin_amdgcn_readfirstlane(kbg * RBB), 0, 0);
+            }
+        }
+        static_for<G>([&](auto j_c) {
+            constexpr int j = decltype(j_c)::value;
+            const int kb = kbg + j;
+            const bool on = live && kb < kb1;
+            const int left_a = on ? kbytes_a - kb * RBA : 0;   // bytes of the row left from this block
+            static_for<PA>([&](auto pc) {
+                constexpr int P = decltype(pc)::value;
+#pragma unroll
+                for (int jm = 0; jm < MT; ++jm) {
+                    const uint32_t v = 32 * P + 16 * q < left_a ? va[jm] + 32 * P : kOOBOffset;
+                    fa[S][j][jm][P] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_a, v, kb * RBA, 0));
+                }
+            });
+            if constexpr (!kBf16) {
+#pragma unroll
+                for (int jm = 0; jm < MT; ++jm)
+                    sa[S][j][jm] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_sa, on ? vsa[jm] : kOOBOffset, kb * sfa_step, 0);
+#pragma unroll
+                for (int jn = 0; jn < NB; ++jn)
+                    sb[S][j][jn] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_sb, on ? vsb[jn] : kOOBOffset, kb * sfb_step, 0);
+            }
+        });
+    };
+
+    f32x16 acc[NB][MT];
+#pragma unroll
+    for (int jn = 0; jn < NB; ++jn)
+#pragma unroll
+        for (int jm = 0; jm < MT; ++jm) acc[jn][jm] = f32x16{};
+
+    // B fragment piece P of block j, strip block jn, from ring slot S
+    auto b_piece = [&](int S, int j, int jn, int P) -> i32x4 {
+        const int R = jn * 32 + r;
+        const int slot = (j * RBB + 32 * P) / 16 + q;
+        return *reinterpret_cast<const i32x4*>(ring + S * SLOT + R * RG + ((slot ^ slot_swizzle<SPR>(R)) << 4));
+    };
+    auto compute = [&](auto slot_tag) {
+        constexpr int S = decltype(slot_tag)::value;
+        // this slot's loads are the oldest D - 1 groups back (the ring's LDS writes are not
+        // visible to the compiler's own wait counting; the memory clobber keeps the LDS reads
+        // below)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((D - 1) * kLoads) : "memory");
+        i32x4 fb[G][NB][PB];
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+#pragma unroll
+            for (int jn = 0; jn < NB; ++jn)
+#pragma unroll
+                for (int P = 0; P < PB; ++P) fb[j][jn][P] = b_piece(S, j, jn, P);
+        static_for<G>([&](auto j_c) {
+            constexpr int j = decltype(j_c)::value;
+#pragma unroll
+            for (int jn = 0; jn < NB; ++jn)
+#pragma unroll
+                for (int jm = 0; jm < MT; ++jm) {
+                    if constexpr (kBf16) {
+#pragma unroll
+                        for (int s = 0; s < 4; ++s)
+                            acc[jn][jm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                __builtin_bit_cast(bf16x8, fb[j][jn][s]), __builtin_bit_cast(bf16x8, fa[S][j][jm][s]),
+                                acc[jn][jm], 0, 0, 0);
+                    } else {
+                        const i32x4 b0 = fb[j][jn][0], a0 = fa[S][j][jm][0];
+                        i32x4 b1 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+                        if constexpr (PB > 1) b1 = fb[j][jn][1];
+                        if constexpr (PA > 1) a1 = fa[S][j][jm][1];
+                        const i32x8 bf = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+                        const i32x8 af = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+                        acc[jn][jm] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                            bf, af, acc[jn][jm], kFmtB, kFmtA, 0, shift_at_use(sb[S][j][jn], sc_shift), 0,
+                            shift_at_use(sa[S][j][jm], sc_shift));
+                    }
+                }
+        });
+    };
+
+    // ------------------------------------------------------------------ main loop
+    // (groups issued in ring order, as in the loop, so that the compiler's wait counts at the loop
+    // head see the same load order from both predecessors)
+    static_for<D - 1>([&](auto s) {
+        load_group(s, decltype(s)::value);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    for (int i = 0; i < ngw; i += D) {
+        static_for<D>([&](auto s_c) {
+            constexpr int s = decltype(s_c)::value;
+            load_group(Int<(s + D - 1) % D>{}, i + s + D - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(Int<s>{});   // (a group past the wave's range holds zeros: adds nothing)
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+
+    // ------------------------------------------------------------------ wave reduction
+    // red[((w * NBLK + blk) * 4 + g) * 64 + lane] = elements 4 g .. 4 g + 3 of the wave's block,
+    // over the rings once every wave is done with them (loads past a wave's range may still be
+    // landing in its ring: wait for them first).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+#pragma unroll
+    for (int jn = 0; jn < NB; ++jn)
+#pragma unroll
+        for (int jm = 0; jm < MT; ++jm)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                red[((w * NBLK + jn * MT + jm) * 4 + g) * 64 + lane] =
+                    f32x4{acc[jn][jm][4 * g], acc[jn][jm][4 * g + 1], acc[jn][jm][4 * g + 2], acc[jn][jm][4 * g + 3]};
+    __syncthreads();
+    // Block blk is summed (waves in order) and finished by wave blk % NW.
+    f32x16 out[NB][MT];
+#pragma unroll
+    for (int jn = 0; jn < NB; ++jn)
+#pragma unroll
+        for (int jm = 0; jm < MT; ++jm) {
+            out[jn][jm] = f32x16{};
+            if ((jn * MT + jm) % NW != w) continue;
+            for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 v = red[((ww * NBLK + jn * MT + jm) * 4 + g) * 64 + lane];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) out[jn][jm][4 * g + i] += v[i];
+                }
+        }
+
+    // ------------------------------------------------------------------ split-K across workgroups
+    if (split_k > 1) {
+        // Partials in accumulator-register order; lanes of rows past M take an offset past the
+        // buffer's end (no bytes move for them).
+        float* const tile_ws = p.ws + (int64_t)tile_id * split_k * (NBLK * 1024);
+        const __amdgpu_buffer_rsrc_t rs_ws = make_rsrc(tile_ws, (int64_t)split_k * NBLK * 1024 * 4);
+        auto part_off = [&](int sp, int blk, int jm) -> uint32_t {
+            return jm * 32 + r < M ? (uint32_t)((sp * NBLK + blk) * 1024 + lane * 16) * 4u : kOOBOffset;
+        };
+#pragma unroll
+        for (int jn = 0; jn < NB; ++jn)
+#pragma unroll
+            for (int jm = 0; jm < MT; ++jm) {
+                if ((jn * MT + jm) % NW != w) continue;
+                const uint32_t off = part_off(split, jn * MT + jm, jm);
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4, f32x4{out[jn][jm][4 * g], out[jn][jm][4 * g + 1], out[jn][jm][4 * g + 2],
+                                                        out[jn][jm][4 * g + 3]}),
+                        rs_ws, off + 16 * g, 0, 0);
+            }
+        // Arrival count, as in gemm_kernel: on the strip's home XCD the stores only need to
+        // reach that XCD's L2; elsewhere they are made visible device-wide and the counter says so.
+        const int xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xf;   // HW_REG_XCC_ID[3:0]
+        const bool home = xcc == (int)(blockIdx.x & 7);
+        if (home) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else __threadfence();
+        __syncthreads();
+        int* flag = reinterpret_cast<int*>(red);
+        if (tid == 0)
+            *flag = __hip_atomic_fetch_add(p.counters + tile_id, home ? 1 : 1 + (1 << 16), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const int prev = *flag;
+        if ((prev & 0xffff) != split_k - 1) return;
+        if (!home || (prev >> 16) != 0) __threadfence();
+#pragma unroll
+        for (int jn = 0; jn < NB; ++jn)
+#pragma unroll
+            for (int jm = 0; jm < MT; ++jm) {
+                if ((jn * MT + jm) % NW != w) continue;
+                out[jn][jm] = f32x16{};
+                for (int sp = 0; sp < split_k; ++sp) {
+                    const uint32_t off = part_off(sp, jn * MT + jm, jm);
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const f32x4 v = __builtin_bit_cast(
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_ws, off + 16 * g, 0, kCacheSc0));
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) out[jn][jm][4 * g + i] += v[i];
+                    }
+                }
+            }
+        if (tid == 0) __hip_atomic_store(p.counters + tile_id, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // ------------------------------------------------------------------ epilogue
+#pragma unroll
+    for (int jn = 0; jn < NB; ++jn)
+#pragma unroll
+        for (int jm = 0; jm < MT; ++jm) {
+            if ((jn * MT + jm) % NW != w) continue;
+            const int m = jm * 32 + r;
+            epilogue_block<EPI>(p, out[jn][jm], d_base, m, m < M, false, n0 + jn * 32, N, batch, q);
+        }
+}
+
+}  // namespace dg

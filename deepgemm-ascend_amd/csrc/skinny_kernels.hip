@@ -1,0 +1,46 @@
+// Instantiates the skinny-M kernel (csrc/skinny_kernel.hpp) for every configuration of the
+// kSkinny menu, operand kind and epilogue.
+#include "gemm_tiles.hpp"
+#include "skinny_kernel.hpp"
+
+namespace dg {
+namespace {
+
+template <int I, int KIND>
+KernelFn skinny_epi(int epi) {
+    constexpr SkinnyCfg c = kSkinny[I];
+    switch (epi) {
+        case kEpiF32: return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, kEpiF32>;
+        case kEpiBf16: return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, kEpiBf16>;
+        case kEpiBf16SR: return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, kEpiBf16SR>;
+        case kEpiFp8:
+            if constexpr (KIND == kFP8FP8) return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, kEpiFp8>;
+            else return nullptr;
+        default: return nullptr;
+    }
+}
+
+template <int KIND, int I = 0>
+KernelFn skinny_find(int mt, int nb, int nw, int d, int epi) {
+    if constexpr (I == kNumSkinny) {
+        return nullptr;
+    } else {
+        if (mt == kSkinny[I].mt && nb == kSkinny[I].nb && nw == kSkinny[I].nw && d == kSkinny[I].d)
+            return skinny_epi<I, KIND>(epi);
+        return skinny_find<KIND, I + 1>(mt, nb, nw, d, epi);
+    }
+}
+
+}  // namespace
+
+KernelFn lookup_skinny(int kind, int mt, int nb, int nw, int d, int epi) {
+    switch (kind) {
+        case kFP8FP8: return skinny_find<kFP8FP8>(mt, nb, nw, d, epi);
+        case kFP8FP4: return skinny_find<kFP8FP4>(mt, nb, nw, d, epi);
+        case kFP4FP4: return skinny_find<kFP4FP4>(mt, nb, nw, d, epi);
+        case kBF16: return skinny_find<kBF16>(mt, nb, nw, d, epi);
+        default: return nullptr;
+    }
+}
+
+}  // namespace dg

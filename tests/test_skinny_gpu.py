@@ -1,0 +1,153 @@
+"""The skinny-M kernel (csrc/skinny_kernel.hpp) on every configuration of its menu, forced through
+the DG_SKINNY tuning override ("mt,nb,nw,d[,split]"), against the CPU oracle (calc_diff < 1e-5):
+ragged N (strips past the row end), K ending inside a 64-K block and inside a wave's group, K
+split across workgroups, every operand kind, fp32 accumulate and bias, batched launches, and
+the bit-exact epilogues (stochastic rounding, FP8 output) against the same launch's fp32 / bf16
+output.  The heuristic's own choice for decode shapes is covered by the default-path tests."""
+import pytest
+import torch
+
+import deep_gemm
+from oracle import gemm as og, epilogue as oe
+from helpers import gen, operand, calc_diff
+
+pytestmark = pytest.mark.gpu
+THRESH = 1e-5
+# (config, M values it serves): the kSkinny menu of csrc/gemm_tiles.hpp, plus forced K splits
+CONFIGS = ['1,1,4,2', '1,1,4,3', '1,1,4,4', '1,1,8,2', '1,1,8,3', '1,2,4,2', '2,1,4,2', '2,1,4,3',
+           '2,1,8,2', '4,1,4,2', '4,1,8,2', '1,1,4,3,3', '2,1,4,3,5', '1,2,4,2,2', '1,1,8,2,4']
+
+
+def _ms(cfg):
+    mt = int(cfg.split(',')[0])
+    return sorted({1, 32 * mt - 3, 32 * mt})
+
+
+@pytest.fixture
+def skinny(monkeypatch):
+    def _set(cfg):
+        monkeypatch.setenv('DG_SKINNY', cfg)
+    return _set
+
+
+@pytest.mark.parametrize('cfg', CONFIGS)
+@pytest.mark.parametrize('kinds', [('e4m3', 'e4m3'), ('e4m3', 'e2m1'), ('e2m1', 'e2m1')])
+def test_skinny_kinds(skinny, cfg, kinds):
+    n, k = 500, 1040   # N: a partial last strip; K: 16 64-K blocks and a 16-element tail
+    skinny(cfg)
+    g = gen(31)
+    b, sfb, b_deq = operand(n, k, kinds[1], (1, 32), g)
+    for m in _ms(cfg):
+        print(f'skinny {cfg} {kinds} m={m} n={n} k={k}', flush=True)
+        a, sfa, a_deq = operand(m, k, kinds[0], (1, 32), g)
+        out = torch.float32 if kinds[0] == 'e2m1' else torch.bfloat16
+        d = torch.empty(m, n, dtype=out, device='cuda')
+        deep_gemm.fp8_fp4_gemm_nt((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d)
+        torch.cuda.synchronize()
+        assert calc_diff(d.cpu(), og.gemm_nt(a_deq, b_deq, out)) < THRESH
+
+
+@pytest.mark.parametrize('cfg', CONFIGS)
+@pytest.mark.parametrize('k', [64, 192, 7168])
+def test_skinny_fp8_accumulate_bias(skinny, cfg, k):
+    """fp32 D += A . B^T (c aliases d), then bf16 D with a bias row; the 1x128 / 128x128 recipe."""
+    m, n = int(cfg.split(',')[0]) * 32 - 1, 230
+    print(f'skinny {cfg} fp8 accumulate/bias m={m} n={n} k={k}', flush=True)
+    skinny(cfg)
+    g = gen(32)
+    a, sfa, a_deq = operand(m, k, 'e4m3', (1, 128), g, mode='randn')
+    b, sfb, b_deq = operand(n, k, 'e4m3', (128, 128), g, mode='randn')
+    args = ((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()))
+    ref = og.gemm_nt(a_deq, b_deq, torch.float32)
+    c = torch.randn(m, n, generator=g)
+    d = c.clone().cuda()
+    deep_gemm.fp8_gemm_nt(*args, d, c=d, recipe_a=(1, 128), recipe_b=(128, 128))
+    torch.cuda.synchronize()
+    assert calc_diff(d.cpu(), ref + c) < THRESH
+    bias = torch.randn(1, n, generator=g).bfloat16()
+    d16 = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
+    deep_gemm.fp8_gemm_nt(*args, d16, c=bias.cuda(), recipe_a=(1, 128), recipe_b=(128, 128))
+    torch.cuda.synchronize()
+    assert calc_diff(d16.cpu(), ref + bias.float()) < THRESH
+
+
+@pytest.mark.parametrize('cfg', CONFIGS)
+def test_skinny_bf16(skinny, cfg):
+    n, k = 300, 1000
+    skinny(cfg)
+    g = gen(33)
+    b = (torch.randn(n, k, generator=g) * 0.1).to(torch.bfloat16)
+    for m in _ms(cfg):
+        print(f'skinny {cfg} bf16 m={m} n={n} k={k}', flush=True)
+        a = (torch.randn(m, k, generator=g) * 0.1).to(torch.bfloat16)
+        d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
+        deep_gemm.bf16_gemm_nt(a.cuda(), b.cuda(), d)
+        torch.cuda.synchronize()
+        assert calc_diff(d.cpu(), og.gemm_nt(a.float(), b.float())) < THRESH
+
+
+@pytest.mark.parametrize('cfg', ['1,1,4,3', '2,1,4,2,2'])
+def test_skinny_bmm(skinny, cfg):
+    bs, m, n, k = 3, 17, 192, 640
+    print(f'skinny {cfg} bmm bs={bs} m={m} n={n} k={k}', flush=True)
+    skinny(cfg)
+    g = gen(34)
+    a, sfa, a_deq = operand(m, k, 'e4m3', (1, 32), g, 'randn', batch=bs)
+    b, sfb, b_deq = operand(n, k, 'e4m3', (1, 32), g, 'randn', batch=bs)
+    d = torch.empty(bs, m, n, dtype=torch.bfloat16, device='cuda')
+    deep_gemm.fp8_bmm((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d)
+    torch.cuda.synchronize()
+    for i in range(bs):
+        assert calc_diff(d[i].cpu(), og.gemm_nt(a_deq[i], b_deq[i])) < THRESH
+
+
+@pytest.mark.parametrize('cfg', ['1,1,4,3', '1,2,4,2,2'])
+def test_skinny_epilogues_bit_exact(skinny, cfg):
+    """Stochastic rounding: bit-exact against the hash of the same launch plan's fp32 output;
+    FP8 output: bit-exact against quantising its bf16 output per (row, 32 columns)."""
+    bs, m, n, k = 2, 9, 256, 512
+    print(f'skinny {cfg} SR / FP8 output bs={bs} m={m} n={n} k={k}', flush=True)
+    skinny(cfg)
+    g = gen(35)
+    a, sfa, _ = operand(m, k, 'e4m3', (1, 32), g, 'randn')
+    b, sfb, _ = operand(n, k, 'e4m3', (1, 32), g, 'randn')
+    args = ((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()))
+    f32 = torch.empty(m, n, device='cuda')
+    deep_gemm.fp8_gemm_nt(*args, f32)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
+    deep_gemm.fp8_gemm_nt(*args, out, epilogue=deep_gemm.epilogue.BF16StochasticRounding())
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu().view(torch.int16), oe.stochastic_round_bf16(f32).cpu().view(torch.int16))
+
+    a3, sfa3, _ = operand(m, k, 'e4m3', (1, 32), g, 'randn', batch=bs)
+    b3, sfb3, _ = operand(n, k, 'e4m3', (1, 32), g, 'randn', batch=bs)
+    args3 = ((a3.cuda(), sfa3.cuda()), (b3.cuda(), sfb3.cuda()))
+    # (FP8 output: D stored [M, B, N], as the SFD layout requires)
+    d_bf16 = torch.empty(m, bs, n, dtype=torch.bfloat16, device='cuda').transpose(0, 1)
+    deep_gemm.fp8_bmm(*args3, d_bf16)
+    fp8 = torch.empty(m, bs, n, dtype=torch.float8_e4m3fn, device='cuda').transpose(0, 1)
+    sfd = torch.empty_strided((m, bs * n // 64), (1, m), device='cuda', dtype=torch.int16)
+    deep_gemm.fp8_bmm(*args3, fp8, epilogue=deep_gemm.epilogue.FP8Quantization(sfd))
+    torch.cuda.synchronize()
+    ref_fp8, ref_sfd = oe.quantize_fp8_output(d_bf16.transpose(0, 1).cpu().reshape(m, bs * n))
+    assert torch.equal(fp8.transpose(0, 1).cpu().view(torch.uint8).reshape(m, bs * n), ref_fp8.view(torch.uint8))
+    assert torch.equal(sfd.cpu(), ref_sfd)
+
+
+@pytest.mark.parametrize('m,n,k', [(1, 2112, 7168), (1, 7168, 2048), (16, 4096, 7168), (5, 24576, 1536)])
+def test_skinny_default_plan_vs_tile_kernel(monkeypatch, m, n, k):
+    """Decode shapes on the heuristic's skinny plan agree with the tile kernel (DG_SKINNY=0) and
+    with the oracle."""
+    print(f'skinny default plan m={m} n={n} k={k}', flush=True)
+    g = gen(36)
+    a, sfa, a_deq = operand(m, k, 'e4m3', (1, 128), g, 'randn')
+    b, sfb, b_deq = operand(n, k, 'e4m3', (128, 128), g, 'randn')
+    args = ((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()))
+    d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
+    deep_gemm.fp8_gemm_nt(*args, d, recipe_a=(1, 128), recipe_b=(128, 128))
+    monkeypatch.setenv('DG_SKINNY', '0')
+    d0 = torch.empty_like(d)
+    deep_gemm.fp8_gemm_nt(*args, d0, recipe_a=(1, 128), recipe_b=(128, 128))
+    torch.cuda.synchronize()
+    assert calc_diff(d.cpu(), og.gemm_nt(a_deq, b_deq)) < THRESH
+    assert calc_diff(d.cpu(), d0.cpu()) < 1e-6
