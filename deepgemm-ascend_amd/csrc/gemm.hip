@@ -82,6 +82,7 @@ struct Plan {
     int split_stages;   // K stages per range (skinny kernel: 64-K blocks per range)
     int skinny_nw;      // > 0: the skinny-M kernel with this many waves (tile = 32 mt x 32 nb)
     int skinny_d;       // its ring depth
+    int skinny_ar;      // and rows of A it stages
 };
 
 // K elements of one kernel stage of tile t
@@ -134,37 +135,43 @@ bool skinny_plan(const dg_gemm_args& a, int cus, bool allow_split, Plan& out) {
         sp = std::max(1, std::min(sp, 16));
     }
     const int sps = ceil_div(ns, sp);
-    out = {tc, ceil_div(ns, sps), sps, 0, 0};
+    out = {tc, ceil_div(ns, sps), sps, 0, 0, 0};
     return true;
 }
 
-// DG_SKINNY (tuning override): "0" = never use the skinny-M kernel, "mt,nb,nw,d[,split]" = use
-// that configuration wherever M fits it.
+// DG_SKINNY (tuning override): "0" = never use the skinny-M kernel, "mt,nb,nw,d,ar[,split]" =
+// use that configuration wherever M fits it.
 struct SkinnyEnv {
     int mode;   // -1 default, 0 off, 1 forced configuration
-    int mt, nb, nw, d, split;
+    int mt, nb, nw, d, ar, split;
 };
 SkinnyEnv skinny_env() {
-    SkinnyEnv e = {-1, 0, 0, 0, 0, 0};
+    SkinnyEnv e = {-1, 0, 0, 0, 0, 0, 0};
     const char* s = std::getenv("DG_SKINNY");
     if (s == nullptr || *s == '\0') return e;
     if (std::strcmp(s, "0") == 0) { e.mode = 0; return e; }
-    if (std::sscanf(s, "%d,%d,%d,%d,%d", &e.mt, &e.nb, &e.nw, &e.d, &e.split) >= 4) e.mode = 1;
+    if (std::sscanf(s, "%d,%d,%d,%d,%d,%d", &e.mt, &e.nb, &e.nw, &e.d, &e.ar, &e.split) >= 5) e.mode = 1;
     return e;
 }
 
-// Decode shapes (M <= 16, dense or batched) stream B through the skinny-M kernel: one
-// workgroup per 32-column strip, its four waves splitting K, and a K split across workgroups
-// only while the strips alone leave CUs idle (each range keeps at least four 64-K blocks per
-// wave).  Measured on MI355X (fp8, M = 1, kernel us, tile kernel in brackets): 2112x7168 8.5
-// (15.0), 7168x2048 5.6 (13.5), 24576x1536 10.4 (11.7), 7168x16384 26.5 (32.1), 4096x7168
-// 9.9 (15.8).  Larger M loads A rows straight to registers and loses to the tile kernel.
+// Decode shapes (dense or batched, M <= 128) stream B through the skinny-M kernel: one
+// workgroup per 32-column strip, its four waves splitting K, A staged for the M it holds, and a
+// K split across workgroups only while the strips alone leave CUs idle (each range keeps at
+// least four 64-K blocks per wave).  Measured on MI355X (fp8, kernel us, tile kernel in
+// brackets): M = 1: 2112x7168 8.8 (15.0), 7168x2048 5.7 (13.2), 24576x1536 10.3 (11.5),
+// 7168x16384 26.9 (31.7); M = 32: 2112x7168 9.9 (17.1), 7168x2048 6.3 (14.8); M = 64:
+// 7168x2048 8.0 (15.9), 4096x7168 14.5 (20.2); M = 128: 7168x2048 11.7 (14.2).  Past 16 rows
+// of A, more than two strips per CU (N = 24576) favour the tile kernel (M = 64: 20.1 vs 15.4).
 bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const SkinnyEnv& env, Plan& out) {
     if (env.mode == 0 || !(a.gemm_type == kNormal || a.gemm_type == kBatched)) return false;
-    int mt = 1, nb = 1, nw = 4, d = 2;
-    if (env.mode == 1) { mt = env.mt; nb = env.nb; nw = env.nw; d = env.d; }
-    else if (a.m > 16) return false;
-    if (a.m > 32 * mt || lookup_skinny(a.kind, mt, nb, nw, d, kEpiBf16) == nullptr) return false;
+    const int groups0 = a.gemm_type == kBatched ? a.num_groups : 1;
+    int mt = a.m <= 32 ? 1 : (a.m <= 64 ? 2 : 4), nb = 1, nw = 4, d = 2, ar = a.m <= 16 ? 16 : 32 * mt;
+    if (env.mode == 1) {
+        mt = env.mt; nb = env.nb; nw = env.nw; d = env.d; ar = env.ar;
+    } else if (a.m > 128 || (a.m > 16 && (int64_t)ceil_div(a.n, 32) * groups0 > 2 * (int64_t)cus)) {
+        return false;
+    }
+    if (a.m > ar || lookup_skinny(a.kind, mt, nb, nw, d, ar, kEpiBf16) == nullptr) return false;
     const int groups = a.gemm_type == kBatched ? a.num_groups : 1;
     const int64_t strips = (int64_t)ceil_div(a.n, 32 * nb) * groups;
     const int nk64 = std::max(1, ceil_div(a.k, 64));
@@ -175,7 +182,7 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
         sp = std::max(1, std::min(sp, std::min(16, nk64)));
     }
     const int ss = ceil_div(nk64, sp);
-    out = {{32 * mt, 32 * nb, 0, nw, 0, 0, 0, 0, 0}, ceil_div(nk64, ss), ss, nw, d};
+    out = {{32 * mt, 32 * nb, 0, nw, 0, 0, 0, 0, 0}, ceil_div(nk64, ss), ss, nw, d, ar};
     return true;
 }
 
@@ -193,7 +200,7 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     // fp32 D of the same call, with the same K split and summation order.)
     const double hbm_bytes = esz * ((double)a.m + a.n) * a.k * groups + 2.0 * a.m * a.n * groups;
     double best = 1e300;
-    Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0, 0}, 1, 1, 0, 0};
+    Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0, 0}, 1, 1, 0, 0, 0};
     for (int i = 0; i < kNumTiles; ++i) {
         const TileCfg& tc = kTiles[i];
         if (!tile_allowed(a, tc.bm, tc.bn)) continue;
@@ -221,7 +228,7 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
             t = std::max(t, bytes / 3800.0);
             if (t < best * 0.97) {
                 best = t;
-                pick = {tc, sp, sps, 0, 0};
+                pick = {tc, sp, sps, 0, 0, 0};
             }
         }
     }
@@ -254,7 +261,7 @@ Plan choose(const dg_gemm_args& a, int cus, bool allow_split) {
         const int ns = ceil_div(a.k, k_stage_elems(a.kind, t));
         int sp = allow_split && tile_splittable(t) && a.split_k > 1 && plan_tiles(a, t) <= kMaxSplitTiles ? std::min(a.split_k, std::max(1, ns)) : 1;
         const int sps = ceil_div(ns, sp);
-        return {t, ceil_div(ns, sps), sps, 0, 0};
+        return {t, ceil_div(ns, sps), sps, 0, 0, 0};
     }
     MemoKey key;
     memset(&key, 0, sizeof(key));
@@ -405,7 +412,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only) {
     const bool jit = a.jit && !skinny;
     if (skinny && compile_only) return DG_OK;
     KernelFn fn = jit ? nullptr
-                : skinny ? lookup_skinny(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_nw, plan.skinny_d, epi_kind)
+                : skinny ? lookup_skinny(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_nw, plan.skinny_d, plan.skinny_ar, epi_kind)
                          : lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind);
     if (fn == nullptr && !jit) {
         char buf[160];

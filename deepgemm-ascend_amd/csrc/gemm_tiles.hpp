@@ -75,16 +75,16 @@ inline int tile_threads(int bm, int bn) {
 int jit_run(const dg_gemm_args& a, const TileCfg& cfg, int epi, int split, const KParams& p, int64_t grid,
             hipStream_t st, bool compile_only);
 
-// Skinny-M kernels (csrc/skinny_kernel.hpp): strips of 32 nb columns, M <= 32 mt, nw waves
-// splitting K, each with a ring of d group slots.
+// Skinny-M kernels (csrc/skinny_kernel.hpp): strips of 32 nb columns, M <= ar (<= 32 mt) rows of
+// A, nw waves splitting K, each with a ring of d group slots.
 struct SkinnyCfg {
-    int mt, nb, nw, d;
+    int mt, nb, nw, d, ar;
 };
-constexpr SkinnyCfg kSkinny[] = {{1, 1, 4, 2}, {1, 1, 4, 3}, {1, 1, 4, 4}, {1, 1, 8, 2}, {1, 1, 8, 3},
-                                 {1, 2, 4, 2}, {2, 1, 4, 2}, {2, 1, 4, 3}, {2, 1, 8, 2},
-                                 {4, 1, 4, 2}, {4, 1, 8, 2}};
+constexpr SkinnyCfg kSkinny[] = {{1, 1, 4, 2, 16}, {1, 1, 4, 3, 16}, {1, 1, 4, 2, 32}, {1, 1, 4, 3, 32},
+                                 {1, 1, 8, 2, 16}, {1, 2, 4, 2, 16}, {2, 1, 4, 2, 64},
+                                 {4, 1, 4, 2, 128}};
 constexpr int kNumSkinny = sizeof(kSkinny) / sizeof(kSkinny[0]);
-KernelFn lookup_skinny(int kind, int mt, int nb, int nw, int d, int epi);
+KernelFn lookup_skinny(int kind, int mt, int nb, int nw, int d, int ar, int epi);
 
 KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi);
 KernelFn lookup_kernel_fp8fp4(int bm, int bn, int epi);

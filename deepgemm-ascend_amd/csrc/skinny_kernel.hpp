@@ -9,8 +9,9 @@
 // in LDS that it fills with whole-line global->LDS loads (buffer_load ... lds: one instruction
 // moves 8 rows x 128 bytes) and reads back in the MFMA operand layout (ds_read_b128, the
 // tile kernel's bank swizzle); no other wave touches the ring, so the main loop has no
-// workgroup barrier, only vmcnt waits.  The few rows of A and the scales go straight to
-// registers through the same ring.  While group i runs its MFMAs, groups i + 1 .. i + D - 1
+// workgroup barrier, only vmcnt waits.  The first AR rows of A travel the same way (rows of
+// the 32 MT-row tile past AR are zeros: AR is sized to the M the configuration serves), the
+// scales go straight to registers.  While group i runs its MFMAs, groups i + 1 .. i + D - 1
 // are in flight.  At the end the waves' partial tiles meet in LDS and are summed in wave
 // order (deterministic).  Long K with few strips is also cut across workgroups (split-K
 // through a workspace, as in gemm_kernel: the last workgroup of a strip sums the partials in
@@ -28,16 +29,16 @@ namespace dg {
 
 // Ring geometry of a skinny kernel configuration (host and device).
 struct SkinnyShape {
-    int g;       // 64-K blocks per group (a group row is 128 bytes for e4m3 / bf16, 64 for e2m1 B)
+    int g;       // 64-K blocks per group (a group row is 128 bytes for e4m3 / bf16, 64 for e2m1)
     int rg;      // bytes of one B row in a group slot
-    int loads;   // vector-memory instructions per group: B rows (1 KB each), A pieces, scale dwords
+    int rga;     // bytes of one A row in a group slot
+    int loads;   // vector-memory instructions per group: B and A rows (1 KB each), scale dwords
 };
-__host__ __device__ constexpr SkinnyShape skinny_shape(int kind, int mt, int nb) {
+__host__ __device__ constexpr SkinnyShape skinny_shape(int kind, int mt, int nb, int ar) {
     const int g = kind == kBF16 ? 1 : 2;
-    const int rbb = kind == kBF16 ? 128 : (kind == kFP8FP8 ? 64 : 32);
-    const int rg = g * rbb;
-    const int pa = kind == kBF16 ? 4 : (kind == kFP4FP4 ? 1 : 2);
-    return {g, rg, nb * 32 * rg / 1024 + mt * g * pa + (kind == kBF16 ? 0 : g * (nb + mt))};
+    const int rg = g * (kind == kBF16 ? 128 : (kind == kFP8FP8 ? 64 : 32));
+    const int rga = g * (kind == kBF16 ? 128 : (kind == kFP4FP4 ? 32 : 64));
+    return {g, rg, rga, (nb * 32 * rg + ar * rga) / 1024 + (kind == kBF16 ? 0 : g * (nb + mt))};
 }
 
 // x >> sh, kept at its place in the instruction stream (volatile), so the compiler cannot move
@@ -48,7 +49,7 @@ __device__ __forceinline__ int shift_at_use(int x, int sh) {
     return y;
 }
 
-template <int KIND, int MT, int NB, int NW, int D, int EPI>
+template <int KIND, int MT, int NB, int NW, int D, int AR, int EPI>
 __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const KParams p) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
@@ -59,18 +60,20 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
     constexpr int RBA = kBf16 ? 128 : (kAFp4 ? 32 : 64);   // bytes of one row per 64-K block
     constexpr int RBB = kBf16 ? 128 : (kBFp4 ? 32 : 64);
     constexpr int PA = RBA / 32, PB = RBB / 32;            // 16-byte pieces per lane and block
-    constexpr SkinnyShape kShape = skinny_shape(KIND, MT, NB);
-    constexpr int G = kShape.g, RG = kShape.rg;
-    constexpr int SPR = RG / 16;                            // 16-byte slots of a B row
-    constexpr int RPI = 64 / SPR;                           // B rows per load instruction
-    constexpr int NDMA = BN / RPI;                          // load instructions per group slot
-    constexpr int SLOT = BN * RG;                           // bytes of one group slot
+    constexpr SkinnyShape kShape = skinny_shape(KIND, MT, NB, AR);
+    constexpr int G = kShape.g, RG = kShape.rg, RGA = kShape.rga;
+    constexpr int SPR = RG / 16, SPRA = RGA / 16;           // 16-byte slots of a B / A row
+    constexpr int RPI = 64 / SPR, RPIA = 64 / SPRA;         // rows per load instruction
+    constexpr int NDMA = BN / RPI, NDMAA = AR / RPIA;       // load instructions per group slot
+    static_assert(AR % RPIA == 0 && AR <= BM, "staged A rows");
+    constexpr int SLOTB = BN * RG;                          // B part of a group slot
+    constexpr int SLOT = SLOTB + AR * RGA;                  // bytes of one group slot
     constexpr int NBLK = NB * MT;                           // 32x32 output blocks
     constexpr int kLoads = kShape.loads;
-    static_assert(kLoads == NDMA + MT * G * PA + (kBf16 ? 0 : G * (NB + MT)), "loads per group");
+    static_assert(kLoads == NDMA + NDMAA + (kBf16 ? 0 : G * (NB + MT)), "loads per group");
     static_assert(D >= 2 && (D - 1) * kLoads <= 63, "vmcnt range");
     constexpr int RING = NW * D * SLOT, RED = NW * NBLK * 4096;
-    static_assert(RING <= 128 * 1024 && RED <= 128 * 1024, "LDS budget");
+    static_assert(RING <= 160 * 1024 && RED <= 128 * 1024, "LDS budget");
     // the wave rings, reused for the wave reduction after the main loop
     __shared__ __attribute__((aligned(1024))) uint8_t smem[RING > RED ? RING : RED];
     f32x4* const red = reinterpret_cast<f32x4*>(smem);
@@ -139,12 +142,11 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
     // use; the MFMA reads the low byte of the scale register.  (Byte loads would need a
     // zero-extension that the compiler hoists to the top of the loop, which makes it wait for
     // the ring's loads in flight.)
-    uint32_t va[MT], vsa[MT], vsb[NB];
+    uint32_t vsa[MT], vsb[NB];
     const int sc_shift = 8 * ((r & 1) * 2 + q);
 #pragma unroll
     for (int jm = 0; jm < MT; ++jm) {
         const int row = jm * 32 + r;
-        va[jm] = row < rows_a ? (uint32_t)(row * p.lda) + 16 * q : kOOBOffset;
         vsa[jm] = row < rows_a ? (uint32_t)((row & ~1) * 2) : kOOBOffset;
     }
 #pragma unroll
@@ -166,12 +168,19 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
         const int row = i * RPI + lane / SPR;
         vrow[i] = row < rows_b ? (uint32_t)(row * p.ldb + lk[i]) : kOOBOffset;
     }
+    int lka[NDMAA];
+    uint32_t vrowa[NDMAA];
+#pragma unroll
+    for (int i = 0; i < NDMAA; ++i) {
+        const int row = i * RPIA + lane / SPRA;
+        lka[i] = ((lane % SPRA) ^ slot_swizzle<SPRA>(row)) * 16;
+        vrowa[i] = row < rows_a ? (uint32_t)(row * p.lda + lka[i]) : kOOBOffset;
+    }
     uint8_t* const ring = smem + w * (D * SLOT);
     const int kbytes_a = p.kbytes_a, kbytes_b = p.kbytes_b;
     const int sfa_step = (int)p.sfa_ld * 2, sfb_step = (int)p.sfb_ld * 2;
 
     // ------------------------------------------------------------------ register ring
-    i32x4 fa[D][G][MT][PA];
     int sa[D][G][MT], sb[D][G][NB];
     // Group gi of this wave (64-K blocks kb0 + (gw0 + gi) G + j) into ring slot S; a group past
     // the wave's range (or a block past K) loads zeros with no memory traffic.
@@ -190,20 +199,20 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, (lds_void*)(ring + S * SLOT + i * 1024), 16, v,
                                                          __builtin_amdgcn_readfirstlane(kbg * RBB), 0, 0);
             }
+            // A rows likewise, behind the B rows of the slot
+            const int left_a = live && kbg < kb1 ? kbytes_a - kbg * RBA : 0;
+            const int kend_a = (kb1 - kbg) * RBA;
+#pragma unroll
+            for (int i = 0; i < NDMAA; ++i) {
+                const uint32_t v = lka[i] < left_a && lka[i] < kend_a ? vrowa[i] : kOOBOffset;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, (lds_void*)(ring + S * SLOT + SLOTB + i * 1024), 16, v,
+                                                         __builtin_amdgcn_readfirstlane(kbg * RBA), 0, 0);
+            }
         }
         static_for<G>([&](auto j_c) {
             constexpr int j = decltype(j_c)::value;
             const int kb = kbg + j;
             const bool on = live && kb < kb1;
-            const int left_a = on ? kbytes_a - kb * RBA : 0;   // bytes of the row left from this block
-            static_for<PA>([&](auto pc) {
-                constexpr int P = decltype(pc)::value;
-#pragma unroll
-                for (int jm = 0; jm < MT; ++jm) {
-                    const uint32_t v = 32 * P + 16 * q < left_a ? va[jm] + 32 * P : kOOBOffset;
-                    fa[S][j][jm][P] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_a, v, kb * RBA, 0));
-                }
-            });
             if constexpr (!kBf16) {
 #pragma unroll
                 for (int jm = 0; jm < MT; ++jm)
@@ -227,6 +236,15 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
         const int slot = (j * RBB + 32 * P) / 16 + q;
         return *reinterpret_cast<const i32x4*>(ring + S * SLOT + R * RG + ((slot ^ slot_swizzle<SPR>(R)) << 4));
     };
+    // A fragment piece P of block j, tile block jm (rows past AR: zeros)
+    auto a_piece = [&](int S, int j, int jm, int P) -> i32x4 {
+        const int R = jm * 32 + r;
+        const int Rc = R < AR ? R : AR - 1;
+        const int slot = (j * RBA + 32 * P) / 16 + q;
+        const i32x4 v = *reinterpret_cast<const i32x4*>(ring + S * SLOT + SLOTB + Rc * RGA +
+                                                        ((slot ^ slot_swizzle<SPRA>(Rc)) << 4));
+        return R < AR ? v : i32x4{0, 0, 0, 0};
+    };
     auto compute = [&](auto slot_tag) {
         constexpr int S = decltype(slot_tag)::value;
         // this slot's loads are the oldest D - 1 groups back (the ring's LDS writes are not
@@ -240,6 +258,13 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
             for (int jn = 0; jn < NB; ++jn)
 #pragma unroll
                 for (int P = 0; P < PB; ++P) fb[j][jn][P] = b_piece(S, j, jn, P);
+        i32x4 fa[G][MT][PA];
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+#pragma unroll
+            for (int jm = 0; jm < MT; ++jm)
+#pragma unroll
+                for (int P = 0; P < PA; ++P) fa[j][jm][P] = a_piece(S, j, jm, P);
         static_for<G>([&](auto j_c) {
             constexpr int j = decltype(j_c)::value;
 #pragma unroll
@@ -250,13 +275,13 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
 #pragma unroll
                         for (int s = 0; s < 4; ++s)
                             acc[jn][jm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                                __builtin_bit_cast(bf16x8, fb[j][jn][s]), __builtin_bit_cast(bf16x8, fa[S][j][jm][s]),
+                                __builtin_bit_cast(bf16x8, fb[j][jn][s]), __builtin_bit_cast(bf16x8, fa[j][jm][s]),
                                 acc[jn][jm], 0, 0, 0);
                     } else {
-                        const i32x4 b0 = fb[j][jn][0], a0 = fa[S][j][jm][0];
+                        const i32x4 b0 = fb[j][jn][0], a0 = fa[j][jm][0];
                         i32x4 b1 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
                         if constexpr (PB > 1) b1 = fb[j][jn][1];
-                        if constexpr (PA > 1) a1 = fa[S][j][jm][1];
+                        if constexpr (PA > 1) a1 = fa[j][jm][1];
                         const i32x8 bf = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
                         const i32x8 af = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
                         acc[jn][jm] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(

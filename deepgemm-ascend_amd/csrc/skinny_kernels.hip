@@ -10,35 +10,35 @@ template <int I, int KIND>
 KernelFn skinny_epi(int epi) {
     constexpr SkinnyCfg c = kSkinny[I];
     switch (epi) {
-        case kEpiF32: return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, kEpiF32>;
-        case kEpiBf16: return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, kEpiBf16>;
-        case kEpiBf16SR: return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, kEpiBf16SR>;
+        case kEpiF32: return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, c.ar, kEpiF32>;
+        case kEpiBf16: return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, c.ar, kEpiBf16>;
+        case kEpiBf16SR: return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, c.ar, kEpiBf16SR>;
         case kEpiFp8:
-            if constexpr (KIND == kFP8FP8) return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, kEpiFp8>;
+            if constexpr (KIND == kFP8FP8) return &skinny_kernel<KIND, c.mt, c.nb, c.nw, c.d, c.ar, kEpiFp8>;
             else return nullptr;
         default: return nullptr;
     }
 }
 
 template <int KIND, int I = 0>
-KernelFn skinny_find(int mt, int nb, int nw, int d, int epi) {
+KernelFn skinny_find(int mt, int nb, int nw, int d, int ar, int epi) {
     if constexpr (I == kNumSkinny) {
         return nullptr;
     } else {
-        if (mt == kSkinny[I].mt && nb == kSkinny[I].nb && nw == kSkinny[I].nw && d == kSkinny[I].d)
+        if (mt == kSkinny[I].mt && nb == kSkinny[I].nb && nw == kSkinny[I].nw && d == kSkinny[I].d && ar == kSkinny[I].ar)
             return skinny_epi<I, KIND>(epi);
-        return skinny_find<KIND, I + 1>(mt, nb, nw, d, epi);
+        return skinny_find<KIND, I + 1>(mt, nb, nw, d, ar, epi);
     }
 }
 
 }  // namespace
 
-KernelFn lookup_skinny(int kind, int mt, int nb, int nw, int d, int epi) {
+KernelFn lookup_skinny(int kind, int mt, int nb, int nw, int d, int ar, int epi) {
     switch (kind) {
-        case kFP8FP8: return skinny_find<kFP8FP8>(mt, nb, nw, d, epi);
-        case kFP8FP4: return skinny_find<kFP8FP4>(mt, nb, nw, d, epi);
-        case kFP4FP4: return skinny_find<kFP4FP4>(mt, nb, nw, d, epi);
-        case kBF16: return skinny_find<kBF16>(mt, nb, nw, d, epi);
+        case kFP8FP8: return skinny_find<kFP8FP8>(mt, nb, nw, d, ar, epi);
+        case kFP8FP4: return skinny_find<kFP8FP4>(mt, nb, nw, d, ar, epi);
+        case kFP4FP4: return skinny_find<kFP4FP4>(mt, nb, nw, d, ar, epi);
+        case kBF16: return skinny_find<kBF16>(mt, nb, nw, d, ar, epi);
         default: return nullptr;
     }
 }

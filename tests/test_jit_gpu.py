@@ -18,6 +18,8 @@ THRESH = 1e-5
 @pytest.fixture(autouse=True)
 def jit_cache(tmp_path, monkeypatch):
     monkeypatch.setenv('DG_JIT_CACHE_DIR', str(tmp_path / 'jit'))
+    # (the skinny-M kernel that decode shapes take is ahead-of-time only: keep the tile kernel)
+    monkeypatch.setenv('DG_SKINNY', '0')
     yield
     deep_gemm.set_jit(False)
 
@@ -129,7 +131,6 @@ def test_jit_batched_and_split(monkeypatch):
     aot, jit = _both(run)
     assert torch.equal(aot, jit)
     monkeypatch.setenv('DG_SPLIT_K', '3')
-    monkeypatch.setenv('DG_SKINNY', '0')   # (M = 64 would take the skinny kernel, which is not run-time compiled)
     a2, sfa2, a_deq = operand(64, 4096, 'e4m3', (1, 32), g)
     b2, sfb2, b_deq = operand(2112, 4096, 'e4m3', (1, 32), g)
     a2, sfa2, b2, sfb2 = a2.cuda(), sfa2.cuda(), b2.cuda(), sfb2.cuda()

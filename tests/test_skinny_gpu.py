@@ -1,5 +1,5 @@
 """The skinny-M kernel (csrc/skinny_kernel.hpp) on every configuration of its menu, forced through
-the DG_SKINNY tuning override ("mt,nb,nw,d[,split]"), against the CPU oracle (calc_diff < 1e-5):
+the DG_SKINNY tuning override ("mt,nb,nw,d,ar[,split]"), against the CPU oracle (calc_diff < 1e-5):
 ragged N (strips past the row end), K ending inside a 64-K block and inside a wave's group, K
 split across workgroups, every operand kind, fp32 accumulate and bias, batched launches, and
 the bit-exact epilogues (stochastic rounding, FP8 output) against the same launch's fp32 / bf16
@@ -14,13 +14,13 @@ from helpers import gen, operand, calc_diff
 pytestmark = pytest.mark.gpu
 THRESH = 1e-5
 # (config, M values it serves): the kSkinny menu of csrc/gemm_tiles.hpp, plus forced K splits
-CONFIGS = ['1,1,4,2', '1,1,4,3', '1,1,4,4', '1,1,8,2', '1,1,8,3', '1,2,4,2', '2,1,4,2', '2,1,4,3',
-           '2,1,8,2', '4,1,4,2', '4,1,8,2', '1,1,4,3,3', '2,1,4,3,5', '1,2,4,2,2', '1,1,8,2,4']
+CONFIGS = ['1,1,4,2,16', '1,1,4,3,16', '1,1,4,2,32', '1,1,4,3,32', '1,1,8,2,16', '1,2,4,2,16', '2,1,4,2,64',
+           '4,1,4,2,128', '1,1,4,3,32,3', '2,1,4,2,64,5', '1,2,4,2,16,2', '1,1,8,2,16,4']
 
 
 def _ms(cfg):
-    mt = int(cfg.split(',')[0])
-    return sorted({1, 32 * mt - 3, 32 * mt})
+    ar = int(cfg.split(',')[4])
+    return sorted({1, ar - 3, ar})
 
 
 @pytest.fixture
@@ -51,7 +51,7 @@ def test_skinny_kinds(skinny, cfg, kinds):
 @pytest.mark.parametrize('k', [64, 192, 7168])
 def test_skinny_fp8_accumulate_bias(skinny, cfg, k):
     """fp32 D += A . B^T (c aliases d), then bf16 D with a bias row; the 1x128 / 128x128 recipe."""
-    m, n = int(cfg.split(',')[0]) * 32 - 1, 230
+    m, n = int(cfg.split(',')[4]) - 1, 230
     print(f'skinny {cfg} fp8 accumulate/bias m={m} n={n} k={k}', flush=True)
     skinny(cfg)
     g = gen(32)
@@ -86,7 +86,7 @@ def test_skinny_bf16(skinny, cfg):
         assert calc_diff(d.cpu(), og.gemm_nt(a.float(), b.float())) < THRESH
 
 
-@pytest.mark.parametrize('cfg', ['1,1,4,3', '2,1,4,2,2'])
+@pytest.mark.parametrize('cfg', ['1,1,4,3,32', '2,1,4,2,64,2'])
 def test_skinny_bmm(skinny, cfg):
     bs, m, n, k = 3, 17, 192, 640
     print(f'skinny {cfg} bmm bs={bs} m={m} n={n} k={k}', flush=True)
@@ -101,7 +101,7 @@ def test_skinny_bmm(skinny, cfg):
         assert calc_diff(d[i].cpu(), og.gemm_nt(a_deq[i], b_deq[i])) < THRESH
 
 
-@pytest.mark.parametrize('cfg', ['1,1,4,3', '1,2,4,2,2'])
+@pytest.mark.parametrize('cfg', ['1,1,4,3,16', '1,2,4,2,16,2'])
 def test_skinny_epilogues_bit_exact(skinny, cfg):
     """Stochastic rounding: bit-exact against the hash of the same launch plan's fp32 output;
     FP8 output: bit-exact against quantising its bf16 output per (row, 32 columns)."""
@@ -134,7 +134,8 @@ def test_skinny_epilogues_bit_exact(skinny, cfg):
     assert torch.equal(sfd.cpu(), ref_sfd)
 
 
-@pytest.mark.parametrize('m,n,k', [(1, 2112, 7168), (1, 7168, 2048), (16, 4096, 7168), (5, 24576, 1536)])
+@pytest.mark.parametrize('m,n,k', [(1, 2112, 7168), (1, 7168, 2048), (16, 4096, 7168), (5, 24576, 1536),
+                                   (64, 7168, 2048), (128, 2112, 7168), (100, 4096, 1024)])
 def test_skinny_default_plan_vs_tile_kernel(monkeypatch, m, n, k):
     """Decode shapes on the heuristic's skinny plan agree with the tile kernel (DG_SKINNY=0) and
     with the oracle."""
