@@ -5,11 +5,11 @@
 // of B through the CUs and the tile kernel's LDS ring cannot keep enough bytes in flight.
 //
 // A workgroup owns one 32 NB-column strip of D (all M rows).  Its NW waves split the strip's K
-// range between them in contiguous runs of groups of G 64-K blocks.  Each wave has a private ring of D group slots
-// in LDS that it fills with whole-line global->LDS loads (buffer_load ... lds: one instruction
-// moves 8 rows x 128 bytes) and reads back in the MFMA operand layout (ds_read_b128, the
-// tile kernel's bank swizzle); no other wave touches the ring, so the main loop has no
-// workgroup barrier, only vmcnt waits.  The first AR rows of A travel the same way (rows of
+// range between them in contiguous runs of groups of G 64-K blocks.  Each wave has a private
+// ring of D group slots in LDS that it fills with whole-line global->LDS loads (buffer_load ...
+// lds: one instruction moves 8 rows x 128 bytes) and reads back in the MFMA operand layout
+// (ds_read_b128, the tile kernel's bank swizzle); no other wave touches the ring, so the main
+// loop has no workgroup barrier, only vmcnt waits.  The first AR rows of A travel the same way (rows of
 // the 32 MT-row tile past AR are zeros: AR is sized to the M the configuration serves), the
 // scales go straight to registers.  While group i runs its MFMAs, groups i + 1 .. i + D - 1
 // are in flight.  At the end the waves' partial tiles meet in LDS and are summed in wave
