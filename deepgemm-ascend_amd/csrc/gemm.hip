@@ -163,12 +163,12 @@ SkinnyEnv skinny_env() {
 // 7168x2048 8.0 (15.9), 4096x7168 14.5 (20.2); M = 128: 7168x2048 11.7 (14.2).  Past 16 rows
 // of A, more than two strips per CU (N = 24576) favour the tile kernel (M = 64: 20.1 vs 15.4).
 bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const SkinnyEnv& env, Plan& out) {
-    if (env.mode == 0 || !(a.gemm_type == kNormal || a.gemm_type == kBatched)) return false;
-    const int groups0 = a.gemm_type == kBatched ? a.num_groups : 1;
+    if (env.mode == 0 || !(a.gemm_type == kNormal || a.gemm_type == kBatched || a.gemm_type == kMasked)) return false;
+    const int groups0 = a.gemm_type == kNormal ? 1 : a.num_groups;
     int mt = a.m <= 32 ? 1 : (a.m <= 64 ? 2 : 4), nb = 1, nw = 4, d = 2, ar = a.m <= 16 ? 16 : 32 * mt;
     // long K over at most one strip per CU: eight waves per strip keep more of it in flight
     // (M = 1, 7168x16384: 24.4 vs 26.9 us)
-    if (a.m <= 16 && a.k >= 8192 && (int64_t)ceil_div(a.n, 32) * (a.gemm_type == kBatched ? a.num_groups : 1) <= cus)
+    if (a.m <= 16 && a.k >= 8192 && (int64_t)ceil_div(a.n, 32) * groups0 <= cus)
         nw = 8;
     if (env.mode == 1) {
         mt = env.mt; nb = env.nb; nw = env.nw; d = env.d; ar = env.ar;
@@ -176,8 +176,7 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
         return false;
     }
     if (a.m > ar || lookup_skinny(a.kind, mt, nb, nw, d, ar, kEpiBf16) == nullptr) return false;
-    const int groups = a.gemm_type == kBatched ? a.num_groups : 1;
-    const int64_t strips = (int64_t)ceil_div(a.n, 32 * nb) * groups;
+    const int64_t strips = (int64_t)ceil_div(a.n, 32 * nb) * groups0;
     const int nk64 = std::max(1, ceil_div(a.k, 64));
     int sp = 1;
     if (allow_split && strips <= kMaxSplitTiles) {

@@ -1,8 +1,9 @@
 // Skinny-M GEMM kernel for gfx950 (decode shapes: the whole of M fits one 32 MT-row tile).
 //
 // Same contract as gemm_kernel (D = alpha * A . B^T (+ bias | + D), per-32-K UE8M0 scales, the
-// epilogue variants of epilogue_block), specialised for M <= 32 MT, where the GEMM is a stream
-// of B through the CUs and the tile kernel's LDS ring cannot keep enough bytes in flight.
+// epilogue variants of epilogue_block) for dense, batched and M-grouped masked GEMMs,
+// specialised for M <= 32 MT (masked: max_m), where the GEMM is a stream of B through the CUs
+// and the tile kernel's LDS ring cannot keep enough bytes in flight.
 //
 // A workgroup owns one 32 NB-column strip of D (all M rows).  Its NW waves split the strip's K
 // range between them in contiguous runs of groups of G 64-K blocks.  Each wave has a private
@@ -98,18 +99,23 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
     const int tile_id = t;
     const int nn = p.num_n_blocks;
     int batch = 0;
-    if (p.gemm_type == kBatched) {
+    if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
         batch = t / nn;
         t -= batch * nn;
     }
     const int n0 = t * BN;
-    const int M = p.m, N = p.n;
+    const int N = p.n;
+    // Masked groups hold masked_m[g] <= max_m valid rows (rows past them are neither read nor
+    // written); an empty group's strips return at once (all its splits alike, so the split-K
+    // arrival counts stay consistent).
+    const int M = __builtin_amdgcn_readfirstlane(p.gemm_type == kMasked ? min(p.m, p.layout[batch]) : p.m);
+    if (M <= 0) return;
     const uint8_t* a_base = p.a;
     const uint8_t* b_base = p.b + (int64_t)n0 * p.ldb;
     const uint16_t* sfa = p.sfa;
     const uint16_t* sfb = p.sfb;
     uint8_t* d_base = p.d;
-    if (p.gemm_type == kBatched) {
+    if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
         a_base += (int64_t)batch * p.bsa;
         b_base += (int64_t)batch * p.bsb;
         d_base += (int64_t)batch * p.bsd * p.out_esize;

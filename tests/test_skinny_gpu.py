@@ -152,3 +152,31 @@ def test_skinny_default_plan_vs_tile_kernel(monkeypatch, m, n, k):
     torch.cuda.synchronize()
     assert calc_diff(d.cpu(), og.gemm_nt(a_deq, b_deq)) < THRESH
     assert calc_diff(d.cpu(), d0.cpu()) < 1e-6
+
+
+@pytest.mark.parametrize('cfg', [None, '1,1,4,2,16', '1,1,4,3,32', '2,1,4,2,64'])
+@pytest.mark.parametrize('max_m,n,k', [(16, 384, 1024), (16, 4096, 640), (48, 300, 1040)])
+def test_skinny_masked(monkeypatch, cfg, max_m, n, k):
+    """M-grouped masked decode (the heuristic's plan for max_m <= 16, and forced configurations):
+    valid rows match the oracle, rows past masked_m keep their previous contents, empty groups
+    write nothing."""
+    if cfg is not None:
+        if max_m > int(cfg.split(',')[4]):
+            pytest.skip('configuration holds fewer rows than max_m')
+        monkeypatch.setenv('DG_SKINNY', cfg)
+    print(f'skinny masked {cfg} max_m={max_m} n={n} k={k}', flush=True)
+    groups = 6
+    g = gen(37)
+    a, sfa, a_deq = operand(max_m, k, 'e4m3', (1, 32), g, batch=groups)
+    b, sfb, b_deq = operand(n, k, 'e4m3', (1, 32), g, batch=groups)
+    masked = torch.tensor([max_m, 0, 1, max_m // 2, 3, max_m - 1], dtype=torch.int32)
+    sentinel = torch.full((groups, max_m, n), 7.0).bfloat16()
+    d = sentinel.clone().cuda()
+    deep_gemm.m_grouped_fp8_gemm_nt_masked((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d, masked.cuda(), max_m)
+    torch.cuda.synchronize()
+    out = d.cpu()
+    for i in range(groups):
+        mg = int(masked[i])
+        if mg:
+            assert calc_diff(out[i, :mg], og.gemm_nt(a_deq[i, :mg], b_deq[i])) < THRESH, i
+        assert torch.equal(out[i, mg:], sentinel[i, mg:]), i
