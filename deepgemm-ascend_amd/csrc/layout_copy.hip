@@ -2,10 +2,11 @@
 //
 // The GEMM kernels stream K-major operand rows; an operand the caller holds MN-major (the `tn`
 // / `nn` / `tt` layouts, the K-grouped wgrad operands [Ktot, M], einsum views whose contraction
-// axis is not the innermost) is transposed once on the device.  One workgroup moves a 64 (K) x
-// 64 (MN) element tile: coalesced 16-byte global loads along MN into a padded LDS tile, then
-// 16-byte global stores along K.  Columns K .. k_padded-1 of the output are written as zeros
-// so the result is directly a 16-byte-aligned K-major operand.
+// axis is not the innermost) is transposed once on the device.  One workgroup moves a tile of
+// 128 / E K-indices x 128 bytes of MN (16 KB for e4m3, 8 KB for bf16) through LDS: every
+// thread keeps its loads of the tile in flight at once, and both the loads (rows of MN) and
+// the stores (rows of K) move whole 128-byte lines per group of 8 threads.  Columns K .. k_padded-1 of the output are written as zeros so the
+// result is directly a 16-byte-aligned K-major operand.
 #include "dg_common.hpp"
 #include "../../include/deep_gemm_amd.h"
 
@@ -20,62 +21,68 @@ struct TransposeParams {
 
 template <int E>   // element bytes: 1 (e4m3 / int8) or 2 (bf16)
 __global__ __launch_bounds__(256) void transpose_to_k_major_kernel(const TransposeParams p) {
-    constexpr int T = 64;                 // tile edge in elements
-    constexpr int ROWB = T * E;           // bytes of one tile row
-    constexpr int PAD = 4;                // LDS row padding (bytes) against bank conflicts
+    constexpr int ROWB = 128;             // bytes of a tile row (MN) and of an output segment (K)
+    constexpr int TM = ROWB / E;          // MN elements of a tile
+    constexpr int TK = ROWB / E;          // K elements of a tile
     constexpr int VEC = 16 / E;           // elements per 16-byte access
-    constexpr int TPR = T / VEC;          // threads per tile row
-    constexpr int RPP = 256 / TPR;        // rows per pass
-    __shared__ __align__(16) uint8_t tile[T][ROWB + PAD];
+    constexpr int PASS = 256 / 8;         // rows per pass (8 threads per 128-byte row)
+    constexpr int NLOAD = TK / PASS;      // loads per thread
+    constexpr int NSTORE = TM / PASS;     // stores per thread
+    // (row padding: the column gathers of the store phase then hit at most two rows per bank)
+    constexpr int PAD = 4;
+    __shared__ __align__(16) uint8_t tile[TK][ROWB + PAD];
 
     const int tid = threadIdx.x;
-    const int k0 = blockIdx.x * T, mn0 = blockIdx.y * T, b = blockIdx.z;
+    const int k0 = blockIdx.x * TK, mn0 = blockIdx.y * TM, b = blockIdx.z;
     const uint8_t* src = p.src + ((int64_t)b * p.src_bs) * E;
     uint8_t* dst = p.dst + ((int64_t)b * p.dst_bs) * E;
+    const int c = (tid % 8) * VEC;        // this thread's 16 bytes of a 128-byte row
 
-    // load: tile row = one K index, 64 MN elements
-    const int c = (tid % TPR) * VEC;
+    // load: tile row = K index k0 + r, its 128 bytes of MN; all loads in flight at once
     const bool vec_ok = (p.src_ld % VEC) == 0 && (reinterpret_cast<uintptr_t>(src) % 16) == 0;
+    i32x4 w[NLOAD];
 #pragma unroll
-    for (int r0 = 0; r0 < T; r0 += RPP) {
-        const int r = r0 + tid / TPR;
-        const int k = k0 + r, mn = mn0 + c;
-        uint32_t w[4] = {0, 0, 0, 0};
+    for (int i = 0; i < NLOAD; ++i) {
+        const int k = k0 + i * PASS + tid / 8, mn = mn0 + c;
+        w[i] = i32x4{0, 0, 0, 0};
         if (k < p.k) {
             const uint8_t* s = src + ((int64_t)k * p.src_ld + mn) * E;
             if (vec_ok && mn + VEC <= p.mn) {
-                const i32x4 v = *reinterpret_cast<const i32x4*>(s);
-                w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+                w[i] = *reinterpret_cast<const i32x4*>(s);
             } else {
-                uint8_t* wb = reinterpret_cast<uint8_t*>(w);
-                for (int i = 0; i < VEC; ++i)
-                    if (mn + i < p.mn)
-                        for (int e = 0; e < E; ++e) wb[i * E + e] = s[i * E + e];
+                uint8_t* wb = reinterpret_cast<uint8_t*>(&w[i]);
+                for (int j = 0; j < VEC; ++j)
+                    if (mn + j < p.mn)
+                        for (int e = 0; e < E; ++e) wb[j * E + e] = s[j * E + e];
             }
         }
-        uint32_t* t = reinterpret_cast<uint32_t*>(&tile[r][c * E]);
-        t[0] = w[0]; t[1] = w[1]; t[2] = w[2]; t[3] = w[3];
+    }
+#pragma unroll
+    for (int i = 0; i < NLOAD; ++i) {
+        uint32_t* t = reinterpret_cast<uint32_t*>(&tile[i * PASS + tid / 8][c * E]);
+        t[0] = w[i][0]; t[1] = w[i][1]; t[2] = w[i][2]; t[3] = w[i][3];
     }
     __syncthreads();
 
-    // store: output row = one MN index, 64 K elements (zeros past K up to k_padded)
+    // store: output row = MN index, 128 bytes of K from 8 threads (whole lines per instruction);
+    // a thread gathers its VEC elements down the tile's column
 #pragma unroll
-    for (int r0 = 0; r0 < T; r0 += RPP) {
-        const int r = r0 + tid / TPR;          // MN within the tile
-        const int mn = mn0 + r, k = k0 + c;    // first K of this thread's 16 bytes
+    for (int i = 0; i < NSTORE; ++i) {
+        const int r = i * PASS + tid / 8;     // MN within the tile
+        const int mn = mn0 + r, k = k0 + c;
         if (mn >= p.mn || k >= p.k_padded) continue;
-        uint32_t w[4];
-        uint8_t* wb = reinterpret_cast<uint8_t*>(w);
+        uint32_t o[4];
+        uint8_t* ob = reinterpret_cast<uint8_t*>(o);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i)
+        for (int j = 0; j < VEC; ++j)
 #pragma unroll
-            for (int e = 0; e < E; ++e) wb[i * E + e] = tile[c + i][r * E + e];
+            for (int e = 0; e < E; ++e) ob[j * E + e] = tile[c + j][r * E + e];
         uint8_t* d = dst + ((int64_t)mn * p.dst_ld + k) * E;
         if (k + VEC <= p.k_padded) {
-            *reinterpret_cast<i32x4*>(d) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+            *reinterpret_cast<i32x4*>(d) = i32x4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
         } else {
-            for (int i = 0; i < VEC && k + i < p.k_padded; ++i)
-                for (int e = 0; e < E; ++e) d[i * E + e] = wb[i * E + e];
+            for (int j = 0; j < VEC && k + j < p.k_padded; ++j)
+                for (int e = 0; e < E; ++e) d[j * E + e] = ob[j * E + e];
         }
     }
 }
@@ -101,7 +108,8 @@ extern "C" int dg_transpose_to_k_major(const void* src, int32_t elem_bytes, int3
     p.dst = reinterpret_cast<uint8_t*>(dst);
     p.src_bs = src_batch_stride; p.src_ld = src_ld; p.dst_bs = dst_batch_stride; p.dst_ld = dst_ld;
     p.k = k; p.mn = mn; p.k_padded = k_padded;
-    const dim3 grid((unsigned)ceil_div(k_padded, 64), (unsigned)ceil_div(mn, 64), (unsigned)batches);
+    const int tile = 128 / elem_bytes;   // K and MN elements of a workgroup's tile
+    const dim3 grid((unsigned)ceil_div(k_padded, tile), (unsigned)ceil_div(mn, tile), (unsigned)batches);
     if (grid.x > 0x7fffffffu || grid.y > 65535u || grid.z > 65535u)
         return dg_set_error("dg_transpose_to_k_major: too many tiles");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
