@@ -180,3 +180,21 @@ def test_skinny_masked(monkeypatch, cfg, max_m, n, k):
         if mg:
             assert calc_diff(out[i, :mg], og.gemm_nt(a_deq[i, :mg], b_deq[i])) < THRESH, i
         assert torch.equal(out[i, mg:], sentinel[i, mg:]), i
+
+
+@pytest.mark.parametrize('cfg', ['1,1,4,2,16', '2,1,4,2,64', '4,1,4,2,128', '1,1,4,3,32,3'])
+@pytest.mark.parametrize('m,n,k', [(3, 257, 320), (33, 99, 1088), (127, 501, 64)])
+def test_skinny_odd_shapes(skinny, cfg, m, n, k):
+    """Odd M and N: the packed scales are loaded as row-pair dwords, so the last row's pair partner
+    lies past the operand (inside the even SF leading dimension) and must not leak in."""
+    if m > int(cfg.split(',')[4]):
+        pytest.skip('configuration holds fewer rows than M')
+    print(f'skinny {cfg} odd m={m} n={n} k={k}', flush=True)
+    skinny(cfg)
+    g = gen(38)
+    a, sfa, a_deq = operand(m, k, 'e4m3', (1, 32), g, 'randn')
+    b, sfb, b_deq = operand(n, k, 'e4m3', (1, 32), g, 'randn')
+    d = torch.empty(m, n, dtype=torch.float32, device='cuda')
+    deep_gemm.fp8_gemm_nt((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d)
+    torch.cuda.synchronize()
+    assert calc_diff(d.cpu(), og.gemm_nt(a_deq, b_deq, torch.float32)) < THRESH
