@@ -24,13 +24,14 @@ struct TileCfg {
     int stage_cycles;   // measured cycles per 64 K with every CU busy (fp8, MI355X)
 };
 
-// Measured on MI355X (fp8, cold L2): 4096x7168x2048 256x224 70 us, 256x256 72 us; M-grouped contiguous (32
+// Measured on MI355X (fp8, cold L2): 4096x7168x2048 256x224 70 us, 256x256 72 us; 4096x2112x7168 256x160
+// (224 tiles, one round at 88% of the CUs) 84.8 us, 256x224 (160 tiles) 91.9 us; M-grouped contiguous (32
 // experts, ~257 rows each, alignment 128) N=4096 K=7168: 128x256 as 8 waves / one workgroup per CU 572 us, as
 // 4 waves / two workgroups per CU 509 us; skinny M=128, N=7168, K=16384: 128x128 split 4 57 us.
 constexpr TileCfg kTiles[] = {
     {256, 256, 4, 8, 4, 2, 2, 1, 1380}, {256, 224, 4, 8, 4, 2, 2, 1, 1250}, {256, 128, 4, 8, 8, 4, 1, 1, 937},
     {128, 256, 2, 4, 4, 3, 1, 2, 985},  {128, 128, 2, 4, 4, 4, 1, 1, 1056}, {64, 128, 2, 4, 4, 6, 1, 2, 588},
-    {32, 128, 1, 4, 4, 6, 1, 2, 643},
+    {32, 128, 1, 4, 4, 6, 1, 2, 643},  {256, 160, 4, 8, 4, 2, 2, 1, 950},
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 

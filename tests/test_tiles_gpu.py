@@ -12,7 +12,7 @@ from helpers import gen, operand, calc_diff
 pytestmark = pytest.mark.gpu
 THRESH = 1e-5
 # the menu compiled into libdeep_gemm_amd.so (csrc/gemm_tiles.hpp)
-TILES = ['256x256', '256x224', '256x128', '128x256', '128x128', '64x128', '32x128']
+TILES = ['256x256', '256x224', '256x160', '256x128', '128x256', '128x128', '64x128', '32x128']
 
 
 @pytest.fixture
@@ -69,7 +69,7 @@ def test_tile_bf16(force, tile):
     assert calc_diff(d.cpu(), og.gemm_nt(a.float(), b.float())) < THRESH
 
 
-@pytest.mark.parametrize('tile', ['256x256', '256x224', '256x128', '128x128'])
+@pytest.mark.parametrize('tile', ['256x256', '256x224', '256x160', '256x128', '128x128'])
 def test_tile_m_grouped(force, tile):
     """psum layout, alignment 256: padding rows exact zeros, valid rows per group's B."""
     counts, n, k = [300, 0, 129], 448, 640
