@@ -7,7 +7,7 @@
 // gran_mn times, M-grouped psum padding rows zeroed, invalid fp32 SF flagged.
 //
 // One thread produces one output int16; consecutive threads walk the contiguous MN axis so
-// the stores are fully coalesced (the output is the larger side of the transform).  The MN
+// the stores are fully coalesced (and the loads too for MN-major sources).  The MN
 // axis is stored with an even leading dimension ld = align(MN, 2) (the GEMM kernel fetches
 // SF rows in pairs with 4-byte loads); the padding element of every column is written as 0.
 #include "dg_common.hpp"
@@ -43,43 +43,91 @@ __device__ __forceinline__ bool psum_is_padding(const SfParams& p, int i, int gr
 
 // kKGrouped: the psum layout splits K (csrc/apis/layout.hpp:94-111): SF of the K padding between
 // groups (fp32 per gran_k column, packed int16 per 64-wide column) becomes 0 and is not validated.
-template <bool kFloat, bool kKGrouped>
+// Grid: x walks the MN axis, y the 64-wide K columns (KPB per workgroup), z the batches, so a
+// workgroup's K-column facts (range, K-grouped padding) are uniform and computed once.  With an
+// MN-contiguous fp32 source (one SF row per MN index, 16-byte aligned columns: the K-grouped and
+// MN-major cases) every thread converts 4 consecutive MN with 16-byte loads and an 8-byte store;
+// otherwise one.
+constexpr int kSfKPB = 2;   // 64-wide K columns per workgroup
+
+// Source bits of SF column j (fp32) for output column k64 half h, or 0 past the range / padding.
+template <bool kKGrouped>
+__device__ __forceinline__ bool sf_column_live(const SfParams& p, int k64, int h, int& j) {
+    const int blk = 2 * k64 + h;   // 32-wide K block
+    j = p.gran_k == 128 ? blk >> 2 : blk;
+    return __builtin_amdgcn_readfirstlane(blk < p.k32 && j < p.sf_k && !(kKGrouped && psum_is_padding(p, j, p.gran_k)));
+}
+
+template <bool kFloat, bool kKGrouped, bool kVec>
 __global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
-    const int64_t per_batch = (int64_t)p.k64 * p.ld;
-    const int64_t total = per_batch * p.num_batches;
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-        const int b = (int)(e / per_batch);
-        const int64_t rem = e - (int64_t)b * per_batch;
-        const int k64 = (int)(rem / p.ld);
-        const int mn = (int)(rem - (int64_t)k64 * p.ld);
-        const int i = mn / p.gran_mn;
-        uint16_t out = 0;
-        const bool mn_pad = !kKGrouped && p.psum != nullptr && psum_is_padding(p, i, p.gran_mn);
-        if (mn < p.mn && i < p.sf_mn && !mn_pad) {
-            const int64_t row_off = (int64_t)b * p.stride_b + (int64_t)i * p.stride_mn;
-            if constexpr (kFloat) {
-                const uint32_t* s = reinterpret_cast<const uint32_t*>(p.src);
-                uint32_t bytes[2] = {0, 0};
+    constexpr int V = kVec ? 4 : 1;
+    const int mn0 = (blockIdx.x * 256 + threadIdx.x) * V;
+    const int b = blockIdx.z;
+    if (mn0 >= p.ld) return;
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int blk = 2 * k64 + h;                       // 32-wide K block
-                    if (blk < p.k32) {
-                        const int j = p.gran_k == 128 ? blk >> 2 : blk;
-                        if (j < p.sf_k && !(kKGrouped && psum_is_padding(p, j, p.gran_k))) {
-                            const uint32_t bits = s[row_off + (int64_t)j * p.stride_k];
-                            if ((bits & 0x807fffffu) != 0 && p.err != nullptr) *p.err = 1;
-                            bytes[h] = (bits >> 23) & 0xffu;
-                        }
-                    }
+    for (int kk = 0; kk < kSfKPB; ++kk) {
+        const int k64 = blockIdx.y * kSfKPB + kk;
+        if (k64 >= p.k64) break;
+        uint16_t out[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) out[v] = 0;
+        if constexpr (kFloat && kVec) {
+            // (gran_mn == 1, stride_mn == 1, no psum on MN: row i = mn)
+            const uint32_t* s = reinterpret_cast<const uint32_t*>(p.src) + (int64_t)b * p.stride_b;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                int j;
+                if (!sf_column_live<kKGrouped>(p, k64, h, j)) continue;
+                const uint32_t* col = s + (int64_t)j * p.stride_k;
+                uint32_t bits[4] = {0, 0, 0, 0};
+                if (mn0 + 4 <= p.mn) {
+                    const i32x4 w = *reinterpret_cast<const i32x4*>(col + mn0);
+                    bits[0] = w[0]; bits[1] = w[1]; bits[2] = w[2]; bits[3] = w[3];
+                } else {
+                    for (int v = 0; v < 4; ++v)
+                        if (mn0 + v < p.mn) bits[v] = col[mn0 + v];
                 }
-                out = (uint16_t)(bytes[0] | (bytes[1] << 8));
-            } else {
-                const uint16_t* s = reinterpret_cast<const uint16_t*>(p.src);
-                if (k64 < p.sf_k && !(kKGrouped && psum_is_padding(p, k64, 64)))
-                    out = s[row_off + (int64_t)k64 * p.stride_k];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    if ((bits[v] & 0x807fffffu) != 0 && mn0 + v < p.mn && p.err != nullptr) *p.err = 1;
+                    out[v] |= (uint16_t)(((bits[v] >> 23) & 0xffu) << (8 * h));
+                }
+            }
+        } else {
+            const int mn = mn0;
+            const int i = mn / p.gran_mn;
+            const bool mn_pad = !kKGrouped && p.psum != nullptr && psum_is_padding(p, i, p.gran_mn);
+            if (mn < p.mn && i < p.sf_mn && !mn_pad) {
+                const int64_t row_off = (int64_t)b * p.stride_b + (int64_t)i * p.stride_mn;
+                if constexpr (kFloat) {
+                    const uint32_t* s = reinterpret_cast<const uint32_t*>(p.src);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        int j;
+                        if (!sf_column_live<kKGrouped>(p, k64, h, j)) continue;
+                        const uint32_t bits = s[row_off + (int64_t)j * p.stride_k];
+                        if ((bits & 0x807fffffu) != 0 && p.err != nullptr) *p.err = 1;
+                        out[0] |= (uint16_t)(((bits >> 23) & 0xffu) << (8 * h));
+                    }
+                } else {
+                    const uint16_t* s = reinterpret_cast<const uint16_t*>(p.src);
+                    const bool live =
+                        __builtin_amdgcn_readfirstlane(k64 < p.sf_k && !(kKGrouped && psum_is_padding(p, k64, 64)));
+                    if (live) out[0] = s[row_off + (int64_t)k64 * p.stride_k];
+                }
             }
         }
-        p.dst[(int64_t)b * p.dst_stride_b + (int64_t)k64 * p.ld + mn] = (int16_t)out;
+        int16_t* d = p.dst + (int64_t)b * p.dst_stride_b + (int64_t)k64 * p.ld + mn0;
+        if constexpr (kVec) {
+            if (mn0 + 4 <= p.ld) {
+                *reinterpret_cast<i32x2*>(d) = i32x2{(int)((uint32_t)out[0] | ((uint32_t)out[1] << 16)),
+                                                     (int)((uint32_t)out[2] | ((uint32_t)out[3] << 16))};
+            } else {
+                for (int v = 0; v < 4 && mn0 + v < p.ld; ++v) d[v] = (int16_t)out[v];
+            }
+        } else {
+            d[0] = (int16_t)out[0];
+        }
     }
 }
 
@@ -121,21 +169,31 @@ static int transform_sf_impl(bool k_grouped, const void* src, int32_t src_kind, 
     p.k64 = ceil_div(k, 64); p.k32 = ceil_div(k, 32); p.gran_mn = gran_mn; p.gran_k = gran_k;
     p.psum = psum; p.num_groups = num_groups; p.alignment = alignment;
     p.dst = dst; p.dst_stride_b = dst_stride_b; p.err = err_flag;
-    const int64_t total = (int64_t)p.k64 * p.ld * num_batches;
-    if (total == 0) return DG_OK;
-    int64_t blocks = ceil_div64(total, 256);
-    if (blocks > 8192) blocks = 8192;
+    if ((int64_t)p.k64 * p.ld * num_batches == 0) return DG_OK;
+    if (ceil_div(p.k64, kSfKPB) > 65535 || num_batches > 65535)
+        return dg_set_error("dg_transform_sf: K or batch count too large");
+    // vector path: fp32 rows one per MN index, MN contiguous, 16-byte aligned columns and batches,
+    // no MN padding search, and output rows of a multiple of 4 elements (8-byte stores)
+    const bool vec = src_kind == DG_SF_F32 && gran_mn == 1 && stride_mn == 1 && (k_grouped || psum == nullptr) &&
+                     (reinterpret_cast<uintptr_t>(src) % 16) == 0 && stride_k % 4 == 0 &&
+                     (num_batches == 1 || stride_b % 4 == 0) && p.ld % 4 == 0 &&
+                     (reinterpret_cast<uintptr_t>(dst) % 8) == 0 && (num_batches == 1 || dst_stride_b % 4 == 0);
+    const dim3 blocks((unsigned)ceil_div(p.ld, 256 * (vec ? 4 : 1)), (unsigned)ceil_div(p.k64, kSfKPB),
+                      (unsigned)num_batches);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (k_grouped) {
+    if (vec) {
+        if (k_grouped) hipLaunchKernelGGL((transform_sf_kernel<true, true, true>), blocks, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((transform_sf_kernel<true, false, true>), blocks, dim3(256), 0, st, p);
+    } else if (k_grouped) {
         if (src_kind == DG_SF_F32)
-            hipLaunchKernelGGL((transform_sf_kernel<true, true>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((transform_sf_kernel<true, true, false>), blocks, dim3(256), 0, st, p);
         else
-            hipLaunchKernelGGL((transform_sf_kernel<false, true>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((transform_sf_kernel<false, true, false>), blocks, dim3(256), 0, st, p);
     } else {
         if (src_kind == DG_SF_F32)
-            hipLaunchKernelGGL((transform_sf_kernel<true, false>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((transform_sf_kernel<true, false, false>), blocks, dim3(256), 0, st, p);
         else
-            hipLaunchKernelGGL((transform_sf_kernel<false, false>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((transform_sf_kernel<false, false, false>), blocks, dim3(256), 0, st, p);
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

@@ -102,6 +102,19 @@ def test_transform_sf_invalid_flag(monkeypatch):
         deep_gemm.transform_sf_into_required_layout(sf, 8, 128, (1, 1, 32), is_sfa=True)
 
 
+def test_transform_sf_invalid_flag_mn_major(monkeypatch):
+    """The same check on the vectorised path (MN-major fp32 SF, 4 MN per thread): one bad value."""
+    monkeypatch.setenv('DG_CHECK_SF', '1')
+    sf = torch.ones(4, 64, device='cuda').t()            # [MN=64, K/32=4] view, MN contiguous
+    sf_bad = sf.clone().t().contiguous().t()
+    sf_bad[37, 2] = -2.0
+    out = deep_gemm.transform_sf_into_required_layout(sf, 64, 128, (1, 1, 32), is_sfa=True)
+    torch.cuda.synchronize()
+    assert out.shape[0] == 64
+    with pytest.raises(RuntimeError, match='Invalid float32 SF'):
+        deep_gemm.transform_sf_into_required_layout(sf_bad, 64, 128, (1, 1, 32), is_sfa=True)
+
+
 @pytest.mark.parametrize('dtype', [torch.float8_e4m3fn, torch.bfloat16])
 @pytest.mark.parametrize('batch,k,mn', [(0, 64, 64), (0, 2048, 7168), (0, 100, 37), (3, 130, 257), (2, 1, 5), (0, 7, 300)])
 def test_transpose_to_k_major(dtype, batch, k, mn):
