@@ -131,6 +131,62 @@ __global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
     }
 }
 
+// K-major fp32 sources (one contiguous row of SF per MN index, the reference's usual [MN, K / gran]
+// layout): a thread owns one MN index and kSfKPBK 64-wide K columns, reading the row's span of
+// them with 16-byte loads (the whole 128-byte line for gran_k = 32) instead of one scattered
+// float per output; the stores stay coalesced along MN.
+constexpr int kSfKPBK = 16;
+
+template <bool kKGrouped>
+__global__ __launch_bounds__(256) void transform_sf_kmajor_kernel(const SfParams p) {
+    constexpr int F = 2 * kSfKPBK;             // floats of a block's K span at gran_k = 32
+    const int mn = blockIdx.x * 256 + threadIdx.x;
+    const int b = blockIdx.z, kbase = blockIdx.y * kSfKPBK;
+    if (mn >= p.ld) return;
+    const int i = mn / p.gran_mn;
+    const bool mn_pad = !kKGrouped && p.psum != nullptr && psum_is_padding(p, i, p.gran_mn);
+    const bool row_ok = mn < p.mn && i < p.sf_mn && !mn_pad;
+    const int per = p.gran_k == 128 ? 4 : 1;   // 32-wide K blocks per source float
+    const int j0 = 2 * kbase / per;            // first source float of the span
+    const int nf = F / per;                    // floats of the span (32 or 8)
+    uint32_t f[F];
+#pragma unroll
+    for (int t = 0; t < F; ++t) f[t] = 0;
+    if (row_ok) {
+        const uint32_t* row = reinterpret_cast<const uint32_t*>(p.src) + (int64_t)b * p.stride_b + (int64_t)i * p.stride_mn;
+        if (j0 + nf <= p.sf_k) {
+            // (16-byte aligned: the host checks the row stride, j0 is a multiple of 8)
+#pragma unroll
+            for (int t = 0; t < F / 4; ++t)
+                if (t * 4 < nf) {
+                    const i32x4 w = *reinterpret_cast<const i32x4*>(row + j0 + 4 * t);
+                    f[4 * t] = w[0]; f[4 * t + 1] = w[1]; f[4 * t + 2] = w[2]; f[4 * t + 3] = w[3];
+                }
+        } else {
+            for (int t = 0; t < nf; ++t)
+                if (j0 + t < p.sf_k) f[t] = row[j0 + t];
+        }
+    }
+#pragma unroll
+    for (int kk = 0; kk < kSfKPBK; ++kk) {
+        const int k64 = kbase + kk;
+        if (k64 >= p.k64) break;
+        uint16_t out = 0;
+        if (row_ok) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                int j;
+                if (!sf_column_live<kKGrouped>(p, k64, h, j)) continue;
+                // (constant register indices: j - j0 is 2 kk + h, or its quarter at gran_k = 128)
+                const uint32_t bits = per == 1 ? f[2 * kk + h] : f[(2 * kk + h) >> 2];
+                if ((bits & 0x807fffffu) != 0 && p.err != nullptr) *p.err = 1;
+                out |= (uint16_t)(((bits >> 23) & 0xffu) << (8 * h));
+            }
+        }
+        p.dst[(int64_t)b * p.dst_stride_b + (int64_t)k64 * p.ld + mn] = (int16_t)out;
+    }
+}
+
 }  // namespace dg
 
 extern "C" __attribute__((visibility("hidden"))) int dg_set_error(const char* msg);
@@ -170,7 +226,7 @@ static int transform_sf_impl(bool k_grouped, const void* src, int32_t src_kind, 
     p.psum = psum; p.num_groups = num_groups; p.alignment = alignment;
     p.dst = dst; p.dst_stride_b = dst_stride_b; p.err = err_flag;
     if ((int64_t)p.k64 * p.ld * num_batches == 0) return DG_OK;
-    if (ceil_div(p.k64, kSfKPB) > 65535 || num_batches > 65535)
+    if (ceil_div(p.k64, 2) > 65535 || num_batches > 65535)
         return dg_set_error("dg_transform_sf: K or batch count too large");
     // vector path: fp32 rows one per MN index, MN contiguous, 16-byte aligned columns and batches,
     // no MN padding search, and output rows of a multiple of 4 elements (8-byte stores)
@@ -178,10 +234,16 @@ static int transform_sf_impl(bool k_grouped, const void* src, int32_t src_kind, 
                      (reinterpret_cast<uintptr_t>(src) % 16) == 0 && stride_k % 4 == 0 &&
                      (num_batches == 1 || stride_b % 4 == 0) && p.ld % 4 == 0 &&
                      (reinterpret_cast<uintptr_t>(dst) % 8) == 0 && (num_batches == 1 || dst_stride_b % 4 == 0);
-    const dim3 blocks((unsigned)ceil_div(p.ld, 256 * (vec ? 4 : 1)), (unsigned)ceil_div(p.k64, kSfKPB),
+    // K-major path: fp32 rows contiguous along K, 16-byte aligned rows
+    const bool kmajor = !vec && src_kind == DG_SF_F32 && stride_k == 1 && (reinterpret_cast<uintptr_t>(src) % 16) == 0 &&
+                        stride_mn % 4 == 0 && (num_batches == 1 || stride_b % 4 == 0);
+    const dim3 blocks((unsigned)ceil_div(p.ld, 256 * (vec ? 4 : 1)), (unsigned)ceil_div(p.k64, kmajor ? kSfKPBK : kSfKPB),
                       (unsigned)num_batches);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (vec) {
+    if (kmajor) {
+        if (k_grouped) hipLaunchKernelGGL((transform_sf_kmajor_kernel<true>), blocks, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((transform_sf_kmajor_kernel<false>), blocks, dim3(256), 0, st, p);
+    } else if (vec) {
         if (k_grouped) hipLaunchKernelGGL((transform_sf_kernel<true, true, true>), blocks, dim3(256), 0, st, p);
         else hipLaunchKernelGGL((transform_sf_kernel<true, false, true>), blocks, dim3(256), 0, st, p);
     } else if (k_grouped) {
