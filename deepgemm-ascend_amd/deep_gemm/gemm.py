@@ -107,7 +107,13 @@ def _transpose_to_k_major(t: torch.Tensor, k: int) -> torch.Tensor:
     return out
 
 
+_raw_stream = getattr(torch._C, '_cuda_getCurrentRawStream', None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    # (torch's raw current-stream handle skips building a Stream object on every launch)
+    if _raw_stream is not None and t.device.index is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

@@ -38,23 +38,24 @@ def _align(x: int, a: int) -> int:
 def check_sf_layout(sf: torch.Tensor, mn: int, k: int, gran_mn: int, gran_k: int,
                     num_groups: Optional[int]) -> bool:
     """Validate ``sf``; True when it is already in the required layout (csrc/apis/layout.hpp:37-65)."""
-    _assert(sf.dtype in (torch.float32, torch.int16), 'SF must be float32 or int16 (packed ue8m0x2)')
-    _assert(sf.dim() == (1 if num_groups is not None else 0) + 2, 'SF rank mismatch')
-    _assert(sf.stride(-1) == 1 or sf.stride(-2) == 1,
-            'SF input must be contiguous in either the last or second-to-last dimension')
+    dt = sf.dtype
+    _assert(dt in (torch.float32, torch.int16), 'SF must be float32 or int16 (packed ue8m0x2)')
+    st, sz = sf.stride(), sf.shape
+    _assert(len(sz) == (1 if num_groups is not None else 0) + 2, 'SF rank mismatch')
+    _assert(st[-1] == 1 or st[-2] == 1, 'SF input must be contiguous in either the last or second-to-last dimension')
     if num_groups is not None:
-        _assert(sf.size(-3) == num_groups, 'SF group count mismatch')
-    if sf.dtype == torch.float32:
+        _assert(sz[-3] == num_groups, 'SF group count mismatch')
+    if dt == torch.float32:
         _assert(gran_k in (32, 128), 'gran_k must be 32 (or 128 for float32 SF)')
         div_k = gran_k
     else:
         _assert(gran_k == 32, 'gran_k must be 32')
         div_k = 64
-    _assert(sf.size(-2) == _ceil_div(mn, gran_mn), f'SF MN extent {sf.size(-2)} != ceil({mn}/{gran_mn})')
-    _assert(sf.size(-1) == _ceil_div(k, div_k), f'SF K extent {sf.size(-1)} != ceil({k}/{div_k})')
-    if sf.dtype == torch.int16 and gran_mn == 1 and sf.stride(-2) == 1 and sf.stride(-1) == _align(sf.size(-2), 2):
+    _assert(sz[-2] == _ceil_div(mn, gran_mn), f'SF MN extent {sz[-2]} != ceil({mn}/{gran_mn})')
+    _assert(sz[-1] == _ceil_div(k, div_k), f'SF K extent {sz[-1]} != ceil({k}/{div_k})')
+    if dt == torch.int16 and gran_mn == 1 and st[-2] == 1 and st[-1] == _align(sz[-2], 2):
         if num_groups is not None:
-            return sf.stride(-3) == sf.stride(-1) * sf.size(-1)
+            return st[-3] == st[-1] * sz[-1]
         return True
     return False
 
