@@ -40,6 +40,10 @@ constexpr uint32_t kBufferRsrcWord3 = 0x00020000u;
 // voffset that is always beyond num_records: such a lane reads zeros.
 // Buffer-instruction cache-policy bit sc0: a load that misses the CU's L1 (served by the L2).
 constexpr int kCacheSc0 = 1;
+// Buffer-instruction cache-policy bit sc1 (device scope): a store is written through to memory
+// and a load is served coherently for every XCD, so partials exchanged between workgroups on
+// different XCDs (each XCD has its own L2) need no L2 writeback or invalidate.
+constexpr int kCacheSc1 = 16;
 constexpr uint32_t kOOBOffset = 0x80000000u;
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));

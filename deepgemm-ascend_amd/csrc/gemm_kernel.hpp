@@ -825,30 +825,22 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
                     __builtin_amdgcn_raw_buffer_store_b128(
                         __builtin_bit_cast(u32x4, f32x4{acc[jn][jm][4 * g], acc[jn][jm][4 * g + 1], acc[jn][jm][4 * g + 2],
                                                         acc[jn][jm][4 * g + 3]}),
-                        rs_ws, off + 16 * g, 0, 0);
+                        rs_ws, off + 16 * g, 0, kCacheSc1);
             });
         });
         // Publish the partial and count arrivals; only the last workgroup of the tile goes on.
-        // A workgroup on its tile's home XCD (hardware XCC id == b % 8) only waits for its
-        // stores to reach the XCD's L2, which every split on that XCD reads; one elsewhere (a
-        // dispatcher that does not place workgroups round-robin) makes its partial visible
-        // device-wide and marks the counter (+ 1 << 16), and the reducer then also acquires
-        // device-wide.  Either way no L2 is flushed or invalidated on the fast path.
-        const int xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xf;   // HW_REG_XCC_ID[3:0]
-        const bool home = xcc == (int)(blockIdx.x & 7);
-        // Every wave waits until its own partial stores are acknowledged by the L2 (the "memory"
-        // clobber keeps the compiler from sinking them past the wait) before the arrival count.
-        if (home) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        else __threadfence();
+        // The partials are stored and reloaded at device scope (written through to memory, read
+        // coherently on every XCD), so once every wave's stores are acknowledged they are
+        // visible to whichever workgroup reduces, on whichever XCD, and no fence (an L2
+        // writeback or invalidate) is needed.  The "memory" clobber keeps the compiler from
+        // sinking the stores past the wait.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         int* flag = reinterpret_cast<int*>(smem);
         if (tid == 0)
-            *flag = __hip_atomic_fetch_add(p.counters + tile_id, home ? 1 : 1 + (1 << 16), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+            *flag = __hip_atomic_fetch_add(p.counters + tile_id, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
-        const int prev = *flag;
-        if ((prev & 0xffff) != split_k - 1) return;
-        if (!home || (prev >> 16) != 0) __threadfence();
+        if (*flag != split_k - 1) return;
         // Sum the partials in split order, whichever split arrived last, so a launch's result
         // does not depend on workgroup timing.  Small wave tiles keep the loads of partial sp + 1
         // in flight while partial sp is added (two register sets), so the reduction costs about
@@ -863,12 +855,12 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
                 constexpr int jn = decltype(jn_c)::value;
                 static_for<TM>([&](auto jm_c) {
                     constexpr int jm = decltype(jm_c)::value;
-                    // sc0 loads miss this CU's L1 (which may hold stale lines) and read the L2
+                    // device-scope loads: coherent with the device-scope partial stores
                     const uint32_t off = part_off(sp, jn, jm);
 #pragma unroll
                     for (int g = 0; g < 4; ++g)
                         pb[set][jn][jm][g] = __builtin_bit_cast(
-                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_ws, off + 16 * g, 0, kCacheSc0));
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_ws, off + 16 * g, 0, kCacheSc1));
                 });
             });
         };

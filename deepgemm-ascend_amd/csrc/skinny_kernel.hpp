@@ -367,23 +367,19 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
                     __builtin_amdgcn_raw_buffer_store_b128(
                         __builtin_bit_cast(u32x4, f32x4{out[jn][jm][4 * g], out[jn][jm][4 * g + 1], out[jn][jm][4 * g + 2],
                                                         out[jn][jm][4 * g + 3]}),
-                        rs_ws, off + 16 * g, 0, 0);
+                        rs_ws, off + 16 * g, 0, kCacheSc1);
             }
-        // Arrival count, as in gemm_kernel: on the strip's home XCD the stores only need to
-        // reach that XCD's L2; elsewhere they are made visible device-wide and the counter says so.
-        const int xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xf;   // HW_REG_XCC_ID[3:0]
-        const bool home = xcc == (int)(blockIdx.x & 7);
-        if (home) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        else __threadfence();
+        // Arrival count.  The partials were stored at device scope, so once every wave's stores
+        // are acknowledged they are visible on every XCD; no fence (which would write back or
+        // invalidate the whole L2) is needed on either side.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         int* flag = reinterpret_cast<int*>(red);
         if (tid == 0)
-            *flag = __hip_atomic_fetch_add(p.counters + tile_id, home ? 1 : 1 + (1 << 16), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+            *flag = __hip_atomic_fetch_add(p.counters + tile_id, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         const int prev = *flag;
-        if ((prev & 0xffff) != split_k - 1) return;
-        if (!home || (prev >> 16) != 0) __threadfence();
+        if (prev != split_k - 1) return;
 #pragma unroll
         for (int jn = 0; jn < NB; ++jn)
 #pragma unroll
@@ -395,7 +391,7 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const f32x4 v = __builtin_bit_cast(
-                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_ws, off + 16 * g, 0, kCacheSc0));
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_ws, off + 16 * g, 0, kCacheSc1));
 #pragma unroll
                         for (int i = 0; i < 4; ++i) out[jn][jm][4 * g + i] += v[i];
                     }
