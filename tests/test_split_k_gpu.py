@@ -125,3 +125,38 @@ def test_split_k_tiles(split_env, monkeypatch, tile, split):
     deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d)
     torch.cuda.synchronize()
     assert calc_diff(d.cpu(), og.gemm_nt(a_deq, b_deq, torch.float32)) < THRESH
+
+
+def test_split_back_to_back_matches_isolated():
+    """Split-K launches issued back to back on one stream with no sync between them (skinny-M kernel
+    with its K split, and a tile-kernel split): workgroups of one tile may then sit on different
+    XCDs.  Each output equals the same GEMM launched alone, bit for bit, on every repetition."""
+    print('split back to back', flush=True)
+    shapes = [(1, 2112, 7168, None), (16, 4096, 7168, None), (128, 2112, 7168, None), (64, 2112, 4096, '3')]
+    cases = []
+    for i, (m, n, k, split) in enumerate(shapes):
+        a, sfa, _, b, sfb, _ = _case(m, n, k, seed=60 + i)
+        if split is not None:
+            os.environ['DG_SKINNY'], os.environ['DG_SPLIT_K'] = '0', split
+        try:
+            d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
+            deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d)
+            torch.cuda.synchronize()
+        finally:
+            os.environ.pop('DG_SKINNY', None)
+            os.environ.pop('DG_SPLIT_K', None)
+        cases.append((a, sfa, b, sfb, d.clone(), split))
+    outs = [torch.empty_like(c[4]) for c in cases]
+    for rep in range(3):
+        for _ in range(8):
+            for (a, sfa, b, sfb, _, split), d in zip(cases, outs):
+                if split is not None:
+                    os.environ['DG_SKINNY'], os.environ['DG_SPLIT_K'] = '0', split
+                try:
+                    deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d)
+                finally:
+                    os.environ.pop('DG_SKINNY', None)
+                    os.environ.pop('DG_SPLIT_K', None)
+        torch.cuda.synchronize()
+        for i, (c, d) in enumerate(zip(cases, outs)):
+            assert torch.equal(d.view(torch.int16), c[4].view(torch.int16)), (rep, shapes[i])
