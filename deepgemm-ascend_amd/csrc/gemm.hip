@@ -44,12 +44,12 @@ extern "C" int dg_device_num_cus(int32_t device) {
 
 namespace dg {
 
-KernelFn lookup_kernel(int kind, int bm, int bn, int epi) {
+KernelFn lookup_kernel(int kind, int bm, int bn, int epi, bool persistent) {
     switch (kind) {
-        case kFP8FP8: return lookup_kernel_fp8fp8(bm, bn, epi);
-        case kFP8FP4: return lookup_kernel_fp8fp4(bm, bn, epi);
-        case kFP4FP4: return lookup_kernel_fp4fp4(bm, bn, epi);
-        case kBF16: return lookup_kernel_bf16(bm, bn, epi);
+        case kFP8FP8: return lookup_kernel_fp8fp8(bm, bn, epi, persistent);
+        case kFP8FP4: return lookup_kernel_fp8fp4(bm, bn, epi, persistent);
+        case kFP4FP4: return lookup_kernel_fp4fp4(bm, bn, epi, persistent);
+        case kBF16: return lookup_kernel_bf16(bm, bn, epi, persistent);
         default: return nullptr;
     }
 }
@@ -189,6 +189,13 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
     return true;
 }
 
+// Tiles with a persistent kernel (csrc/gemm_persistent.hpp): the 128-K-stage tiles whose
+// persistent body fits the register file (256x256 does not).
+bool tile_persistable(const TileCfg& t) { return t.km == 2 && t.stages == 2 && !(t.bm == 256 && t.bn == 256); }
+
+// CUs the launch may occupy are capped below the device's (set_num_sms).
+bool cus_capped(int cus) { return cus < device_cus(); }
+
 Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     Plan skinny;
     if (skinny_kernel_plan(a, cus, allow_split, skinny_env(), skinny)) return skinny;
@@ -204,9 +211,13 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     const double hbm_bytes = esz * ((double)a.m + a.n) * a.k * groups + 2.0 * a.m * a.n * groups;
     double best = 1e300;
     Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0, 0}, 1, 1, 0, 0, 0};
+    // Under a CU cap the 128-K-stage tiles run persistently (one workgroup per allowed CU), so only
+    // those with a persistent kernel are offered.
+    const bool capped = cus_capped(cus);
     for (int i = 0; i < kNumTiles; ++i) {
         const TileCfg& tc = kTiles[i];
         if (!tile_allowed(a, tc.bm, tc.bn)) continue;
+        if (capped && tc.km == 2 && !tile_persistable(tc)) continue;
         const int ns = ceil_div(k_tile, k_stage_elems(a.kind, tc));
         const int64_t tiles = plan_tiles(a, tc);
         const int max_split = allow_split && tile_splittable(tc) && tiles <= kMaxSplitTiles ? std::min(16, std::max(1, ns / 4)) : 1;
@@ -339,7 +350,8 @@ extern "C" int dg_gemm_workspace_size(const dg_gemm_args* args, int64_t* bytes) 
 
 namespace {
 
-int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only) {
+// Checks, plans and launches one GEMM; with `info` it stops short of the launch and describes it.
+int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_launch_info* info = nullptr) {
     using namespace dg;
     if (args == nullptr) return dg_set_error("dg_gemm: null args");
     const dg_gemm_args& a = *args;
@@ -362,13 +374,16 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only) {
         if (a.ldd % 4 || (reinterpret_cast<uintptr_t>(a.d) & 3) || (a.gemm_type == kBatched && a.batch_stride_d % 4))
             return dg_set_error("dg_gemm: FP8 output rows must be 4-byte aligned");
     }
+    if (info != nullptr) memset(info, 0, sizeof(*info));
     if (a.m == 0 || a.n == 0) return DG_OK;
     const bool bf16 = a.kind == kBF16;
-    if (a.a == nullptr || a.b == nullptr || a.d == nullptr) return dg_set_error("dg_gemm: null operand");
-    if (!bf16 && (a.sfa == nullptr || a.sfb == nullptr)) return dg_set_error("dg_gemm: scale factors required");
+    // (a launch-plan query needs sizes and strides only)
+    const bool plan_only = info != nullptr;
+    if (!plan_only && (a.a == nullptr || a.b == nullptr || a.d == nullptr)) return dg_set_error("dg_gemm: null operand");
+    if (!plan_only && !bf16 && (a.sfa == nullptr || a.sfb == nullptr)) return dg_set_error("dg_gemm: scale factors required");
     const bool grouped = a.gemm_type != kNormal;
-    if ((a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx || a.gemm_type == kMasked ||
-         a.gemm_type == kKGrouped) &&
+    if (!plan_only && (a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx || a.gemm_type == kMasked ||
+                       a.gemm_type == kKGrouped) &&
         a.grouped_layout == nullptr)
         return dg_set_error("dg_gemm: grouped_layout required");
     if (grouped && a.num_groups < 1) return dg_set_error("dg_gemm: num_groups must be >= 1");
@@ -413,10 +428,27 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only) {
     // (the skinny-M kernel is not specialised per problem: the JIT setting leaves it ahead-of-time)
     const bool skinny = plan.skinny_nw > 0;
     const bool jit = a.jit && !skinny;
-    if (skinny && compile_only) return DG_OK;
+    if (skinny && compile_only && info == nullptr) return DG_OK;
+    // Persistent launch (one workgroup per CU walking the tiles, the LDS ring running on across
+    // them): the 128-K-stage tiles of unsplit GEMMs whose operand tensors fit 31-bit offsets.
+    const int groups_all = (a.gemm_type == kBatched || a.gemm_type == kMasked) ? a.num_groups : 1;
+    const int groups_b = a.gemm_type == kNormal ? 1 : a.num_groups;
+    const int64_t nk64 = ceil_div(a.k, 64);
+    const int64_t a_span = (int64_t)(groups_all - 1) * a.batch_stride_a * esz_a + (int64_t)(a.m - 1) * lda_b + kbytes_a;
+    const int64_t b_span = (int64_t)(groups_b - 1) * a.batch_stride_b * esz_b + (int64_t)(a.n - 1) * ldb_b + kbytes_b;
+    const int64_t sfa_span = bf16 ? 0 : ((int64_t)(groups_all - 1) * a.sfa_batch_stride + nk64 * a.sfa_ld) * 2;
+    const int64_t sfb_span = bf16 ? 0 : ((int64_t)(groups_b - 1) * a.sfb_batch_stride + nk64 * a.sfb_ld) * 2;
+    // The persistent kernel runs where the launch must stay within `cus` CUs (set_num_sms below the
+    // device's count) or when DG_PERSISTENT=1 asks for it (tuning); it measured no faster than
+    // one tile per workgroup at full occupancy (the same ring, the epilogue still not overlapped).
+    static const char* persist_env = std::getenv("DG_PERSISTENT");
+    const bool want_persistent = cus_capped(cus) || (persist_env != nullptr && persist_env[0] == '1');
+    const bool persistent = want_persistent && !jit && !skinny && plan.split == 1 && tile_persistable(cfg) &&
+                            a.k > 0 && a.gemm_type != kKGrouped && a_span <= 0x7fffffffLL &&
+                            b_span <= 0x7fffffffLL && sfa_span <= 0x7fffffffLL && sfb_span <= 0x7fffffffLL;
     KernelFn fn = jit ? nullptr
                 : skinny ? lookup_skinny(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_nw, plan.skinny_d, plan.skinny_ar, epi_kind)
-                         : lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind);
+                         : lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind, persistent);
     if (fn == nullptr && !jit) {
         char buf[160];
         snprintf(buf, sizeof(buf), "dg_gemm: no compiled kernel for kind=%d block=%dx%d", a.kind, cfg.bm, cfg.bn);
@@ -453,8 +485,11 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only) {
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
     const int64_t tiles = (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
     if (tiles <= 0) return DG_OK;
-    // split-K grids are padded to whole groups of 8 tiles (one per XCD)
-    const int64_t grid = plan.split > 1 ? align_up64(tiles, 8) * plan.split : tiles;
+    // split-K grids are padded to whole groups of 8 tiles (one per XCD); persistent grids hold
+    // one workgroup per CU (set_num_sms caps them)
+    const int64_t grid = persistent ? std::min<int64_t>(tiles, (int64_t)cus * cfg.occ)
+                       : plan.split > 1 ? align_up64(tiles, 8) * plan.split : tiles;
+    p.a_span = a_span; p.b_span = b_span; p.sfa_span = sfa_span; p.sfb_span = sfb_span;
     if (grid > 0x7fffffffLL) return dg_set_error("dg_gemm: too many tiles");
     p.split_k = plan.split;
     p.split_stages = plan.split_stages;
@@ -463,9 +498,20 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only) {
         p.counters = reinterpret_cast<int*>(a.workspace);
         p.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.workspace) + kCounterBytes);
     }
+    const int threads = skinny ? plan.skinny_nw * 64 : tile_threads(cfg.bm, cfg.bn);
+    if (info != nullptr) {
+        info->block_m = cfg.bm;
+        info->block_n = cfg.bn;
+        info->grid = grid;
+        info->threads = threads;
+        info->tiles = tiles;
+        info->split_k = plan.split;
+        info->persistent = persistent ? 1 : 0;
+        info->skinny = skinny ? 1 : 0;
+        return DG_OK;
+    }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (jit) return jit_run(a, cfg, epi_kind, plan.split, p, grid, st, compile_only);
-    const int threads = skinny ? plan.skinny_nw * 64 : tile_threads(cfg.bm, cfg.bn);
     hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3((unsigned)threads), 0, st, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
@@ -478,6 +524,11 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only) {
 }  // namespace
 
 extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) { return gemm_impl(args, stream, false); }
+
+extern "C" int dg_launch_plan(const dg_gemm_args* args, dg_launch_info* info) {
+    if (args == nullptr || info == nullptr) return dg_set_error("dg_launch_plan: null argument");
+    return gemm_impl(args, nullptr, true, info);
+}
 
 extern "C" int dg_jit_compile(const dg_gemm_args* args) {
     if (args == nullptr) return dg_set_error("dg_jit_compile: null args");

@@ -61,6 +61,9 @@ struct KParams {
     // sfd[(batch * n + col) / 64 * sfd_ld + row], lower byte = the even 32-column block.
     uint8_t* sfd;
     int64_t sfd_ld;
+    // Persistent launches: bytes of each operand / SF tensor over all its batches or groups (every
+    // span below 2^31, so a tile's base fits a buffer instruction's scalar offset).
+    int64_t a_span, b_span, sfa_span, sfb_span;
 };
 
 // Epilogue variants.

@@ -2,5 +2,5 @@
 #include "gemm_tiles.hpp"
 
 namespace dg {
-KernelFn lookup_kernel_bf16(int bm, int bn, int epi) { return lookup_tile<kBF16>(bm, bn, epi); }
+KernelFn lookup_kernel_bf16(int bm, int bn, int epi, bool persistent) { return lookup_tile<kBF16>(bm, bn, epi, persistent); }
 }  // namespace dg

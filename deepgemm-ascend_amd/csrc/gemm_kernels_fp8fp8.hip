@@ -2,5 +2,5 @@
 #include "gemm_tiles.hpp"
 
 namespace dg {
-KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi) { return lookup_tile<kFP8FP8>(bm, bn, epi); }
+KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi, bool persistent) { return lookup_tile<kFP8FP8>(bm, bn, epi, persistent); }
 }  // namespace dg

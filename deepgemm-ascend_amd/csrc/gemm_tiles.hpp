@@ -2,6 +2,7 @@
 #pragma once
 
 #include "gemm_kernel.hpp"
+#include "gemm_persistent.hpp"
 #include "../../include/deep_gemm_amd.h"
 
 namespace dg {
@@ -54,13 +55,33 @@ KernelFn pick_epi(int epi) {
     }
 }
 
+// Persistent kernels exist for the 128-K-stage (km = 2, two-slot ring) tiles.
+template <int I, int KIND>
+KernelFn pick_persistent_epi(int epi) {
+    constexpr TileCfg t = kTiles[I];
+    if constexpr (t.km != 2 || t.stages != 2) {
+        return nullptr;
+    } else {
+        switch (epi) {
+            case kEpiF32: return &gemm_persistent_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.occ, KIND, kEpiF32>;
+            case kEpiBf16: return &gemm_persistent_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.occ, KIND, kEpiBf16>;
+            case kEpiBf16SR: return &gemm_persistent_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.occ, KIND, kEpiBf16SR>;
+            case kEpiFp8:
+                if constexpr (KIND == kFP8FP8) return &gemm_persistent_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.occ, KIND, kEpiFp8>;
+                else return nullptr;
+            default: return nullptr;
+        }
+    }
+}
+
 template <int KIND, int I = 0>
-KernelFn lookup_tile(int bm, int bn, int epi) {
+KernelFn lookup_tile(int bm, int bn, int epi, bool persistent) {
     if constexpr (I == kNumTiles) {
         return nullptr;
     } else {
-        if (bm == kTiles[I].bm && bn == kTiles[I].bn) return pick_epi<I, KIND>(epi);
-        return lookup_tile<KIND, I + 1>(bm, bn, epi);
+        if (bm == kTiles[I].bm && bn == kTiles[I].bn)
+            return persistent ? pick_persistent_epi<I, KIND>(epi) : pick_epi<I, KIND>(epi);
+        return lookup_tile<KIND, I + 1>(bm, bn, epi, persistent);
     }
 }
 
@@ -87,9 +108,9 @@ constexpr SkinnyCfg kSkinny[] = {{1, 1, 4, 2, 16}, {1, 1, 4, 3, 16}, {1, 1, 4, 2
 constexpr int kNumSkinny = sizeof(kSkinny) / sizeof(kSkinny[0]);
 KernelFn lookup_skinny(int kind, int mt, int nb, int nw, int d, int ar, int epi);
 
-KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi);
-KernelFn lookup_kernel_fp8fp4(int bm, int bn, int epi);
-KernelFn lookup_kernel_fp4fp4(int bm, int bn, int epi);
-KernelFn lookup_kernel_bf16(int bm, int bn, int epi);
+KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi, bool persistent);
+KernelFn lookup_kernel_fp8fp4(int bm, int bn, int epi, bool persistent);
+KernelFn lookup_kernel_fp4fp4(int bm, int bn, int epi, bool persistent);
+KernelFn lookup_kernel_bf16(int bm, int bn, int epi, bool persistent);
 
 }  // namespace dg

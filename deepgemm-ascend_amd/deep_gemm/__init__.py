@@ -34,6 +34,7 @@ from .gemm import (  # noqa: E402
     m_grouped_bf16_gemm_nt_masked,
     k_grouped_fp8_gemm_tn_contiguous, k_grouped_fp8_gemm_nt_contiguous, k_grouped_bf16_gemm_tn_contiguous,
     select_config,
+    launch_plan,
 )
 from .einsum import fp8_bmm, bf16_bmm, einsum, fp8_einsum  # noqa: E402
 from . import epilogue  # noqa: E402

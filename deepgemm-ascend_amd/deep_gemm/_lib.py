@@ -23,7 +23,7 @@ DG_COMPILED_M, DG_COMPILED_N, DG_COMPILED_K = 1, 2, 4
 # Every symbol include/deep_gemm_amd.h declares.
 EXPORTED_SYMBOLS = ('dg_gemm', 'dg_transform_sf', 'dg_transform_k_grouped_sf', 'dg_transpose_to_k_major', 'dg_device_num_cus', 'dg_select_config',
                     'dg_gemm_workspace_size', 'dg_last_error', 'dg_version', 'dg_jit_compile', 'dg_jit_set_include_dir',
-                    'dg_jit_stats')
+                    'dg_jit_stats', 'dg_launch_plan')
 
 
 class GemmArgs(ctypes.Structure):
@@ -44,6 +44,15 @@ class GemmArgs(ctypes.Structure):
         ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_int64),
         ('epilogue', ctypes.c_int32), ('sfd', ctypes.c_void_p), ('sfd_ld', ctypes.c_int64),
         ('jit', ctypes.c_int32), ('compiled_dims', ctypes.c_int32),
+    ]
+
+
+class LaunchInfo(ctypes.Structure):
+    """Mirror of ``dg_launch_info`` (include/deep_gemm_amd.h)."""
+    _fields_ = [
+        ('block_m', ctypes.c_int32), ('block_n', ctypes.c_int32), ('grid', ctypes.c_int64),
+        ('threads', ctypes.c_int32), ('tiles', ctypes.c_int64), ('split_k', ctypes.c_int32),
+        ('persistent', ctypes.c_int32), ('skinny', ctypes.c_int32),
     ]
 
 
@@ -90,6 +99,8 @@ def load(path=None) -> ctypes.CDLL:
         lib.dg_select_config.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(ctypes.c_int32),
                                          ctypes.POINTER(ctypes.c_int32)]
         lib.dg_select_config.restype = ctypes.c_int
+        lib.dg_launch_plan.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(LaunchInfo)]
+        lib.dg_launch_plan.restype = ctypes.c_int
         lib.dg_gemm_workspace_size.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(ctypes.c_int64)]
         lib.dg_gemm_workspace_size.restype = ctypes.c_int
         lib.dg_jit_compile.argtypes = [ctypes.POINTER(GemmArgs)]

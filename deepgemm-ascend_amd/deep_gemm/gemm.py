@@ -640,3 +640,31 @@ def select_config(m: int, n: int, k: int, kind: int = _lib.DG_KIND_FP8_FP8, gemm
     lib = _lib.load()
     _lib.check(lib.dg_select_config(args, ctypes.byref(bm), ctypes.byref(bn)), lib)
     return bm.value, bn.value
+
+
+def launch_plan(m: int, n: int, k: int, kind: int = _lib.DG_KIND_FP8_FP8, gemm_type: int = _lib.DG_GEMM_NORMAL,
+                num_groups: int = 1) -> dict:
+    """The launch the library would make for a K-major GEMM of this shape under the current
+    runtime settings (set_num_sms, mk alignment): tile, workgroups, threads, tiles, K split and
+    whether the workgroups walk tiles persistently.  Nothing is launched."""
+    import ctypes
+    args = _lib.GemmArgs()
+    # K as the calls pass it to the kernels: padded so rows stay whole 16-byte pieces
+    k = -(-k // {_lib.DG_KIND_BF16: 8, _lib.DG_KIND_FP4_FP4: 32, _lib.DG_KIND_FP8_FP4: 32}.get(kind, 16)) * \
+        {_lib.DG_KIND_BF16: 8, _lib.DG_KIND_FP4_FP4: 32, _lib.DG_KIND_FP8_FP4: 32}.get(kind, 16)
+    args.kind, args.gemm_type, args.m, args.n, args.k, args.num_groups = kind, gemm_type, m, n, k, num_groups
+    # leading dimensions in storage elements (packed FP4: two per byte)
+    args.lda = k // 2 if kind == _lib.DG_KIND_FP4_FP4 else k
+    args.ldb = k // 2 if kind in (_lib.DG_KIND_FP4_FP4, _lib.DG_KIND_FP8_FP4) else k
+    args.ldd = n
+    args.batch_stride_a, args.batch_stride_b = m * args.lda, n * args.ldb
+    args.batch_stride_d = m * n
+    nk64 = (k + 63) // 64
+    args.sfa_ld, args.sfb_ld = (m + 1) // 2 * 2, (n + 1) // 2 * 2
+    args.sfa_batch_stride, args.sfb_batch_stride = args.sfa_ld * nk64, args.sfb_ld * nk64
+    args.alignment = get_mk_alignment_for_contiguous_layout()
+    args.num_cus = get_num_sms()
+    info = _lib.LaunchInfo()
+    lib = _lib.load()
+    _lib.check(lib.dg_launch_plan(args, ctypes.byref(info)), lib)
+    return {f: getattr(info, f) for f, _ in _lib.LaunchInfo._fields_}

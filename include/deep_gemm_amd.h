@@ -194,6 +194,23 @@ int dg_gemm_workspace_size(const dg_gemm_args *args, int64_t *bytes);
 /* Tile shape dg_gemm() would pick for `args` (block_m, block_n written to the pointers). */
 int dg_select_config(const dg_gemm_args *args, int32_t *block_m, int32_t *block_n);
 
+/* The launch dg_gemm() would make for `args`, described without launching (nothing touches the
+ * device).  Replaces the reference's GemmConfig / LaunchOptions as its heuristic returns them
+ * (csrc/jit_kernels/gemm_config.hpp:39-95, csrc/jit_kernels/heuristics.hpp:92-98): the reference
+ * launches `num_blocks = num_cores` persistent blocks; here `grid` is the workgroup count, equal
+ * to min(tiles, num_cus) for a persistent launch (set_num_sms caps it) and to the tile count
+ * (times split_k) otherwise. */
+typedef struct dg_launch_info {
+    int32_t block_m, block_n;     /* tile (skinny kernel: rows of A staged x strip columns)       */
+    int64_t grid;                 /* workgroups launched                                          */
+    int32_t threads;              /* threads per workgroup                                        */
+    int64_t tiles;                /* output tiles (strips) of the problem                         */
+    int32_t split_k;              /* K ranges per tile (1 = unsplit)                              */
+    int32_t persistent;           /* 1: workgroups walk tiles (grid < tiles possible)             */
+    int32_t skinny;               /* 1: the decode-shape kernel                                   */
+} dg_launch_info;
+int dg_launch_plan(const dg_gemm_args *args, dg_launch_info *info);
+
 /* Message of the last failing call on this thread ("" if none). */
 const char *dg_last_error(void);
 

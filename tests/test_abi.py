@@ -102,3 +102,29 @@ def test_transform_sf_argument_checks(lib):
     assert b'sf_k' in lib.dg_last_error()
     # psum with an alignment that gran_mn does not divide
     assert f(4096, 0, 0, 1, 1, 1, 1, 2, 128, 64, 128, 32, 4096, 2, 64, 4096, 0, None, None) == -1
+
+
+def _plan_args(m, n, k, num_cus):
+    args = _lib.GemmArgs()
+    args.kind, args.gemm_type, args.m, args.n, args.k, args.num_groups = 0, 0, m, n, k, 1
+    args.lda, args.ldb, args.ldd = k, k, n
+    args.sfa_ld, args.sfb_ld = (m + 1) // 2 * 2, (n + 1) // 2 * 2
+    args.alignment, args.num_cus = 256, num_cus
+    return args
+
+
+def test_launch_plan_without_device(lib):
+    """dg_launch_plan describes the launch and touches no device: one workgroup per tile at the
+    full CU count, persistent min(tiles, num_cus) workgroups under a set_num_sms cap (below the
+    256 CUs of MI355X the library assumes when it cannot query a device)."""
+    full = _lib.LaunchInfo()
+    assert lib.dg_launch_plan(_plan_args(4096, 7168, 2048, 0), ctypes.byref(full)) == 0, lib.dg_last_error()
+    assert full.persistent == 0 and full.grid == full.tiles and full.block_m == 256
+    capped = _lib.LaunchInfo()
+    assert lib.dg_launch_plan(_plan_args(4096, 7168, 2048, 64), ctypes.byref(capped)) == 0, lib.dg_last_error()
+    assert capped.persistent == 1 and capped.grid == 64 and capped.tiles > 64
+    assert (capped.block_m, capped.block_n) != (256, 256)   # no persistent 256x256 kernel
+    small = _lib.LaunchInfo()
+    assert lib.dg_launch_plan(_plan_args(1, 2112, 7168, 64), ctypes.byref(small)) == 0, lib.dg_last_error()
+    assert small.skinny == 1 and small.persistent == 0
+    assert lib.dg_launch_plan(None, None) == -1
