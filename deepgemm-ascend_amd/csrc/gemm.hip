@@ -525,6 +525,69 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
 
 extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) { return gemm_impl(args, stream, false); }
 
+// ---------------------------------------------------------------------------------------------
+// dg_gemm_noalloc: dg_gemm with the split-K workspace taken from a fixed device array instead of
+// the caller's (for callers that cannot allocate: graph capture, serving loops).
+namespace {
+
+// Scratch of dg_gemm_noalloc: the workspace layout of dg_gemm (64 KiB of tile counters, then the
+// fp32 partial tiles).  Zero at load; every launch leaves the counters zero again.  Each device
+// holds its own copy until the process ends.
+constexpr int64_t kNoAllocScratchBytes = (16 << 20) + dg::kCounterBytes;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {nullptr};
+
+// Device address of `scratch` on the current device (host code never passes the array's name:
+// that is a host-side stand-in, not a device address).
+int scratch_address(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return dg_set_error("dg_gemm_noalloc: no current HIP device");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            std::string msg = std::string("dg_gemm_noalloc: hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e);
+            dg_set_error(msg.c_str());
+            return DG_ELAUNCH;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return DG_OK;
+}
+
+}  // namespace
+
+extern "C" int dg_gemm_noalloc(const dg_gemm_args* args, void* stream) {
+    if (args == nullptr) return dg_set_error("dg_gemm_noalloc: null args");
+    dg_gemm_args a = *args;
+    if (a.workspace != nullptr || a.workspace_bytes != 0)
+        return dg_set_error("dg_gemm_noalloc: the library provides the workspace (pass workspace = NULL, 0 bytes)");
+    int64_t need = 0;
+    a.workspace = reinterpret_cast<void*>(1);   // (any non-null value: the plan may then split K)
+    int rc = dg_gemm_workspace_size(&a, &need);
+    if (rc != DG_OK) return rc;
+    if (need > kNoAllocScratchBytes) {
+        char buf[200];
+        snprintf(buf, sizeof(buf), "dg_gemm_noalloc: this problem's split-K plan needs %lld bytes of scratch, more than "
+                 "the %lld-byte maximum (call dg_gemm with a workspace, or split_k = 1)", (long long)need,
+                 (long long)kNoAllocScratchBytes);
+        return dg_set_error(buf);
+    }
+    // (the scratch stands in for a workspace whether or not this plan splits K, so the plan is
+    // always the one dg_gemm makes when given a workspace)
+    void* ptr = nullptr;
+    rc = scratch_address(&ptr);
+    if (rc != DG_OK) return rc;
+    a.workspace = ptr;
+    a.workspace_bytes = kNoAllocScratchBytes;
+    return gemm_impl(&a, stream, false);
+}
+
 extern "C" int dg_launch_plan(const dg_gemm_args* args, dg_launch_info* info) {
     if (args == nullptr || info == nullptr) return dg_set_error("dg_launch_plan: null argument");
     return gemm_impl(args, nullptr, true, info);

@@ -23,7 +23,7 @@ DG_COMPILED_M, DG_COMPILED_N, DG_COMPILED_K = 1, 2, 4
 # Every symbol include/deep_gemm_amd.h declares.
 EXPORTED_SYMBOLS = ('dg_gemm', 'dg_transform_sf', 'dg_transform_k_grouped_sf', 'dg_transpose_to_k_major', 'dg_device_num_cus', 'dg_select_config',
                     'dg_gemm_workspace_size', 'dg_last_error', 'dg_version', 'dg_jit_compile', 'dg_jit_set_include_dir',
-                    'dg_jit_stats', 'dg_launch_plan')
+                    'dg_jit_stats', 'dg_launch_plan', 'dg_gemm_noalloc')
 
 
 class GemmArgs(ctypes.Structure):
@@ -99,6 +99,8 @@ def load(path=None) -> ctypes.CDLL:
         lib.dg_select_config.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(ctypes.c_int32),
                                          ctypes.POINTER(ctypes.c_int32)]
         lib.dg_select_config.restype = ctypes.c_int
+        lib.dg_gemm_noalloc.argtypes = [ctypes.POINTER(GemmArgs), ctypes.c_void_p]
+        lib.dg_gemm_noalloc.restype = ctypes.c_int
         lib.dg_launch_plan.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(LaunchInfo)]
         lib.dg_launch_plan.restype = ctypes.c_int
         lib.dg_gemm_workspace_size.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(ctypes.c_int64)]

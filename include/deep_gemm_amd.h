@@ -191,6 +191,16 @@ int dg_device_num_cus(int32_t device);
  */
 int dg_gemm_workspace_size(const dg_gemm_args *args, int64_t *bytes);
 
+/* dg_gemm() that allocates nothing and takes no workspace: a split-K plan keeps its tile counters
+ * and fp32 partials in a fixed device array of the library, 16 MiB + 64 KiB, held by every device
+ * the library runs on until the process ends (args->workspace must be NULL and workspace_bytes 0;
+ * a problem whose split-K plan needs more scratch is rejected with an error).  No counterpart in
+ * the reference: it is for callers that cannot allocate -- code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc.  Calls on one device share that array: calls that
+ * overlap in time on one device (different streams) race; calls issued in order on one stream do
+ * not (each launch leaves the counters zero for the next). */
+int dg_gemm_noalloc(const dg_gemm_args *args, void *stream);
+
 /* Tile shape dg_gemm() would pick for `args` (block_m, block_n written to the pointers). */
 int dg_select_config(const dg_gemm_args *args, int32_t *block_m, int32_t *block_n);
 

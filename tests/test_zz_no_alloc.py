@@ -1,0 +1,85 @@
+"""dg_gemm_noalloc (the allocation-free dg_gemm: split-K scratch in a fixed device array) against
+dg_gemm with a caller workspace, through the C ABI: the same plan, bit-identical D, on two calls in
+a row (the second smaller), plus the oracle and the over-size rejection."""
+import ctypes
+
+import pytest
+import torch
+
+import deep_gemm
+from deep_gemm import _lib
+from oracle import gemm as og
+from helpers import gen, operand, calc_diff
+
+pytestmark = pytest.mark.gpu
+
+
+def _args(m, n, k, seed):
+    """Filled dg_gemm_args (K-major e4m3 A / B, packed SF) and the tensors it points at."""
+    g = gen(seed)
+    a, sfa, a_deq = operand(m, k, 'e4m3', (1, 128), g, 'randn')
+    b, sfb, b_deq = operand(n, k, 'e4m3', (128, 128), g, 'randn')
+    a, b = a.cuda(), b.cuda()
+    sfa_t = deep_gemm.transform_sf_into_required_layout(sfa.cuda(), m, k, (1, 128), is_sfa=True)
+    sfb_t = deep_gemm.transform_sf_into_required_layout(sfb.cuda(), n, k, (128, 128), is_sfa=False)
+    args = _lib.GemmArgs()
+    args.kind, args.gemm_type, args.m, args.n, args.k, args.num_groups = _lib.DG_KIND_FP8_FP8, _lib.DG_GEMM_NORMAL, m, n, k, 1
+    args.a, args.b, args.sfa, args.sfb = a.data_ptr(), b.data_ptr(), sfa_t.data_ptr(), sfb_t.data_ptr()
+    args.lda, args.ldb, args.ldd = a.stride(0), b.stride(0), n
+    args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
+    args.d_dtype, args.alpha, args.alignment = _lib.DG_DTYPE_BF16, 1.0, 256
+    keep = (a, b, sfa_t, sfb_t)
+    return args, keep, og.gemm_nt(a_deq, b_deq)
+
+
+def _run(lib, args, noalloc):
+    d = torch.empty(args.m, args.n, dtype=torch.bfloat16, device='cuda')
+    args.d = d.data_ptr()
+    stream = torch.cuda.current_stream().cuda_stream
+    if noalloc:
+        args.workspace, args.workspace_bytes = None, 0
+        rc = lib.dg_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(stream))
+        ws = None
+    else:
+        nbytes = ctypes.c_int64(0)
+        _lib.check(lib.dg_gemm_workspace_size(ctypes.byref(args), ctypes.byref(nbytes)), lib)
+        ws = torch.zeros(max(nbytes.value, 1), dtype=torch.uint8, device='cuda')
+        args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes.value
+        rc = lib.dg_gemm(ctypes.byref(args), ctypes.c_void_p(stream))
+    _lib.check(rc, lib)
+    torch.cuda.synchronize()
+    return d.cpu()
+
+
+def test_noalloc_matches_dg_gemm_on_two_calls():
+    lib = _lib.load()
+    # a split-K decode plan, then a smaller one (the array keeps the first call's contents)
+    for (m, n, k), seed in (((64, 4096, 7168), 1), ((1, 2112, 4096), 2)):
+        args, keep, ref = _args(m, n, k, seed)
+        info = _lib.LaunchInfo()
+        args.workspace, args.workspace_bytes = 1, 1 << 40   # plan as for a caller with a workspace
+        _lib.check(lib.dg_launch_plan(ctypes.byref(args), ctypes.byref(info)), lib)
+        args.workspace, args.workspace_bytes = None, 0
+        print(f'noalloc m={m} n={n} k={k} split_k={info.split_k} skinny={info.skinny}', flush=True)
+        assert info.split_k > 1, 'the case must exercise the split-K scratch'
+        d_noalloc = _run(lib, args, True)
+        d_ws = _run(lib, args, False)
+        assert torch.equal(d_noalloc, d_ws)
+        assert calc_diff(d_noalloc, ref) < 1e-5
+        # again, now that the array holds this call's counters and partials
+        assert torch.equal(_run(lib, args, True), d_ws)
+
+
+def test_noalloc_rejects_oversize_and_a_workspace():
+    lib = _lib.load()
+    args, keep, _ = _args(128, 8192, 16384, 3)
+    d = torch.empty(128, 8192, dtype=torch.bfloat16, device='cuda')
+    args.d = d.data_ptr()
+    args.split_k = 16   # forced: 16 K ranges of every strip need more than the fixed array
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.dg_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(stream)) != 0
+    assert b'maximum' in lib.dg_last_error()
+    args.split_k = 0
+    args.workspace, args.workspace_bytes = d.data_ptr(), 16
+    assert lib.dg_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(stream)) != 0
+    assert b'library provides the workspace' in lib.dg_last_error()
