@@ -44,6 +44,10 @@ def parse():
                          '(cold-L2 kernel times) instead of the north-star line')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a 256 MiB device copy (reference kernel for FETCH_SIZE / WRITE_SIZE scaling)')
+    ap.add_argument('--profile-case', choices=('north', 'grouped', 'decode'), default=None,
+                    help='launch one workload 20 times and exit (the command rocprofv3 wraps for the profiles/ '
+                         'summaries): north = fp8_gemm_nt 4096x7168x2048, grouped = m_grouped contiguous G=32 '
+                         'N=4096 K=7168, decode = fp8_gemm_nt 128x2112x7168')
     return ap.parse_args()
 
 
@@ -65,6 +69,47 @@ def make_inputs(m, n, k):
     a, sfa, a_deq = quant.quantize_blockwise(torch.randn(m, k, generator=g), (1, 128), 'e4m3')
     b, sfb, b_deq = quant.quantize_blockwise(torch.randn(n, k, generator=g), (128, 128), 'e4m3')
     return a, sfa, a_deq, b, sfb, b_deq
+
+
+def cpu_model() -> str:
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return 'unknown'
+
+
+def cpu_baseline_config1(runs=15):
+    """BASELINE config 1 on the host: fp8_gemm_nt 128x256x512 through the oracle (per-block dequantise
+    -> fp32 matmul -> bf16), seeded N(0,1) A / B with 1x128 / 128x128 UE8M0 scales; 3 warm-ups, median of
+    `runs` timed calls."""
+    import torch
+    from oracle import quant, gemm as og
+    m, n, k = 128, 256, 512
+    g = torch.Generator().manual_seed(0)
+    a, sfa, _ = quant.quantize_blockwise(torch.randn(m, k, generator=g), (1, 128), 'e4m3')
+    b, sfb, _ = quant.quantize_blockwise(torch.randn(n, k, generator=g), (128, 128), 'e4m3')
+
+    def run():
+        a_deq = quant.decode(a) * quant.expand_sf(sfa, (m, k), (1, 128))
+        b_deq = quant.decode(b) * quant.expand_sf(sfb, (n, k), (128, 128))
+        return og.gemm_nt(a_deq, b_deq)
+
+    for _ in range(3):
+        run()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {'config': 'fp8_gemm_nt 128x256x512 (BASELINE config 1)', 'median_us': round(med * 1e6, 1),
+            'gflops': round(2.0 * m * n * k / med / 1e9, 2), 'runs': runs, 'threads': torch.get_num_threads(),
+            'os_cpu_count': os.cpu_count(), 'cpu_model': cpu_model()}
 
 
 def cpu_baseline(a, sfa, b, sfb, m, n, k, seconds):
@@ -90,7 +135,7 @@ def cpu_baseline(a, sfa, b, sfb, m, n, k, seconds):
         'value': round(2.0 * m * n * k / med / 1e12, 4), 'unit': 'TFLOP/s', 'cores': torch.get_num_threads(),
         'kind': 'port',
         'sample': f'full {m}x{n}x{k} fp8_gemm_nt oracle (dequant->fp32 matmul->bf16), median of {len(times)} '
-                  f'runs ({med * 1e3:.1f} ms each), host os.cpu_count()={os.cpu_count()}',
+                  f'runs ({med * 1e3:.1f} ms each), host os.cpu_count()={os.cpu_count()}, {cpu_model()}',
     }
 
 
@@ -267,6 +312,42 @@ def run_suite(groups):
                   bsz * h * r + h * dd * r + 2 * bsz * h * dd, includes='SF transform')
 
 
+def profile_case(case):
+    """20 launches of one workload (warm), nothing else: the command the profiles/ summaries wrap."""
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    gen = torch.Generator(device=dev).manual_seed(0)
+    if case in ('north', 'decode'):
+        m, n, k = (4096, 7168, 2048) if case == 'north' else (128, 2112, 7168)
+        a, sfa = _gpu_codes((m, k), dev, gen), _gpu_sf((m, k // 128), dev, gen)
+        b, sfb = _gpu_codes((n, k), dev, gen), _gpu_sf((-(-n // 128), k // 128), dev, gen)
+        sfa = deep_gemm.transform_sf_into_required_layout(sfa, m, k, (1, 128), is_sfa=True)
+        sfb = deep_gemm.transform_sf_into_required_layout(sfb, n, k, (128, 128), is_sfa=False)
+        d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        fn = lambda: deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d)
+    else:
+        counts = _routed_counts()
+        align = 128
+        deep_gemm.set_mk_alignment_for_contiguous_layout(align)
+        total, psum = 0, []
+        for c in counts:
+            psum.append(total + c)
+            total = -(-(total + c) // align) * align
+        n, k, g_ = 4096, 7168, len(counts)
+        a, sfa = _gpu_codes((total, k), dev, gen), _gpu_sf((total, k // 128), dev, gen)
+        b, sfb = _gpu_codes((g_, n, k), dev, gen), _gpu_sf((g_, n // 128, k // 128), dev, gen)
+        layout = torch.tensor(psum, dtype=torch.int32, device=dev)
+        sfa = deep_gemm.transform_sf_into_required_layout(sfa, total, k, (1, 128), is_sfa=True, psum_layout=layout)
+        sfb = deep_gemm.transform_sf_into_required_layout(sfb, n, k, (128, 128), num_groups=g_, is_sfa=False)
+        d = torch.empty(total, n, dtype=torch.bfloat16, device=dev)
+        fn = lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous((a, sfa), (b, sfb), d, layout)
+    for _ in range(20):
+        fn()
+    torch.cuda.synchronize()
+    print(json.dumps({'profile_case': case, 'launches': 20}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
@@ -278,6 +359,9 @@ def main():
         return
     if args.suite:
         run_suite(set(args.suite.split(',')))
+        return
+    if args.profile_case:
+        profile_case(args.profile_case)
         return
     import torch
     import deep_gemm
@@ -328,10 +412,13 @@ def main():
     torch.cuda.synchronize()
     kern_ms = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
     kern_avg = sum(kern_ms) / len(kern_ms)
+    # cold-L2 kernel time (operands evicted from L2 and the MALL before every launch, as the
+    # reference times its kernels): the roofline's achieved rate
+    cold_us = _time_cold(step, iters=max(10, min(args.steps, 40)))
 
     flops = 2.0 * m * n * k
     tflops = flops / (ms_per_step * 1e-3) / 1e12
-    achieved = flops / (kern_avg * 1e-3) / 1e12
+    achieved = flops / (cold_us * 1e-6) / 1e12
     traffic = None
     if os.path.exists(TRAFFIC_FILE) and (m, n, k) == (M, N, K):
         with open(TRAFFIC_FILE) as f:
@@ -348,12 +435,16 @@ def main():
                    'tile': f'{cfg[0]}x{cfg[1]}', 'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': round(achieved, 2), 'peak': PEAK_FP8_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': round(achieved / PEAK_FP8_TFLOPS, 4), 'traffic': traffic,
-                     'kernel_avg_us': round(kern_avg * 1e3, 3), 'kernel_min_us': round(kern_ms[0] * 1e3, 3)},
+                     'kernel_us_cold_median': round(cold_us, 3),
+                     'kernel_avg_us_warm': round(kern_avg * 1e3, 3), 'kernel_min_us_warm': round(kern_ms[0] * 1e3, 3),
+                     'timing': 'achieved = 2MNK / cold-L2 kernel time (HIP events around each launch on its stream, '
+                               '1 GiB read evicts L2 and the MALL before each); value = back-to-back warm steps'},
         'calc_diff': diff,
         'wall_s_timed': round(wall, 4),
     }
     if not args.no_cpu:
         out['cpu_baseline'] = cpu_baseline(a, sfa, b, sfb, m, n, k, args.cpu_seconds)
+        out['cpu_baseline_config1'] = cpu_baseline_config1()
     print(json.dumps(out), flush=True)
 
 
