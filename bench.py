@@ -40,7 +40,7 @@ def parse():
     ap.add_argument('--n', type=int, default=N)
     ap.add_argument('--k', type=int, default=K)
     ap.add_argument('--suite', default=None,
-                    help='comma list of dense,bf16,fp4,grouped,kgrouped,einsum: one JSON line per shape '
+                    help='comma list of dense,bf16,fp4,grouped,kgrouped,einsum,host: one JSON line per shape '
                          '(cold-L2 kernel times) instead of the north-star line')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a 256 MiB device copy (reference kernel for FETCH_SIZE / WRITE_SIZE scaling)')
@@ -299,6 +299,38 @@ def run_suite(groups):
             sk = sum(ks)
             _line('kgrouped', f'k_grouped_fp8_gemm_tn G={g_} M={m} N={n} sumK={sk} fp32 acc', us,
                   2.0 * m * n * sk, total * (m + n) + 8 * g_ * m * n, includes='MN->K-major operand copy and SF transform')
+    if 'host' in groups:
+        # Host time per call: `calls` launches queued behind a spin kernel (so the device never
+        # pushes back), wall time / calls; through the C++ host path and through the Python path.
+        from deep_gemm import _lib
+        calls = 200
+        for m, n, k in ((128, 2112, 7168), (4096, 7168, 2048)):
+            a, sfa32 = fp8_operand(m, k, 1)
+            b, sfb32 = fp8_operand(n, k, 128)
+            sfa = deep_gemm.transform_sf_into_required_layout(sfa32, m, k, (1, 128), is_sfa=True)
+            sfb = deep_gemm.transform_sf_into_required_layout(sfb32, n, k, (128, 128), is_sfa=False)
+            d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            for sf_kind, (sa, sb) in (('packed', (sfa, sfb)), ('fp32', (sfa32, sfb32))):
+                for path in ('cpp', 'python'):
+                    saved = _lib.ext()
+                    if path == 'python':
+                        _lib._ext = None
+                    try:
+                        rec = dict(recipe_a=(1, 128), recipe_b=(128, 128)) if sf_kind == 'fp32' else {}
+                        fn = lambda: deep_gemm.fp8_gemm_nt((a, sa), (b, sb), d, **rec)
+                        for _ in range(5):
+                            fn()
+                        torch.cuda.synchronize()
+                        torch.cuda._sleep(int(3e8))
+                        t0 = time.perf_counter()
+                        for _ in range(calls):
+                            fn()
+                        host_us = (time.perf_counter() - t0) / calls * 1e6
+                        torch.cuda.synchronize()
+                    finally:
+                        _lib._ext = saved
+                    print(json.dumps({'suite': 'host', 'workload': f'fp8_gemm_nt {m}x{n}x{k}', 'sf': sf_kind,
+                                      'path': path, 'host_us_per_call': round(host_us, 2)}), flush=True)
     if 'einsum' in groups:
         h, r, dd = 8, 4096, 1024
         for bsz in (4096, 8192):

@@ -64,10 +64,32 @@ def build(jobs: int = 0, verbose: bool = False) -> Path:
     return LIB
 
 
+EXT_NAME = 'deep_gemm_C'
+EXT = ROOT / 'deep_gemm' / f'{EXT_NAME}.so'
+
+
+def build_ext(verbose: bool = False) -> Path:
+    """The C++ host-path extension (csrc/torch_ext.cpp), built with torch's extension builder into
+    ``deep_gemm/deep_gemm_C.so``.  It links no HIP code: the Python layer hands it the loaded
+    library's entry points."""
+    import torch.utils.cpp_extension as ce
+    bdir = OUT_DIR / 'ext'
+    bdir.mkdir(parents=True, exist_ok=True)
+    ce.load(name=EXT_NAME, sources=[str(CSRC / 'torch_ext.cpp')], build_directory=str(bdir),
+            extra_cflags=['-O2', '-std=c++17'], extra_include_paths=[str(ROOT.parent / 'include')],
+            with_cuda=False, verbose=verbose, is_python_module=True)
+    built = bdir / f'{EXT_NAME}.so'
+    tmp = EXT.with_suffix('.so.tmp')
+    shutil.copyfile(built, tmp)
+    os.replace(tmp, EXT)
+    return EXT
+
+
 if __name__ == '__main__':
     ap = argparse.ArgumentParser()
     ap.add_argument('-j', type=int, default=0)
     ap.add_argument('-v', action='store_true')
     args = ap.parse_args()
     print(build(args.j, args.v))
+    print(build_ext(args.v))
     sys.exit(0)

@@ -7,9 +7,11 @@
 // fixed menu of tile shapes; the heuristic scores each shape with a gfx950 model
 // (256 CUs, waves-of-tiles quantisation, measured cycles per K stage of each tile shape and a
 // fixed per-tile cost) and memoises the choice per problem signature.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -43,6 +45,10 @@ extern "C" int dg_device_num_cus(int32_t device) {
 }
 
 namespace dg {
+
+// csrc/status.hip: m_indices layout check of M-grouped launches (reports through the sticky error
+// words; with may_alloc false it never allocates them)
+int check_m_indices(const int32_t* idx, int m, int alignment, int num_groups, hipStream_t st, bool may_alloc);
 
 KernelFn lookup_kernel(int kind, int bm, int bn, int epi, bool persistent) {
     switch (kind) {
@@ -330,7 +336,7 @@ int elem_bytes_times2(int kind, bool is_a) {
 extern "C" int dg_select_config(const dg_gemm_args* args, int32_t* block_m, int32_t* block_n) {
     if (args == nullptr) return dg_set_error("dg_select_config: null args");
     const int cus = args->num_cus > 0 ? args->num_cus : dg::device_cus();
-    const dg::Plan pl = dg::choose(*args, cus, args->workspace != nullptr || args->split_k > 1);
+    const dg::Plan pl = dg::choose(*args, cus, args->workspace != nullptr || args->library_workspace != 0 || args->split_k > 1);
     if (pl.tile.bm == 0) return dg_set_error("no tile shape fits this problem (M-grouped alignment must be a multiple of 32)");
     if (block_m) *block_m = pl.tile.bm;
     if (block_n) *block_n = pl.tile.bn;
@@ -350,8 +356,75 @@ extern "C" int dg_gemm_workspace_size(const dg_gemm_args* args, int64_t* bytes) 
 
 namespace {
 
+// Launches an ahead-of-time kernel through hipModuleLaunchKernel: its hipFunction_t handle is
+// looked up once (hipGetFuncBySymbol) and cached per kernel.
+std::mutex g_func_mu;
+std::unordered_map<const void*, hipFunction_t> g_funcs;
+
+hipError_t launch_module_kernel(const void* kernel, unsigned grid, unsigned threads, dg::KParams& p, hipStream_t st) {
+    hipFunction_t f = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_func_mu);
+        auto it = g_funcs.find(kernel);
+        if (it != g_funcs.end()) {
+            f = it->second;
+        } else {
+            const hipError_t e = hipGetFuncBySymbol(&f, kernel);
+            if (e != hipSuccess) return e;
+            g_funcs.emplace(kernel, f);
+        }
+    }
+    void* params[] = {&p};
+    return hipModuleLaunchKernel(f, grid, 1, 1, threads, 1, 1, 0, st, params, nullptr);
+}
+
+// Split-K workspaces the library owns, one per (device, stream): zero-filled when allocated, left
+// zero-filled by every launch (so calls issued in order on one stream share one), only ever grown,
+// and never freed -- a graph captured on the stream may still hold an older one.  Calls that run
+// at the same time on one stream's workspace (a graph replayed on another stream while the capture
+// stream runs eager calls) race on its counters.
+struct StreamWorkspace {
+    void* ptr = nullptr;
+    int64_t bytes = 0;
+};
+std::mutex g_stream_ws_mu;
+std::map<std::pair<int, hipStream_t>, StreamWorkspace> g_stream_ws;
+
+int stream_workspace(hipStream_t st, int64_t need, void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return dg_set_error("dg_gemm: no current HIP device");
+    std::lock_guard<std::mutex> lk(g_stream_ws_mu);
+    StreamWorkspace& w = g_stream_ws[{dev, st}];
+    if (w.bytes >= need) {
+        *out = w.ptr;
+        return DG_OK;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) (void)hipGetLastError();
+    if (cs != hipStreamCaptureStatusNone) {
+        char buf[256];
+        snprintf(buf, sizeof(buf), "dg_gemm: this split-K call needs a %lld-byte workspace but the stream's is %lld "
+                 "bytes, and it cannot grow while the stream is being captured: run the same call once before "
+                 "the capture", (long long)need, (long long)w.bytes);
+        return dg_set_error(buf);
+    }
+    const int64_t bytes = std::max<int64_t>({need, 2 * w.bytes, int64_t(1) << 20});
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, (size_t)bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(p, 0, (size_t)bytes, st);   // (never inside a capture: checked above)
+    if (e != hipSuccess) {
+        std::string msg = std::string("dg_gemm: split-K workspace allocation failed: ") + hipGetErrorString(e);
+        return dg_set_error(msg.c_str());
+    }
+    w.ptr = p;
+    w.bytes = bytes;
+    *out = p;
+    return DG_OK;
+}
+
 // Checks, plans and launches one GEMM; with `info` it stops short of the launch and describes it.
-int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_launch_info* info = nullptr) {
+int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_launch_info* info = nullptr,
+              bool noalloc = false) {
     using namespace dg;
     if (args == nullptr) return dg_set_error("dg_gemm: null args");
     const dg_gemm_args& a = *args;
@@ -413,8 +486,15 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
 
     const int cus = a.num_cus > 0 ? a.num_cus : device_cus();
     if (a.split_k < 0) return dg_set_error("dg_gemm: split_k must be >= 0");
-    Plan plan = choose(a, cus, a.workspace != nullptr);
-    if (plan.split > 1 && plan_workspace(a, plan) > a.workspace_bytes) {
+    const bool lib_ws = a.workspace == nullptr && a.library_workspace != 0;
+    Plan plan = choose(a, cus, a.workspace != nullptr || lib_ws);
+    void* workspace = a.workspace;
+    if (plan.split > 1 && lib_ws) {
+        if (!plan_only && !compile_only) {
+            const int rc = stream_workspace(reinterpret_cast<hipStream_t>(stream), plan_workspace(a, plan), &workspace);
+            if (rc != DG_OK) return rc;
+        }
+    } else if (plan.split > 1 && plan_workspace(a, plan) > a.workspace_bytes) {
         if (a.split_k > 1) return dg_set_error("dg_gemm: workspace smaller than dg_gemm_workspace_size() reports");
         plan = choose(a, cus, false);
     }
@@ -495,8 +575,8 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     p.split_stages = plan.split_stages;
     p.num_tiles = (int)tiles;
     if (plan.split > 1) {
-        p.counters = reinterpret_cast<int*>(a.workspace);
-        p.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.workspace) + kCounterBytes);
+        p.counters = reinterpret_cast<int*>(workspace);
+        p.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + kCounterBytes);
     }
     const int threads = skinny ? plan.skinny_nw * 64 : tile_threads(cfg.bm, cfg.bn);
     if (info != nullptr) {
@@ -511,9 +591,15 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         return DG_OK;
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (a.gemm_type == kMGroupedIdx && !compile_only) {
+        // m_indices layout check: a device kernel that sets the sticky DG_ERR_M_INDICES word
+        // (no host synchronisation; without the words -- a call that may not allocate, before
+        // any other call allocated them -- it is skipped)
+        const int rc = check_m_indices(a.grouped_layout, a.m, a.alignment, a.num_groups, st, !noalloc);
+        if (rc != DG_OK) return rc;
+    }
     if (jit) return jit_run(a, cfg, epi_kind, plan.split, p, grid, st, compile_only);
-    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3((unsigned)threads), 0, st, p);
-    const hipError_t e = hipGetLastError();
+    const hipError_t e = launch_module_kernel(reinterpret_cast<const void*>(fn), (unsigned)grid, (unsigned)threads, p, st);
     if (e != hipSuccess) {
         dg_set_error(hipGetErrorString(e));
         return DG_ELAUNCH;
@@ -524,6 +610,17 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
 }  // namespace
 
 extern "C" int dg_gemm(const dg_gemm_args* args, void* stream) { return gemm_impl(args, stream, false); }
+
+extern "C" int dg_stream_workspace(void* stream, void** ptr, int64_t* bytes) {
+    if (ptr == nullptr || bytes == nullptr) return dg_set_error("dg_stream_workspace: null argument");
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return dg_set_error("dg_stream_workspace: no current HIP device");
+    std::lock_guard<std::mutex> lk(g_stream_ws_mu);
+    auto it = g_stream_ws.find({dev, reinterpret_cast<hipStream_t>(stream)});
+    *ptr = it == g_stream_ws.end() ? nullptr : it->second.ptr;
+    *bytes = it == g_stream_ws.end() ? 0 : it->second.bytes;
+    return DG_OK;
+}
 
 // ---------------------------------------------------------------------------------------------
 // dg_gemm_noalloc: dg_gemm with the split-K workspace taken from a fixed device array instead of
@@ -565,8 +662,9 @@ int scratch_address(void** out) {
 extern "C" int dg_gemm_noalloc(const dg_gemm_args* args, void* stream) {
     if (args == nullptr) return dg_set_error("dg_gemm_noalloc: null args");
     dg_gemm_args a = *args;
-    if (a.workspace != nullptr || a.workspace_bytes != 0)
-        return dg_set_error("dg_gemm_noalloc: the library provides the workspace (pass workspace = NULL, 0 bytes)");
+    if (a.workspace != nullptr || a.workspace_bytes != 0 || a.library_workspace != 0)
+        return dg_set_error("dg_gemm_noalloc: the library provides the workspace (pass workspace = NULL, 0 bytes, "
+                            "library_workspace = 0)");
     int64_t need = 0;
     a.workspace = reinterpret_cast<void*>(1);   // (any non-null value: the plan may then split K)
     int rc = dg_gemm_workspace_size(&a, &need);
@@ -585,7 +683,7 @@ extern "C" int dg_gemm_noalloc(const dg_gemm_args* args, void* stream) {
     if (rc != DG_OK) return rc;
     a.workspace = ptr;
     a.workspace_bytes = kNoAllocScratchBytes;
-    return gemm_impl(&a, stream, false);
+    return gemm_impl(&a, stream, false, nullptr, true);
 }
 
 extern "C" int dg_launch_plan(const dg_gemm_args* args, dg_launch_info* info) {

@@ -494,7 +494,9 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         }
     } else if (gemm_type == kMGroupedIdx) {
         group = __builtin_amdgcn_readfirstlane(p.layout[m0]);
-        if (group < 0) zero_tile = true;
+        // (padding rows, and ids past the last group -- which the m_indices check reports --
+        // read no B)
+        if (group < 0 || group >= p.num_groups) zero_tile = true;
     }
     group = __builtin_amdgcn_readfirstlane(group);
     valid_end = __builtin_amdgcn_readfirstlane(valid_end);

@@ -72,7 +72,9 @@ __device__ __forceinline__ PTile ptile_info(const KParams& p, int v, int gemm_ty
         }
     } else if (gemm_type == kMGroupedIdx) {
         ti.group = lay[ti.m0];
-        if (ti.group < 0) ti.state = kPZero;
+        // (padding rows, and ids past the last group -- which the m_indices check reports --
+        // read no B)
+        if (ti.group < 0 || ti.group >= p.num_groups) ti.state = kPZero;
     }
     ti.m0 = __builtin_amdgcn_readfirstlane(ti.m0);
     ti.n0 = __builtin_amdgcn_readfirstlane(ti.n0);

@@ -1,0 +1,101 @@
+// Sticky error words that kernels set and the host reads without a synchronisation, and the
+// m_indices layout check of M-grouped GEMMs.
+//
+// The reference stops on a device-side assertion when a float32 scale factor carries sign or
+// mantissa bits (deep_gemm/include/deep_gemm/transform_sf.hpp:13-21).  Here the kernel that meets
+// such an input stores 1 into a word of host-mapped pinned memory; the host API reads (and clears)
+// the words at its next call and raises there, so the check costs no stream synchronisation and
+// no memcpy node inside a captured graph (the kernels write through a fixed host-mapped pointer).
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/deep_gemm_amd.h"
+
+extern "C" __attribute__((visibility("hidden"))) int dg_set_error(const char* msg);
+
+namespace dg {
+
+// words[i] != 0: error i happened (DG_ERR_* bit i) since the last dg_take_errors()
+constexpr int kNumStatusWords = 2;
+
+namespace {
+std::once_flag g_status_once;
+uint32_t* g_status_host = nullptr;     // host view of the pinned words
+std::atomic<uint32_t*> g_status_dev{nullptr};   // device view (same memory)
+
+void status_alloc() {
+    void* h = nullptr;
+    if (hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent) != hipSuccess ||
+        h == nullptr) {
+        (void)hipGetLastError();
+        return;
+    }
+    void* d = nullptr;
+    if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess || d == nullptr) {
+        (void)hipGetLastError();
+        return;
+    }
+    std::memset(h, 0, 64);
+    g_status_host = static_cast<uint32_t*>(h);
+    g_status_dev.store(static_cast<uint32_t*>(d), std::memory_order_release);
+}
+}  // namespace
+
+// Device address of the status words (allocated on the first call; nullptr if the pinned
+// allocation failed, and then kernels skip the checks that report through it).
+uint32_t* status_words() {
+    std::call_once(g_status_once, status_alloc);
+    return g_status_dev.load(std::memory_order_acquire);
+}
+
+// The same, without allocating: nullptr until some call has allocated the words.
+uint32_t* status_words_if_ready() {
+    return g_status_dev.load(std::memory_order_acquire);
+}
+
+// m_indices of an M-grouped contiguous GEMM: every `alignment`-row block must hold one group id
+// (0 <= id < num_groups) on a prefix of its rows and padding (< 0) on the rest -- the layout the
+// grouped kernel's per-tile group lookup relies on.  Thread r checks row r against row r - 1.
+__global__ __launch_bounds__(256) void check_m_indices_kernel(const int32_t* idx, int m, int alignment,
+                                                              int num_groups, uint32_t* status) {
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= m) return;
+    const int v = idx[r];
+    bool bad = v >= num_groups;
+    if (v >= 0 && r % alignment != 0) bad = bad || idx[r - 1] != v;
+    if (bad) status[1] = 1u;
+}
+
+int check_m_indices(const int32_t* idx, int m, int alignment, int num_groups, hipStream_t st, bool may_alloc) {
+    uint32_t* status = may_alloc ? status_words() : status_words_if_ready();
+    if (status == nullptr || m <= 0) return DG_OK;
+    hipLaunchKernelGGL(check_m_indices_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, idx, m, alignment,
+                       num_groups, status);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        dg_set_error(hipGetErrorString(e));
+        return DG_ELAUNCH;
+    }
+    return DG_OK;
+}
+
+}  // namespace dg
+
+extern "C" uint32_t dg_take_errors(void) {
+    // (no allocation: before any call has allocated the words there is nothing to report)
+    if (dg::status_words_if_ready() == nullptr) return 0;
+    uint32_t bits = 0;
+    for (int i = 0; i < dg::kNumStatusWords; ++i) {
+        auto* w = reinterpret_cast<std::atomic<uint32_t>*>(dg::g_status_host + i);
+        if (w->exchange(0u, std::memory_order_acq_rel) != 0u) bits |= 1u << i;
+    }
+    return bits;
+}
+
+extern "C" const uint32_t* dg_error_words(void) {
+    dg::status_words();
+    return dg::g_status_host;
+}

@@ -41,6 +41,14 @@ __device__ __forceinline__ bool psum_is_padding(const SfParams& p, int i, int gr
     return i >= ceil_div(p.psum[lo], gran);
 }
 
+// Is SF row i of an M-grouped operand padding?  num_groups >= 1: the psum layout above; -1: `psum`
+// holds the m_indices of the rows (gran_mn 1), a negative index marking a padding row.
+__device__ __forceinline__ bool mn_is_padding(const SfParams& p, int i) {
+    if (p.psum == nullptr) return false;
+    if (p.num_groups < 0) return p.psum[i] < 0;
+    return psum_is_padding(p, i, p.gran_mn);
+}
+
 // kKGrouped: the psum layout splits K (csrc/apis/layout.hpp:94-111): SF of the K padding between
 // groups (fp32 per gran_k column, packed int16 per 64-wide column) becomes 0 and is not validated.
 // Grid: x walks the MN axis, y the 64-wide K columns (KPB per workgroup), z the batches, so a
@@ -96,7 +104,7 @@ __global__ __launch_bounds__(256) void transform_sf_kernel(const SfParams p) {
         } else {
             const int mn = mn0;
             const int i = mn / p.gran_mn;
-            const bool mn_pad = !kKGrouped && p.psum != nullptr && psum_is_padding(p, i, p.gran_mn);
+            const bool mn_pad = !kKGrouped && i < p.sf_mn && mn_is_padding(p, i);
             if (mn < p.mn && i < p.sf_mn && !mn_pad) {
                 const int64_t row_off = (int64_t)b * p.stride_b + (int64_t)i * p.stride_mn;
                 if constexpr (kFloat) {
@@ -144,7 +152,7 @@ __global__ __launch_bounds__(256) void transform_sf_kmajor_kernel(const SfParams
     const int b = blockIdx.z, kbase = blockIdx.y * kSfKPBK;
     if (mn >= p.ld) return;
     const int i = mn / p.gran_mn;
-    const bool mn_pad = !kKGrouped && p.psum != nullptr && psum_is_padding(p, i, p.gran_mn);
+    const bool mn_pad = !kKGrouped && i < p.sf_mn && mn_is_padding(p, i);
     const bool row_ok = mn < p.mn && i < p.sf_mn && !mn_pad;
     const int per = p.gran_k == 128 ? 4 : 1;   // 32-wide K blocks per source float
     const int j0 = 2 * kbase / per;            // first source float of the span
@@ -190,6 +198,9 @@ __global__ __launch_bounds__(256) void transform_sf_kmajor_kernel(const SfParams
 }  // namespace dg
 
 extern "C" __attribute__((visibility("hidden"))) int dg_set_error(const char* msg);
+namespace dg {
+uint32_t* status_words();
+}
 
 static int transform_sf_impl(bool k_grouped, const void* src, int32_t src_kind, int64_t stride_b, int64_t stride_mn,
                              int64_t stride_k, int32_t num_batches, int32_t sf_mn, int32_t sf_k,
@@ -214,7 +225,9 @@ static int transform_sf_impl(bool k_grouped, const void* src, int32_t src_kind, 
     if (sf_mn != ceil_div(mn, gran_mn)) return dg_set_error("dg_transform_sf: sf_mn != ceil(MN / gran_mn)");
     if (num_batches > 1 && dst_stride_b < (int64_t)ceil_div(k, 64) * align_up(mn, 2))
         return dg_set_error("dg_transform_sf: dst batch stride smaller than ceil(K / 64) * align(MN, 2)");
-    if (!k_grouped && psum != nullptr && (num_groups < 1 || alignment < 1 || alignment % gran_mn != 0))
+    if (!k_grouped && psum != nullptr && num_groups == -1 && (gran_mn != 1 || num_batches != 1))
+        return dg_set_error("dg_transform_sf: an m_indices layout needs gran_mn == 1 and one batch");
+    if (!k_grouped && psum != nullptr && num_groups != -1 && (num_groups < 1 || alignment < 1 || alignment % gran_mn != 0))
         return dg_set_error("dg_transform_sf: psum needs num_groups >= 1 and alignment % gran_mn == 0");
     if (k_grouped && (psum == nullptr || num_groups < 1 || num_batches != 1 || alignment < 64 || alignment % 64 != 0))
         return dg_set_error("dg_transform_k_grouped_sf: needs a psum layout, one batch and alignment % 64 == 0");
@@ -224,7 +237,10 @@ static int transform_sf_impl(bool k_grouped, const void* src, int32_t src_kind, 
     p.num_batches = num_batches; p.sf_mn = sf_mn; p.sf_k = sf_k; p.mn = mn; p.ld = align_up(mn, 2);
     p.k64 = ceil_div(k, 64); p.k32 = ceil_div(k, 32); p.gran_mn = gran_mn; p.gran_k = gran_k;
     p.psum = psum; p.num_groups = num_groups; p.alignment = alignment;
-    p.dst = dst; p.dst_stride_b = dst_stride_b; p.err = err_flag;
+    p.dst = dst; p.dst_stride_b = dst_stride_b;
+    // (without a caller's flag, invalid SFs set the library's sticky error word, which the host
+    // API reads at its next call)
+    p.err = err_flag != nullptr ? err_flag : reinterpret_cast<int32_t*>(dg::status_words());
     if ((int64_t)p.k64 * p.ld * num_batches == 0) return DG_OK;
     if (ceil_div(p.k64, 2) > 65535 || num_batches > 65535)
         return dg_set_error("dg_transform_sf: K or batch count too large");

@@ -23,7 +23,11 @@ DG_COMPILED_M, DG_COMPILED_N, DG_COMPILED_K = 1, 2, 4
 # Every symbol include/deep_gemm_amd.h declares.
 EXPORTED_SYMBOLS = ('dg_gemm', 'dg_transform_sf', 'dg_transform_k_grouped_sf', 'dg_transpose_to_k_major', 'dg_device_num_cus', 'dg_select_config',
                     'dg_gemm_workspace_size', 'dg_last_error', 'dg_version', 'dg_jit_compile', 'dg_jit_set_include_dir',
-                    'dg_jit_stats', 'dg_launch_plan', 'dg_gemm_noalloc')
+                    'dg_jit_stats', 'dg_launch_plan', 'dg_gemm_noalloc', 'dg_take_errors', 'dg_error_words',
+                    'dg_stream_workspace')
+
+# Sticky error bits kernels report through host-mapped words (DG_ERR_* in the header)
+DG_ERR_SF_INVALID, DG_ERR_M_INDICES = 1, 2
 
 
 class GemmArgs(ctypes.Structure):
@@ -43,7 +47,7 @@ class GemmArgs(ctypes.Structure):
         ('num_cus', ctypes.c_int32), ('split_k', ctypes.c_int32),
         ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_int64),
         ('epilogue', ctypes.c_int32), ('sfd', ctypes.c_void_p), ('sfd_ld', ctypes.c_int64),
-        ('jit', ctypes.c_int32), ('compiled_dims', ctypes.c_int32),
+        ('jit', ctypes.c_int32), ('compiled_dims', ctypes.c_int32), ('library_workspace', ctypes.c_int32),
     ]
 
 
@@ -113,11 +117,70 @@ def load(path=None) -> ctypes.CDLL:
         lib.dg_jit_stats.restype = ctypes.c_int
         # kernel headers the run-time compiler reads: csrc/ beside this package
         lib.dg_jit_set_include_dir(str(Path(__file__).resolve().parent.parent / 'csrc').encode())
+        lib.dg_stream_workspace.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int64)]
+        lib.dg_stream_workspace.restype = ctypes.c_int
+        lib.dg_take_errors.restype = ctypes.c_uint32
+        lib.dg_take_errors.argtypes = []
+        lib.dg_error_words.restype = ctypes.c_void_p
+        lib.dg_error_words.argtypes = []
         lib.dg_last_error.restype = ctypes.c_char_p
         lib.dg_version.restype = ctypes.c_char_p
         if path is None:
             _lib = lib
         return lib
+
+
+def error_message(bits: int) -> str:
+    """Text of the sticky error bits (the C++ host path words it the same way, csrc/torch_ext.cpp)."""
+    parts = []
+    if bits & DG_ERR_SF_INVALID:
+        parts.append('Invalid float32 SF: only the 8-bit exponent may be set (sign and mantissa must be 0)')
+    if bits & DG_ERR_M_INDICES:
+        parts.append('m_indices is not padded to the M-grouped alignment (every alignment-row block must hold one '
+                     'group id < num_groups followed only by -1 padding)')
+    return '; '.join(parts) + ' [reported by a kernel of an earlier deep_gemm call]'
+
+
+def raise_pending() -> None:
+    """Raise the errors kernels of earlier calls reported (no synchronisation: what has not
+    completed yet is reported by a later call)."""
+    if _lib is None:
+        return
+    bits = _lib.dg_take_errors()
+    if bits:
+        raise RuntimeError(error_message(bits))
+
+
+_EXT_NAME = 'deep_gemm_C'
+_ext = None
+_ext_tried = False
+
+
+def ext():
+    """The C++ host-path extension (deep_gemm_C.so beside this file), bound to the loaded
+    library's entry points; None when it has not been built (the Python path then serves every
+    call)."""
+    global _ext, _ext_tried
+    if _ext_tried:
+        return _ext
+    lib = load()
+    with _lock:
+        if _ext_tried:
+            return _ext
+        path = Path(__file__).resolve().parent / f'{_EXT_NAME}.so'
+        mod = None
+        if path.exists() and not os.environ.get('DG_DISABLE_EXT'):
+            import importlib.util
+            import torch  # noqa: F401  (the extension links torch's libraries)
+            spec = importlib.util.spec_from_file_location(_EXT_NAME, str(path))
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+            addr = lambda f: ctypes.cast(f, ctypes.c_void_p).value
+            mod.init(addr(lib.dg_gemm), addr(lib.dg_transform_sf), addr(lib.dg_take_errors), addr(lib.dg_last_error),
+                     lib.dg_error_words() or 0)
+        _ext = mod
+        _ext_tried = True
+        return _ext
 
 
 def jit_stats(lib=None):

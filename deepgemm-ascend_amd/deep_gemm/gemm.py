@@ -20,6 +20,7 @@ import torch
 from . import _lib
 from . import epilogue as _epi
 from .layout import (transform_sf_into_required_layout, transform_k_grouped_sf_into_required_layout, get_recipe,
+                     transform_sf_rows,
                      operand_recipes, _assert)
 from .runtime import get_num_sms, get_mk_alignment_for_contiguous_layout, get_dry_run, get_jit
 
@@ -129,23 +130,53 @@ def _kind(a: torch.Tensor, b: torch.Tensor) -> int:
     raise RuntimeError('Unsupported operand dtypes')
 
 
-# Split-K workspaces, one per (device, stream): zero-filled at allocation and left zero-filled by
-# every launch, so back-to-back launches on one stream share it.
-_workspaces = {}
-_ws_lock = threading.Lock()
+# The C++ host path (csrc/torch_ext.cpp) serves the common calls: K-major aligned operands, no
+# bias, alpha or output epilogue, no dry run, JIT or tuning override.  It returns False for
+# anything else, and the Python path below then runs (and raises the reference's errors).
+_OVERRIDES = ('DG_SPLIT_K', 'DG_FORCE_BLOCK', 'DG_CHECK_SF')
+_recipe_cache = {}
 
 
-def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    key = (device.index, stream)
-    with _ws_lock:
-        ws = _workspaces.get(key)
-        if ws is None or ws.numel() < nbytes:
-            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-            _workspaces[key] = ws
-        return ws
+def _fast():
+    """The extension when the fast path may serve this call, else None."""
+    from . import runtime as _rt
+    if _rt._dry_run or _rt._jit:
+        return None
+    env = os.environ
+    for key in _OVERRIDES:
+        if key in env:
+            return None
+    return _lib.ext()
+
+
+def _fast_recipes(recipe, recipe_a, recipe_b):
+    """operand_recipes flattened to (gran_a_mn, gran_a_k, gran_b_mn, gran_b_k), memoised."""
+    key = (recipe, recipe_a, recipe_b)
+    try:
+        hit = _recipe_cache.get(key)
+    except TypeError:   # (unhashable recipe lists)
+        (ga, ka), (gb, kb) = operand_recipes(recipe, recipe_a, recipe_b)
+        return ga, ka, gb, kb
+    if hit is None:
+        (ga, ka), (gb, kb) = operand_recipes(recipe, recipe_a, recipe_b)
+        hit = _recipe_cache[key] = (ga, ka, gb, kb)
+    return hit
+
+
+def _fast_gemm(gemm_type, a, sfa, b, sfb, d, c, layout, recipes) -> bool:
+    if not d.is_cuda:
+        return False
+    ext = _fast()
+    if ext is None:
+        return False
+    from . import runtime as _rt
+    ga, ka, gb, kb = recipes
+    return ext.gemm(gemm_type, a, sfa, b, sfb, d, c, layout, ga, ka, gb, kb, _rt._num_sms, _rt._mk_alignment,
+                    _stream(d))
 
 
 def _launch(args: _lib.GemmArgs, d: torch.Tensor) -> None:
+    _lib.raise_pending()
     if get_dry_run():
         # the reference's dry run compiles the kernel without loading or launching it
         # (csrc/jit_kernels/fp8_gemm.hpp:75-78); ahead-of-time kernels need nothing
@@ -159,11 +190,9 @@ def _launch(args: _lib.GemmArgs, d: torch.Tensor) -> None:
     if forced:
         args.split_k = int(forced)
     if args.gemm_type in (_lib.DG_GEMM_NORMAL, _lib.DG_GEMM_BATCHED) and args.split_k != 1:
-        nbytes = ctypes.c_int64(0)
-        _lib.check(lib.dg_gemm_workspace_size(args, ctypes.byref(nbytes)), lib)
-        if nbytes.value > 0:
-            ws = _workspace(d.device, stream, nbytes.value)
-            args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+        # split-K partials and tile counters go to the library's workspace of this stream (grown
+        # only outside graph capture, never freed)
+        args.library_workspace = 1
     _lib.check(lib.dg_gemm(args, stream), lib)
 
 
@@ -296,6 +325,9 @@ def _make_fp8_fp4_gemm(trans_a: bool, trans_b: bool, default_dims: str):
            compiled_dims: str = default_dims, disable_ue8m0_cast: bool = False,
            alpha: Optional[float] = None, epilogue=None) -> None:
         (a_, sfa), (b_, sfb) = a, b
+        if not (trans_a or trans_b) and alpha is None and epilogue is None and not disable_ue8m0_cast and \
+                _fast_gemm(0, a_, sfa, b_, sfb, d, c, None, _fast_recipes(recipe, recipe_a, recipe_b)):
+            return
         if trans_a:
             a_, sfa = a_.transpose(0, 1), sfa.transpose(0, 1)
         if trans_b:
@@ -318,6 +350,9 @@ for _f, _name in ((fp8_fp4_gemm_nt, 'nt'), (fp8_fp4_gemm_nn, 'nn'), (fp8_fp4_gem
 def _make_bf16_gemm(trans_a: bool, trans_b: bool, default_dims: str):
     def fn(a: torch.Tensor, b: torch.Tensor, d: torch.Tensor, c: Optional[torch.Tensor] = None,
            compiled_dims: str = default_dims, alpha: Optional[float] = None, epilogue=None) -> None:
+        if not (trans_a or trans_b) and alpha is None and epilogue is None and \
+                _fast_gemm(0, a, None, b, None, d, c, None, (0, 0, 0, 0)):
+            return
         a_ = a.transpose(0, 1) if trans_a else a
         b_ = b.transpose(0, 1) if trans_b else b
         _dense_gemm(a_, None, b_, None, d, c, None, None, None, False, alpha, epilogue, bf16=True, dims=compiled_dims)
@@ -369,8 +404,9 @@ def _grouped_contiguous(a, sfa, b, sfb, d, grouped_layout, recipe, recipe_a, rec
     else:
         kind = _kind(a, b)
         ra, rb = operand_recipes(recipe, recipe_a, recipe_b)
-        sfa_t = transform_sf_into_required_layout(sfa, m, k, ra, None, True, disable_ue8m0_cast,
-                                                  grouped_layout if use_psum_layout else None)
+        sfa_t = transform_sf_rows(sfa, m, k, ra, None, True, disable_ue8m0_cast,
+                                  grouped_layout if use_psum_layout else None,
+                                  None if use_psum_layout else grouped_layout)
         sfb_t = transform_sf_into_required_layout(sfb, n, k, rb, g, False, disable_ue8m0_cast)
         args.sfa, args.sfb = sfa_t.data_ptr(), sfb_t.data_ptr()
         args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
@@ -396,6 +432,10 @@ def _make_m_grouped_fp8_fp4(trans_b: bool):
            disable_ue8m0_cast: bool = False, use_psum_layout: bool = True, ensure_zero_padding: bool = True,
            expected_m_for_psum_layout: Optional[int] = None, epilogue=None) -> None:
         (a_, sfa), (b_, sfb) = a, b
+        if not trans_b and epilogue is None and not disable_ue8m0_cast and \
+                _fast_gemm(2 if use_psum_layout else 3, a_, sfa, b_, sfb, d, None, grouped_layout,
+                           _fast_recipes(recipe, recipe_a, recipe_b)):
+            return
         if trans_b:
             b_, sfb = b_.transpose(1, 2), sfb.transpose(1, 2)
         _grouped_contiguous(a_, sfa, b_, sfb, d, grouped_layout, recipe, recipe_a, recipe_b, disable_ue8m0_cast,
@@ -413,6 +453,9 @@ def _make_m_grouped_bf16(trans_b: bool):
     def fn(a, b, d, grouped_layout, compiled_dims: str = 'nk', use_psum_layout: bool = True,
            ensure_zero_padding: bool = True, expected_m_for_psum_layout: Optional[int] = None,
            epilogue=None) -> None:
+        if not trans_b and epilogue is None and \
+                _fast_gemm(2 if use_psum_layout else 3, a, None, b, None, d, None, grouped_layout, (0, 0, 0, 0)):
+            return
         b_ = b.transpose(1, 2) if trans_b else b
         _grouped_contiguous(a, None, b_, None, d, grouped_layout, None, None, None, False, use_psum_layout,
                             epilogue, bf16=True, dims=compiled_dims)
@@ -468,11 +511,16 @@ def m_grouped_fp8_fp4_gemm_nt_masked(a, b, d, masked_m: torch.Tensor, expected_m
                                      recipe_a=None, recipe_b=None, compiled_dims: str = 'nk',
                                      disable_ue8m0_cast: bool = False) -> None:
     (a_, sfa), (b_, sfb) = a, b
+    if not disable_ue8m0_cast and _fast_gemm(4, a_, sfa, b_, sfb, d, None, masked_m,
+                                             _fast_recipes(recipe, recipe_a, recipe_b)):
+        return
     _masked(a_, sfa, b_, sfb, d, masked_m, recipe, recipe_a, recipe_b, disable_ue8m0_cast, bf16=False, dims=compiled_dims)
 
 
 def m_grouped_bf16_gemm_nt_masked(a, b, d, masked_m: torch.Tensor, expected_m: int,
                                   compiled_dims: str = 'nk') -> None:
+    if _fast_gemm(4, a, None, b, None, d, None, masked_m, (0, 0, 0, 0)):
+        return
     _masked(a, None, b, None, d, masked_m, None, None, None, False, bf16=True, dims=compiled_dims)
 
 
@@ -664,6 +712,8 @@ def launch_plan(m: int, n: int, k: int, kind: int = _lib.DG_KIND_FP8_FP8, gemm_t
     args.sfa_batch_stride, args.sfb_batch_stride = args.sfa_ld * nk64, args.sfb_ld * nk64
     args.alignment = get_mk_alignment_for_contiguous_layout()
     args.num_cus = get_num_sms()
+    # (dense and batched calls may split K into the library's per-stream workspace)
+    args.library_workspace = 1 if gemm_type in (_lib.DG_GEMM_NORMAL, _lib.DG_GEMM_BATCHED) else 0
     info = _lib.LaunchInfo()
     lib = _lib.load()
     _lib.check(lib.dg_launch_plan(args, ctypes.byref(info)), lib)

@@ -61,7 +61,7 @@ def check_sf_layout(sf: torch.Tensor, mn: int, k: int, gran_mn: int, gran_k: int
 
 
 def _launch_transform_sf(sf: torch.Tensor, mn: int, k: int, gran_mn: int, gran_k: int,
-                         psum: Optional[torch.Tensor]) -> torch.Tensor:
+                         psum: Optional[torch.Tensor], m_indices: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The reference's launch_transform_sf (csrc/jit_kernels/transform_sf.hpp:15-105)."""
     squeeze = sf.dim() == 2
     if squeeze:
@@ -78,6 +78,10 @@ def _launch_transform_sf(sf: torch.Tensor, mn: int, k: int, gran_mn: int, gran_k
                 'grouped_layout must be a contiguous 1D int32 tensor')
         num_groups = psum.numel()
         _assert(num_groups > 0, 'grouped_layout must contain at least one group')
+    rows_layout = psum
+    if m_indices is not None and psum is None and num_batches == 1 and gran_mn == 1:
+        # padding rows (negative m_indices) are neither read nor validated
+        rows_layout, num_groups = m_indices, -1
     k64 = _ceil_div(k, 64)
     # MN axis padded to an even leading dimension (the GEMM kernels fetch SF rows in pairs)
     ld = _align(mn, 2)
@@ -90,7 +94,7 @@ def _launch_transform_sf(sf: torch.Tensor, mn: int, k: int, gran_mn: int, gran_k
     rc = lib.dg_transform_sf(
         sf.data_ptr(), _lib.DG_SF_F32 if sf.dtype == torch.float32 else _lib.DG_SF_I16,
         sf.stride(0), sf.stride(1), sf.stride(2), num_batches, sf_mn, sf_k, mn, k, gran_mn, gran_k,
-        psum.data_ptr() if psum is not None else None, num_groups, alignment,
+        rows_layout.data_ptr() if rows_layout is not None else None, num_groups, alignment,
         out.data_ptr(), k64 * ld, err.data_ptr() if err is not None else None,
         torch.cuda.current_stream(sf.device).cuda_stream)
     _lib.check(rc, lib)
@@ -110,6 +114,12 @@ def transform_sf_into_required_layout(sf: torch.Tensor, mn: int, k: int, recipe,
                                       disable_ue8m0_cast: bool = False,
                                       psum_layout: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Same contract as the reference (csrc/apis/layout.hpp:68-92, bound at :131-137)."""
+    return transform_sf_rows(sf, mn, k, recipe, num_groups, is_sfa, disable_ue8m0_cast, psum_layout)
+
+
+def transform_sf_rows(sf, mn, k, recipe, num_groups, is_sfa, disable_ue8m0_cast, psum_layout=None, m_indices=None):
+    """transform_sf_into_required_layout, plus an m_indices layout of an M-grouped A (its padding
+    rows, negative indices, are neither read nor validated)."""
     _assert(is_sfa is not None, 'is_sfa must be set')
     gran_mn, gran_k = _split_recipe(recipe, is_sfa)
     if check_sf_layout(sf, mn, k, gran_mn, gran_k, num_groups):
@@ -117,7 +127,7 @@ def transform_sf_into_required_layout(sf: torch.Tensor, mn: int, k: int, recipe,
     if sf.dtype == torch.float32:
         _assert(not disable_ue8m0_cast,
                 'Float32 SF must be converted into ue8m0, but disable_ue8m0_cast is set true')
-    return _launch_transform_sf(sf, mn, k, gran_mn, gran_k, psum_layout)
+    return _launch_transform_sf(sf, mn, k, gran_mn, gran_k, psum_layout, m_indices)
 
 
 def transform_k_grouped_sf_into_required_layout(sf: torch.Tensor, mn: int, k: int, recipe, is_sfa: Optional[bool],

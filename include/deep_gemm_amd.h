@@ -108,6 +108,11 @@ typedef struct dg_gemm_args {
     int32_t compiled_dims;        /* jit only: DG_COMPILED_* sizes fixed at compile time (the
                                      reference's compiled_dims, csrc/jit_kernels/fp8_gemm.hpp:
                                      42-44); the GEMM type and K split always are              */
+    int32_t library_workspace;    /* 1 (with workspace = NULL): a split-K plan takes its workspace
+                                     from the library, one per (device, stream), allocated on first
+                                     need, zero-filled, only ever grown and never freed (a captured
+                                     graph may hold it).  Growing it while the stream is being
+                                     captured is an error: run the call once before the capture. */
 } dg_gemm_args;
 
 #define DG_COMPILED_M 1
@@ -143,8 +148,11 @@ int dg_jit_stats(int64_t *compiled, int64_t *disk_hits, int64_t *memory_hits);
  * gran_k: 32 or 128 for DG_SF_F32 (128 repeats each exponent over four 32-blocks), 32 for I16.
  * psum (optional, device int32[num_groups]): M-grouped padding rows
  *      [ceil(psum[g]/gran_mn), align(psum[g], alignment)/gran_mn) (in SF rows) become 0.
+ *      With num_groups = -1 it is instead the m_indices of the mn rows (gran_mn 1, one batch):
+ *      rows with a negative index are padding and become 0.  Padding SF rows are not validated.
  * err_flag (optional, device int32): set to 1 when an fp32 SF has sign or mantissa bits
- *      (the reference traps on this, deep_gemm/include/deep_gemm/transform_sf.hpp:13-21).
+ *      (the reference traps on this, deep_gemm/include/deep_gemm/transform_sf.hpp:13-21);
+ *      NULL: the library's sticky DG_ERR_SF_INVALID word is set instead (dg_take_errors).
  */
 int dg_transform_sf(const void *src, int32_t src_kind, int64_t stride_b, int64_t stride_mn,
                     int64_t stride_k, int32_t num_batches, int32_t sf_mn, int32_t sf_k,
@@ -200,6 +208,25 @@ int dg_gemm_workspace_size(const dg_gemm_args *args, int64_t *bytes);
  * overlap in time on one device (different streams) race; calls issued in order on one stream do
  * not (each launch leaves the counters zero for the next). */
 int dg_gemm_noalloc(const dg_gemm_args *args, void *stream);
+
+/* Sticky error words (no counterpart in the reference, which stops on a device-side assertion:
+ * deep_gemm/include/deep_gemm/transform_sf.hpp:13-21).  Kernels that meet invalid input set a
+ * word of host-mapped pinned memory instead of trapping; the host reads the words without any
+ * stream synchronisation.
+ *   DG_ERR_SF_INVALID  a float32 SF given to dg_transform_sf / dg_transform_k_grouped_sf (with
+ *                      err_flag = NULL) had sign or mantissa bits set;
+ *   DG_ERR_M_INDICES   an M-grouped m_indices layout (DG_GEMM_MGROUPED_IDX) was not padded to
+ *                      `alignment`: some alignment-row block mixed two group ids, had a group id
+ *                      after a padding row, or held an id >= num_groups.
+ * dg_take_errors returns the DG_ERR_* bits set by kernels that completed since the last call and
+ * clears them.  dg_error_words returns the host address of the words (word i != 0: bit i). */
+#define DG_ERR_SF_INVALID 1u
+#define DG_ERR_M_INDICES 2u
+/* The split-K workspace the library holds for (current device, stream) -- see library_workspace in
+ * dg_gemm_args -- or NULL / 0 before a call needed one.  Nothing is allocated (inspection). */
+int dg_stream_workspace(void *stream, void **ptr, int64_t *bytes);
+uint32_t dg_take_errors(void);
+const uint32_t *dg_error_words(void);
 
 /* Tile shape dg_gemm() would pick for `args` (block_m, block_n written to the pointers). */
 int dg_select_config(const dg_gemm_args *args, int32_t *block_m, int32_t *block_n);

@@ -26,7 +26,7 @@ def lib():
 
 def _declared_symbols():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r'^\s*(?:int|const char \*)\s*(dg_\w+)\s*\(', text, re.M)))
+    return sorted(set(re.findall(r'^\s*(?:int|uint32_t|const char \*|const uint32_t \*)\s*(dg_\w+)\s*\(', text, re.M)))
 
 
 def test_header_declares_the_binding_table():
@@ -128,3 +128,25 @@ def test_launch_plan_without_device(lib):
     assert lib.dg_launch_plan(_plan_args(1, 2112, 7168, 64), ctypes.byref(small)) == 0, lib.dg_last_error()
     assert small.skinny == 1 and small.persistent == 0
     assert lib.dg_launch_plan(None, None) == -1
+
+
+def test_error_words_and_stream_workspace_without_device(lib):
+    # no kernel has run: nothing pending; the workspace query rejects null outputs
+    assert lib.dg_take_errors() == 0
+    assert lib.dg_stream_workspace(None, None, None) == -1
+    assert b'null argument' in lib.dg_last_error()
+
+
+def test_error_message_words():
+    msg = _lib.error_message(_lib.DG_ERR_SF_INVALID | _lib.DG_ERR_M_INDICES)
+    assert 'Invalid float32 SF' in msg and 'm_indices is not padded' in msg
+
+
+def test_host_extension_loads_and_binds(lib):
+    """The C++ host path (deep_gemm_C.so) imports and takes the library's entry points; with no
+    device the error words are unavailable and it still binds."""
+    path = Path(_lib.__file__).resolve().parent / 'deep_gemm_C.so'
+    if not path.exists():
+        pytest.skip('host extension not built')
+    mod = _lib.ext()
+    assert mod is not None and hasattr(mod, 'gemm') and hasattr(mod, 'init')

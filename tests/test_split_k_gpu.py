@@ -8,7 +8,6 @@ import pytest
 import torch
 
 import deep_gemm
-from deep_gemm import gemm as dg_gemm
 from oracle import gemm as og
 from helpers import gen, operand, calc_diff
 
@@ -48,7 +47,14 @@ def _counters_zero(m, n, k, kind=0):
     _lib.check(lib.dg_select_config(ctypes.byref(args), ctypes.byref(bm), ctypes.byref(bn)), lib)
     tiles = -(-m // bm.value) * -(-n // bn.value)
     nbytes = -(-tiles * 4 // 256) * 256
-    return all(int(ws[:nbytes].count_nonzero()) == 0 for ws in dg_gemm._workspaces.values())
+    ptr, size = ctypes.c_void_p(), ctypes.c_int64()
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.dg_stream_workspace(stream, ctypes.byref(ptr), ctypes.byref(size)), lib)
+    assert ptr.value and size.value >= nbytes
+    host = (ctypes.c_uint8 * nbytes)()
+    hip = ctypes.CDLL('libamdhip64.so')
+    assert hip.hipMemcpy(host, ptr, ctypes.c_size_t(nbytes), 2) == 0   # hipMemcpyDeviceToHost
+    return not any(host)
 
 
 @pytest.mark.parametrize('split', [2, 3, 5, 8])
