@@ -575,6 +575,9 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     p.split_stages = plan.split_stages;
     p.num_tiles = (int)tiles;
     if (plan.split > 1) {
+        // DG_SPLIT_SPREAD=1 (test knob): the splits of a tile run on different XCDs
+        const char* spread = std::getenv("DG_SPLIT_SPREAD");
+        p.split_spread = spread != nullptr && spread[0] == '1';
         p.counters = reinterpret_cast<int*>(workspace);
         p.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + kCounterBytes);
     }

@@ -57,6 +57,7 @@ struct KParams {
     int num_tiles;             // tiles of the launch (split-K grids are padded past it)
     float* ws;
     int* counters;
+    int split_spread;          // test knob: the splits of a tile go to consecutive workgroups (other XCDs)
     // FP8 output: per-(row, 32 columns) UE8M0 exponents, packed in pairs into int16
     // sfd[(batch * n + col) / 64 * sfd_ld + row], lower byte = the even 32-column block.
     uint8_t* sfd;
@@ -427,6 +428,11 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         const int b = blockIdx.x, r = b >> 3;
         t = (r / split_k) * 8 + (b & 7);
         split = r % split_k;
+        if (p.split_spread) {
+            // (test knob: consecutive workgroups -- different XCDs -- take the splits of a tile)
+            t = b / split_k;
+            split = b % split_k;
+        }
         if (t >= p.num_tiles) return;
     } else {
         t = xcd_remap(blockIdx.x, gridDim.x);
@@ -838,7 +844,15 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         // coherently on every XCD), so once every wave's stores are acknowledged they are
         // visible to whichever workgroup reduces, on whichever XCD, and no fence (an L2
         // writeback or invalidate) is needed.  The "memory" clobber keeps the compiler from
-        // sinking the stores past the wait.
+        // sinking the stores past the wait.  This follows the GFX942 code sequences of the LLVM
+        // AMDGPU memory model (llvm/docs/AMDGPUUsage.rst, "Memory Model GFX942", which gfx950
+        // shares): a monotonic agent-scope atomic store or load is a plain buffer store / load
+        // with sc1 set, so these partial stores and loads are relaxed agent-scope atomics; an
+        // agent-scope release is "buffer_wbl2 sc1=1; s_waitcnt vmcnt(0)", whose L2 writeback
+        // serves only non-atomic data, so the vmcnt(0) before the counter's fetch-add is the whole
+        // release here; the acquire's "buffer_inv sc1=1" likewise serves only non-atomic loads,
+        // so the reducing workgroup's sc1 loads need none.  (tests/test_split_k_gpu.py forces the
+        // splits of one tile onto different XCDs to keep this checked.)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         int* flag = reinterpret_cast<int*>(smem);

@@ -92,6 +92,11 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
         const int b = blockIdx.x, rr = b >> 3;
         t = (rr / split_k) * 8 + (b & 7);
         split = rr % split_k;
+        if (p.split_spread) {
+            // (test knob: consecutive workgroups -- different XCDs -- take the splits of a strip)
+            t = b / split_k;
+            split = b % split_k;
+        }
         if (t >= p.num_tiles) return;
     } else {
         t = blockIdx.x;
@@ -371,7 +376,16 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
             }
         // Arrival count.  The partials were stored at device scope, so once every wave's stores
         // are acknowledged they are visible on every XCD; no fence (which would write back or
-        // invalidate the whole L2) is needed on either side.
+        // invalidate the whole L2) is needed on either side.  This follows the GFX942 code
+        // sequences of the LLVM AMDGPU memory model (llvm/docs/AMDGPUUsage.rst, "Memory Model
+        // GFX942", which gfx950 shares): a monotonic agent-scope atomic store or load is a plain
+        // buffer store / load with sc1 set, so the partial stores and loads here are relaxed
+        // agent-scope atomics; a release at agent scope is "buffer_wbl2 sc1=1; s_waitcnt vmcnt(0)",
+        // where the L2 writeback serves only non-atomic data, so for these stores the vmcnt(0)
+        // before the counter's fetch-add is the whole release; an acquire is "buffer_inv sc1=1"
+        // after the atomic, which again serves only non-atomic loads, so the sc1 loads of the
+        // last workgroup need no invalidate.  (tests/test_split_k_gpu.py forces the splits of
+        // one tile onto different XCDs to keep this checked.)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         int* flag = reinterpret_cast<int*>(red);

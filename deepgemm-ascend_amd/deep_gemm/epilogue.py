@@ -50,11 +50,6 @@ class BF16StochasticRounding(Epilogue):
         _check(c is None and d.dtype == torch.bfloat16, 'Stochastic rounding requires a direct BF16 output')
 
 
-class _Bias(Epilogue):
-    def __init__(self, bias):
-        self.bias = bias
-
-
 def _check(cond: bool, msg: str = 'Assertion error') -> None:
     if not cond:
         raise RuntimeError(msg)

@@ -691,10 +691,11 @@ def select_config(m: int, n: int, k: int, kind: int = _lib.DG_KIND_FP8_FP8, gemm
 
 
 def launch_plan(m: int, n: int, k: int, kind: int = _lib.DG_KIND_FP8_FP8, gemm_type: int = _lib.DG_GEMM_NORMAL,
-                num_groups: int = 1) -> dict:
+                num_groups: int = 1, split_k: int = 0) -> dict:
     """The launch the library would make for a K-major GEMM of this shape under the current
     runtime settings (set_num_sms, mk alignment): tile, workgroups, threads, tiles, K split and
-    whether the workgroups walk tiles persistently.  Nothing is launched."""
+    whether the workgroups walk tiles persistently (split_k > 1 forces a K split, as DG_SPLIT_K
+    does for the calls).  Nothing is launched."""
     import ctypes
     args = _lib.GemmArgs()
     # K as the calls pass it to the kernels: padded so rows stay whole 16-byte pieces
@@ -714,6 +715,7 @@ def launch_plan(m: int, n: int, k: int, kind: int = _lib.DG_KIND_FP8_FP8, gemm_t
     args.num_cus = get_num_sms()
     # (dense and batched calls may split K into the library's per-stream workspace)
     args.library_workspace = 1 if gemm_type in (_lib.DG_GEMM_NORMAL, _lib.DG_GEMM_BATCHED) else 0
+    args.split_k = split_k
     info = _lib.LaunchInfo()
     lib = _lib.load()
     _lib.check(lib.dg_launch_plan(args, ctypes.byref(info)), lib)

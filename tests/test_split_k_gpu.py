@@ -166,3 +166,27 @@ def test_split_back_to_back_matches_isolated():
         torch.cuda.synchronize()
         for i, (c, d) in enumerate(zip(cases, outs)):
             assert torch.equal(d.view(torch.int16), c[4].view(torch.int16)), (rep, shapes[i])
+
+
+@pytest.mark.parametrize('m,n,k,split', [(64, 2112, 7168, 4), (130, 257, 1984, 3), (256, 1024, 4096, 5)])
+def test_split_k_across_xcds(split_env, m, n, k, split):
+    """The splits of one tile on different XCDs (DG_SPLIT_SPREAD=1 hands them to consecutive
+    workgroups, which the dispatcher places round-robin over the 8 XCDs): the device-scope partial
+    stores and loads must still meet, on every one of three back-to-back calls."""
+    print(f'split_k across XCDs m={m} n={n} k={k} split={split}', flush=True)
+    os.environ['DG_SPLIT_K'] = str(split)
+    os.environ['DG_SPLIT_SPREAD'] = '1'
+    try:
+        plan = deep_gemm.launch_plan(m, n, k, split_k=split)
+        print('plan', plan, flush=True)
+        assert plan['split_k'] == split
+        a, sfa, a_deq, b, sfb, b_deq = _case(m, n, k, seed=m + split)
+        ref = og.gemm_nt(a_deq, b_deq)
+        for _ in range(3):
+            d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
+            deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d)
+            torch.cuda.synchronize()
+            assert calc_diff(d.cpu(), ref) < THRESH
+        assert _counters_zero(m, n, k)
+    finally:
+        os.environ.pop('DG_SPLIT_SPREAD', None)
