@@ -4,8 +4,9 @@
 // / `nn` / `tt` layouts, the K-grouped wgrad operands [Ktot, M], einsum views whose contraction
 // axis is not the innermost) is transposed once on the device.  One workgroup moves a tile of
 // 128 / E K-indices x 128 bytes of MN (16 KB for e4m3, 8 KB for bf16) through LDS: every
-// thread keeps its loads of the tile in flight at once, and both the loads (rows of MN) and
-// the stores (rows of K) move whole 128-byte lines per group of 8 threads.  Columns K .. k_padded-1 of the output are written as zeros so the
+// thread keeps its loads of the tile in flight at once, transposes 4-byte blocks in registers
+// (v_perm_b32) into K-contiguous words, and both the loads (rows of MN) and the stores (rows of
+// K) move whole 128-byte lines per group of 8 threads.  Columns K .. k_padded-1 of the output are written as zeros so the
 // result is directly a 16-byte-aligned K-major operand.
 #include "dg_common.hpp"
 #include "../../include/deep_gemm_amd.h"
@@ -25,25 +26,29 @@ __global__ __launch_bounds__(256) void transpose_to_k_major_kernel(const Transpo
     constexpr int TM = ROWB / E;          // MN elements of a tile
     constexpr int TK = ROWB / E;          // K elements of a tile
     constexpr int VEC = 16 / E;           // elements per 16-byte access
+    constexpr int KP = 4 / E;             // K elements of one 32-bit word
     constexpr int PASS = 256 / 8;         // rows per pass (8 threads per 128-byte row)
-    constexpr int NLOAD = TK / PASS;      // loads per thread
     constexpr int NSTORE = TM / PASS;     // stores per thread
-    // (row padding: the column gathers of the store phase then hit at most two rows per bank)
-    constexpr int PAD = 4;
-    __shared__ __align__(16) uint8_t tile[TK][ROWB + PAD];
+    static_assert(TK / KP == PASS, "one K word per thread group");
+    // Transposed tile: row = MN index, ROWB bytes of K in 16-byte chunks, chunk j of row r stored
+    // at j ^ ((r / 16) % 8): a wave's word writes (its lanes 16 rows apart) then spread over the
+    // banks, and every 16-byte read stays aligned.
+    __shared__ __align__(16) uint8_t tile_t[TM][ROWB];
+    auto chunk_at = [](int r, int j) { return ((j ^ ((r >> 4) & 7)) << 4); };
 
     const int tid = threadIdx.x;
     const int k0 = blockIdx.x * TK, mn0 = blockIdx.y * TM, b = blockIdx.z;
     const uint8_t* src = p.src + ((int64_t)b * p.src_bs) * E;
     uint8_t* dst = p.dst + ((int64_t)b * p.dst_bs) * E;
-    const int c = (tid % 8) * VEC;        // this thread's 16 bytes of a 128-byte row
+    const int g = tid / 8;                // K word of the tile: K rows [KP g, KP g + KP)
+    const int c = (tid % 8) * VEC;        // MN elements [c, c + VEC) of the tile
 
-    // load: tile row = K index k0 + r, its 128 bytes of MN; all loads in flight at once
+    // load: KP source rows (K indices) of 16 MN bytes each, all in flight at once
     const bool vec_ok = (p.src_ld % VEC) == 0 && (reinterpret_cast<uintptr_t>(src) % 16) == 0;
-    i32x4 w[NLOAD];
+    i32x4 w[KP];
 #pragma unroll
-    for (int i = 0; i < NLOAD; ++i) {
-        const int k = k0 + i * PASS + tid / 8, mn = mn0 + c;
+    for (int i = 0; i < KP; ++i) {
+        const int k = k0 + KP * g + i, mn = mn0 + c;
         w[i] = i32x4{0, 0, 0, 0};
         if (k < p.k) {
             const uint8_t* s = src + ((int64_t)k * p.src_ld + mn) * E;
@@ -57,30 +62,52 @@ __global__ __launch_bounds__(256) void transpose_to_k_major_kernel(const Transpo
             }
         }
     }
+    // Transpose in registers: for each of the VEC MN elements, one 32-bit word holding its KP
+    // K-consecutive values (v_perm_b32 picks bytes from a pair of words: selector byte n takes
+    // byte n of the second operand for n < 4, byte n - 4 of the first for n >= 4).
 #pragma unroll
-    for (int i = 0; i < NLOAD; ++i) {
-        uint32_t* t = reinterpret_cast<uint32_t*>(&tile[i * PASS + tid / 8][c * E]);
-        t[0] = w[i][0]; t[1] = w[i][1]; t[2] = w[i][2]; t[3] = w[i][3];
+    for (int q = 0; q < 4; ++q) {
+        uint32_t t[4];
+        if constexpr (E == 1) {
+            // 4x4 byte block: rows = K 0..3 (words w[i][q]), columns = MN 4q .. 4q + 3
+            const uint32_t r0 = w[0][q], r1 = w[1][q], r2 = w[2][q], r3 = w[3][q];
+            const uint32_t lo01 = __builtin_amdgcn_perm(r1, r0, 0x05010400u);   // r0.b0 r1.b0 r0.b1 r1.b1
+            const uint32_t hi01 = __builtin_amdgcn_perm(r1, r0, 0x07030602u);   // r0.b2 r1.b2 r0.b3 r1.b3
+            const uint32_t lo23 = __builtin_amdgcn_perm(r3, r2, 0x05010400u);
+            const uint32_t hi23 = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
+            t[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);   // MN 4q:     K 0..3
+            t[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);   // MN 4q + 1
+            t[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);   // MN 4q + 2
+            t[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);   // MN 4q + 3
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<uint32_t*>(&tile_t[c + 4 * q + j][chunk_at(c + 4 * q + j, g >> 2) + (g & 3) * 4]) = t[j];
+        } else {
+            // 2x2 block of 16-bit elements: rows = K 0..1, columns = MN 2q, 2q + 1
+            const uint32_t r0 = w[0][q], r1 = w[1][q];
+            t[0] = __builtin_amdgcn_perm(r1, r0, 0x05040100u);   // MN 2q:     K 0, 1
+            t[1] = __builtin_amdgcn_perm(r1, r0, 0x07060302u);   // MN 2q + 1
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                *reinterpret_cast<uint32_t*>(&tile_t[c + 2 * q + j][chunk_at(c + 2 * q + j, g >> 2) + (g & 3) * 4]) = t[j];
+        }
     }
     __syncthreads();
 
-    // store: output row = MN index, 128 bytes of K from 8 threads (whole lines per instruction);
-    // a thread gathers its VEC elements down the tile's column
+    // store: output row = MN index, 128 bytes of K from 8 threads (whole lines per instruction),
+    // each thread's 16 bytes one LDS read of the transposed tile
 #pragma unroll
     for (int i = 0; i < NSTORE; ++i) {
         const int r = i * PASS + tid / 8;     // MN within the tile
-        const int mn = mn0 + r, k = k0 + c;
+        const int cb = (tid % 8) * 16;        // byte of the tile's K segment
+        const int mn = mn0 + r, k = k0 + cb / E;
         if (mn >= p.mn || k >= p.k_padded) continue;
-        uint32_t o[4];
-        uint8_t* ob = reinterpret_cast<uint8_t*>(o);
-#pragma unroll
-        for (int j = 0; j < VEC; ++j)
-#pragma unroll
-            for (int e = 0; e < E; ++e) ob[j * E + e] = tile[c + j][r * E + e];
+        const i32x4 o = *reinterpret_cast<const i32x4*>(&tile_t[r][chunk_at(r, tid % 8)]);
         uint8_t* d = dst + ((int64_t)mn * p.dst_ld + k) * E;
         if (k + VEC <= p.k_padded) {
-            *reinterpret_cast<i32x4*>(d) = i32x4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+            *reinterpret_cast<i32x4*>(d) = o;
         } else {
+            const uint8_t* ob = reinterpret_cast<const uint8_t*>(&o);
             for (int j = 0; j < VEC && k + j < p.k_padded; ++j)
                 for (int e = 0; e < E; ++e) d[j * E + e] = ob[j * E + e];
         }
