@@ -207,6 +207,50 @@ __device__ __forceinline__ void swizzle_tile(int t, int nm, int nn, int gm, int&
     nb = in_band / size;
 }
 
+// Tile order of an M-grouped contiguous GEMM with a psum layout: the M-blocks of one expert's
+// N-block take consecutive tile indices, so they run at the same time on one XCD and share the
+// expert's weight tile in its L2 (the bands of swizzle_tile cut across experts).  Experts in
+// order, each expert's N-blocks in order; the blocks past the last group's aligned end (zero
+// tiles) come last.  Expert e's rows are [align(psum[e-1]), align(psum[e])); alignment is a
+// multiple of BM.  Each wave scans 64 experts per round: a lane per expert, a prefix sum of their
+// tile counts over the lanes.
+__device__ __forceinline__ void expert_major_tile(const int* psum, int num_groups, int alignment, int t, int bm,
+                                                  int nm, int nn, int& mb, int& nb) {
+    const int lane = threadIdx.x & 63;
+    int before = 0;   // tiles of the experts of earlier rounds
+    for (int base = 0; base < num_groups; base += 64) {
+        const int e = base + lane;
+        int start = 0, end = 0;
+        if (e < num_groups) {
+            start = e == 0 ? 0 : align_up(psum[e - 1], alignment);
+            end = align_up(psum[e], alignment);
+        }
+        const int blocks = max(0, end - start) / bm;
+        const int tiles = blocks * nn;
+        int incl = tiles;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
+        }
+        const uint64_t hit = __ballot(e < num_groups && t < before + incl);
+        if (hit != 0) {
+            const int src = __builtin_ctzll(hit);
+            const int l = t - before - __shfl(incl - tiles, src, 64);
+            const int bl = __shfl(blocks, src, 64);
+            nb = l / bl;
+            mb = __shfl(start, src, 64) / bm + l % bl;
+            return;
+        }
+        before += __shfl(incl, 63, 64);
+    }
+    const int first = min(nm, align_up(psum[num_groups - 1], alignment) / bm);
+    const int rest = max(1, nm - first);
+    const int l = t - before;
+    nb = min(nn - 1, l / rest);
+    mb = min(nm - 1, first + l % rest);
+}
+
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // Epilogue of one 32x32 accumulator block: lane (r, q) holds output row m (the caller's
@@ -444,7 +488,13 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         t -= batch * nm * nn;
     }
     int mb, nb;
-    swizzle_tile(t, nm, nn, p.group_m, mb, nb);
+    if (gemm_type == kMGroupedPsum && p.num_groups > 0) {
+        expert_major_tile(p.layout, p.num_groups, p.alignment, t, BM, nm, nn, mb, nb);
+        mb = __builtin_amdgcn_readfirstlane(mb);
+        nb = __builtin_amdgcn_readfirstlane(nb);
+    } else {
+        swizzle_tile(t, nm, nn, p.group_m, mb, nb);
+    }
     const int m0 = mb * BM, n0 = nb * BN;
     const int M = CM > 0 ? CM : p.m, N = CN > 0 ? CN : p.n;
 
