@@ -73,11 +73,16 @@ int device_cus() {
     return cached[dev];
 }
 
+// Tiles taller than 256 rows serve M-grouped psum layouts only, anchored at each group's first row
+// (gemm_kernel.hpp, anchored_tile); there BM need not divide the alignment.
+bool tile_anchored(int bm) { return bm > 256; }
+
 bool tile_allowed(const dg_gemm_args& a, int bm, int bn) {
+    (void)bn;
+    if (tile_anchored(bm)) return a.gemm_type == kMGroupedPsum;
     if (a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) {
         if (a.alignment % bm != 0) return false;
     }
-    (void)bn;
     return true;
 }
 
@@ -99,7 +104,9 @@ bool split_capable(const dg_gemm_args& a) { return a.gemm_type == kNormal || a.g
 
 int64_t plan_tiles(const dg_gemm_args& a, const TileCfg& t) {
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
-    return (int64_t)ceil_div(a.m, t.bm) * ceil_div(a.n, t.bn) * groups;
+    // anchored tiles: each group's rows start a new tile, so at most one extra tile row per group
+    const int64_t mrows = ceil_div(a.m, t.bm) + (tile_anchored(t.bm) ? a.num_groups : 0);
+    return mrows * ceil_div(a.n, t.bn) * groups;
 }
 
 // Workspace layout: a fixed area of tile counters that every launch leaves at zero (shared by
@@ -197,7 +204,9 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
 
 // Tiles with a persistent kernel (csrc/gemm_persistent.hpp): the 128-K-stage tiles whose
 // persistent body fits the register file (256x256 does not).
-bool tile_persistable(const TileCfg& t) { return t.km == 2 && t.stages == 2 && !(t.bm == 256 && t.bn == 256); }
+bool tile_persistable(const TileCfg& t) {
+    return t.km == 2 && t.stages == 2 && !(t.bm == 256 && t.bn == 256) && !tile_anchored(t.bm);
+}
 
 // CUs the launch may occupy are capped below the device's (set_num_sms).
 bool cus_capped(int cus) { return cus < device_cus(); }
@@ -206,6 +215,15 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     Plan skinny;
     if (skinny_kernel_plan(a, cus, allow_split, skinny_env(), skinny)) return skinny;
     if (skinny_plan(a, cus, allow_split, skinny)) return skinny;
+    // M-grouped psum layouts whose alignment rules out 256-row tiles take 384x192 tiles anchored at
+    // each group's first row: a group of up to 384 rows streams its weights once instead of once
+    // per 128-row block.  Measured (G = 32 routed top-8 counts, ~257 rows a group, alignment 128,
+    // cold us): N=4096 K=7168 345.6 vs 458.7 (128x256), N=7168 K=2048 200.3 vs 237.9.  With
+    // alignment 256 the 256-row tiles are faster (443 vs 526 at N=4096 K=7168).
+    if (a.gemm_type == kMGroupedPsum && a.alignment % 256 != 0 && a.kind != kBF16) {
+        for (const TileCfg& tc : kTiles)
+            if (tc.bm == 384 && tc.bn == 192) return {tc, 1, ceil_div(a.k, k_stage_elems(a.kind, tc)), 0, 0, 0};
+    }
     allow_split = false;   // wide problems fill the CUs with tiles
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
     // (K-grouped: each tile contracts one group's share of K)
@@ -558,6 +576,10 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     p.vec_store = (a.ldd % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.d) % (4 * out_esz)) == 0) &&
                   (a.gemm_type != kBatched && a.gemm_type != kMasked ? true : (a.batch_stride_d % 4 == 0));
     p.num_m_blocks = ceil_div(a.m, cfg.bm);
+    // anchored tiles (M-grouped psum, BM > 256): a tile row per BM rows plus one per group bounds
+    // the tile count; the kernel maps tiles group by group and the spare workgroups exit
+    p.anchored = a.gemm_type == kMGroupedPsum && tile_anchored(cfg.bm);
+    if (p.anchored) p.num_m_blocks += a.num_groups;
     p.num_n_blocks = ceil_div(a.n, cfg.bn);
     p.kbytes_a = (int)kbytes_a; p.kbytes_b = (int)kbytes_b;
     static const int group_m_env = std::getenv("DG_GROUP_M") ? std::atoi(std::getenv("DG_GROUP_M")) : 0;   // tuning

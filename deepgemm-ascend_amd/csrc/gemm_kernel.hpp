@@ -58,6 +58,9 @@ struct KParams {
     float* ws;
     int* counters;
     int split_spread;          // test knob: the splits of a tile go to consecutive workgroups (other XCDs)
+    // M-grouped psum GEMMs with tiles anchored at each group's first row (BM need not divide the
+    // alignment): an upper bound of the tile count is launched; the grid's extra workgroups exit.
+    int anchored;
     // FP8 output: per-(row, 32 columns) UE8M0 exponents, packed in pairs into int16
     // sfd[(batch * n + col) / 64 * sfd_ld + row], lower byte = the even 32-column block.
     uint8_t* sfd;
@@ -249,6 +252,79 @@ __device__ __forceinline__ void expert_major_tile(const int* psum, int num_group
     const int l = t - before;
     nb = min(nn - 1, l / rest);
     mb = min(nm - 1, first + l % rest);
+}
+
+// Anchored tiles of an M-grouped psum GEMM: group e's rows [align(psum[e-1]), align(psum[e])) are
+// cut into chunks of BM rows starting at the group's first row, so a tile never mixes groups and a
+// group of up to BM rows is one tile row (its weight tile streamed once, whatever the alignment).
+// Tiles run expert-major as in expert_major_tile; then chunks of the rows past the last group's
+// aligned end (zero tiles).  Outputs: the group (-1: zero tile, -2: no tile), the tile's first row,
+// N-block, the end of its rows (rows at or past it belong to another tile) and of its valid rows.
+__device__ __forceinline__ void anchored_tile(const int* psum, int num_groups, int alignment, int t, int bm, int m_total,
+                                              int nn, int& group, int& m0, int& nb, int& tile_end, int& valid_end) {
+    const int lane = threadIdx.x & 63;
+    int before = 0;
+    for (int base = 0; base < num_groups; base += 64) {
+        const int e = base + lane;
+        int start = 0, end = 0;
+        if (e < num_groups) {
+            start = e == 0 ? 0 : align_up(psum[e - 1], alignment);
+            end = align_up(psum[e], alignment);
+        }
+        const int chunks = ceil_div(max(0, end - start), bm);
+        const int tiles = chunks * nn;
+        int incl = tiles;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
+        }
+        const uint64_t hit = __ballot(e < num_groups && t < before + incl);
+        if (hit != 0) {
+            const int src = __builtin_ctzll(hit);
+            const int l = t - before - __shfl(incl - tiles, src, 64);
+            const int ch = __shfl(chunks, src, 64);
+            group = base + src;
+            nb = l / ch;
+            m0 = __shfl(start, src, 64) + (l % ch) * bm;
+            tile_end = min(m0 + bm, __shfl(end, src, 64));
+            valid_end = min(tile_end, psum[group]);
+            if (valid_end <= m0) group = -1;
+            return;
+        }
+        before += __shfl(incl, 63, 64);
+    }
+    const int last = align_up(psum[num_groups - 1], alignment);
+    const int chunks = ceil_div(max(0, m_total - last), bm);
+    const int l = t - before;
+    if (chunks == 0 || l >= chunks * nn) {
+        group = -2;
+        return;
+    }
+    group = -1;
+    nb = l / chunks;
+    m0 = last + (l % chunks) * bm;
+    tile_end = min(m0 + bm, m_total);
+    valid_end = m0;
+}
+
+// Number of anchored tiles of a launch (the tiles of every group, then the zero tiles of the rows
+// past the last group): the grid is an upper bound, and only this many workgroups take a tile.
+__device__ __forceinline__ int anchored_total(const int* psum, int num_groups, int alignment, int bm, int m_total,
+                                              int nn) {
+    const int lane = threadIdx.x & 63;
+    int chunks = 0;
+    for (int base = 0; base < num_groups; base += 64) {
+        const int e = base + lane;
+        if (e < num_groups) {
+            const int start = e == 0 ? 0 : align_up(psum[e - 1], alignment);
+            chunks += ceil_div(max(0, align_up(psum[e], alignment) - start), bm);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) chunks += __shfl_xor(chunks, off, 64);
+    const int last = align_up(psum[num_groups - 1], alignment);
+    return (chunks + ceil_div(max(0, m_total - last), bm)) * nn;
 }
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -487,16 +563,31 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         batch = t / (nm * nn);
         t -= batch * nm * nn;
     }
-    int mb, nb;
-    if (gemm_type == kMGroupedPsum && p.num_groups > 0) {
-        expert_major_tile(p.layout, p.num_groups, p.alignment, t, BM, nm, nn, mb, nb);
+    const int M = CM > 0 ? CM : p.m, N = CN > 0 ? CN : p.n;
+    int mb = 0, nb = 0, m0, anchor_group = -1, tile_end = M, anchor_valid = M;
+    const bool anchored = gemm_type == kMGroupedPsum && p.anchored && p.num_groups > 0;
+    if (anchored) {
+        // the launch's real tiles spread over the XCDs as xcd_remap spreads a full grid
+        const int total = __builtin_amdgcn_readfirstlane(anchored_total(p.layout, p.num_groups, p.alignment, BM, M, nn));
+        if ((int)blockIdx.x >= total) return;
+        t = xcd_remap(blockIdx.x, total);
+        anchored_tile(p.layout, p.num_groups, p.alignment, t, BM, M, nn, anchor_group, m0, nb, tile_end, anchor_valid);
+        anchor_group = __builtin_amdgcn_readfirstlane(anchor_group);
+        if (anchor_group == -2) return;   // past the last tile of this launch
+        m0 = __builtin_amdgcn_readfirstlane(m0);
+        nb = __builtin_amdgcn_readfirstlane(nb);
+        tile_end = __builtin_amdgcn_readfirstlane(tile_end);
+        anchor_valid = __builtin_amdgcn_readfirstlane(anchor_valid);
+    } else {
+        if (gemm_type == kMGroupedPsum && p.num_groups > 0)
+            expert_major_tile(p.layout, p.num_groups, p.alignment, t, BM, nm, nn, mb, nb);
+        else
+            swizzle_tile(t, nm, nn, p.group_m, mb, nb);
         mb = __builtin_amdgcn_readfirstlane(mb);
         nb = __builtin_amdgcn_readfirstlane(nb);
-    } else {
-        swizzle_tile(t, nm, nn, p.group_m, mb, nb);
+        m0 = mb * BM;
     }
-    const int m0 = mb * BM, n0 = nb * BN;
-    const int M = CM > 0 ? CM : p.m, N = CN > 0 ? CN : p.n;
+    const int n0 = nb * BN;
 
     const uint8_t* a_base = p.a;
     const uint8_t* b_base = p.b;
@@ -532,6 +623,10 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
             valid_end = min(M, p.layout[batch]);
             if (m0 >= valid_end) return;   // whole tile beyond masked_m: nothing to write
         }
+    } else if (anchored) {
+        group = anchor_group;
+        valid_end = anchor_valid;
+        if (group < 0) zero_tile = true;
     } else if (gemm_type == kMGroupedPsum) {
         int found = -1;
         for (int base = 0; base < p.num_groups; base += 64) {
@@ -558,13 +653,23 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     valid_end = __builtin_amdgcn_readfirstlane(valid_end);
 
     if (zero_tile) {
-        // Padding-only tile of an M-grouped layout: its D rows are exact zeros.
-        const int rows = min(BM, M - m0), cols = min(BN, N - n0);
-        for (int e = tid; e < rows * cols; e += NT) {
-            const int rr = e / cols, cc = e % cols;
-            const int64_t off = (int64_t)(m0 + rr) * p.ldd + n0 + cc;
-            if (out_esize == 4) reinterpret_cast<float*>(d_base)[off] = 0.f;
-            else reinterpret_cast<uint16_t*>(d_base)[off] = 0;
+        // Padding-only tile of an M-grouped layout: its D rows are exact zeros (16-byte stores when
+        // the rows allow them).
+        const int rows = min(BM, tile_end - m0), cols = min(BN, N - n0);
+        const int row_bytes = cols * out_esize;
+        uint8_t* d0 = d_base + ((int64_t)m0 * p.ldd + n0) * out_esize;
+        const int64_t ld_bytes = p.ldd * out_esize;
+        if (row_bytes % 16 == 0 && ld_bytes % 16 == 0 && (reinterpret_cast<uint64_t>(d0) & 15) == 0) {
+            const int per_row = row_bytes / 16;
+            for (int e = tid; e < rows * per_row; e += NT)
+                *reinterpret_cast<i32x4*>(d0 + (int64_t)(e / per_row) * ld_bytes + (e % per_row) * 16) = i32x4{0, 0, 0, 0};
+        } else {
+            for (int e = tid; e < rows * cols; e += NT) {
+                const int rr = e / cols, cc = e % cols;
+                const int64_t off = (int64_t)(m0 + rr) * p.ldd + n0 + cc;
+                if (out_esize == 4) reinterpret_cast<float*>(d_base)[off] = 0.f;
+                else reinterpret_cast<uint16_t*>(d_base)[off] = 0;
+            }
         }
         return;
     }
@@ -573,7 +678,8 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         if (!kBf16) sfb += (int64_t)group * p.sfb_bs;
     }
 
-    const int rows_a = min(BM, M - m0);
+    // (an anchored tile loads only its group's valid rows: the rest of the tile reads zeros)
+    const int rows_a = anchored ? min(BM, valid_end - m0) : min(BM, M - m0);
     const int rows_b = min(BN, N - n0);
     const int64_t lda = p.lda, ldb = p.ldb;
     const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(a_base + (int64_t)m0 * lda, (int64_t)rows_a * lda);
@@ -971,7 +1077,7 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     static_for<TM>([&](auto jm_c) {
         constexpr int jm = decltype(jm_c)::value;
         const int m = m0 + wm * WM + jm * 32 + r;
-        const bool row_ok = m < M && !(gemm_type == kMasked && m >= valid_end);
+        const bool row_ok = m < tile_end && !(gemm_type == kMasked && m >= valid_end);
         bool pad_row = false;
         if (gemm_type == kMGroupedPsum) pad_row = m >= valid_end;
         else if (gemm_type == kMGroupedIdx) pad_row = row_ok && p.layout[m] != group;

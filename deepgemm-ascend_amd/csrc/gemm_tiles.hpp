@@ -33,6 +33,8 @@ constexpr TileCfg kTiles[] = {
     {256, 256, 4, 8, 4, 2, 2, 1, 1380}, {256, 224, 4, 8, 4, 2, 2, 1, 1250}, {256, 128, 4, 8, 8, 4, 1, 1, 937},
     {128, 256, 2, 4, 4, 3, 1, 2, 985},  {128, 128, 2, 4, 4, 4, 1, 1, 1056}, {64, 128, 2, 4, 4, 6, 1, 2, 588},
     {32, 128, 1, 4, 4, 6, 1, 2, 643},  {256, 160, 4, 8, 4, 2, 2, 1, 950},
+    // tiles anchored at each group's first row (M-grouped psum layouts only)
+    {384, 192, 4, 8, 8, 2, 2, 1, 1250}, {384, 128, 4, 8, 4, 2, 2, 1, 1000},
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -55,11 +57,11 @@ KernelFn pick_epi(int epi) {
     }
 }
 
-// Persistent kernels exist for the 128-K-stage (km = 2, two-slot ring) tiles.
+// Persistent kernels exist for the 128-K-stage (km = 2, two-slot ring) tiles of up to 256 rows.
 template <int I, int KIND>
 KernelFn pick_persistent_epi(int epi) {
     constexpr TileCfg t = kTiles[I];
-    if constexpr (t.km != 2 || t.stages != 2) {
+    if constexpr (t.km != 2 || t.stages != 2 || t.bm > 256) {
         return nullptr;
     } else {
         switch (epi) {

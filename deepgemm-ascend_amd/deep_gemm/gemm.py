@@ -716,6 +716,9 @@ def launch_plan(m: int, n: int, k: int, kind: int = _lib.DG_KIND_FP8_FP8, gemm_t
     # (dense and batched calls may split K into the library's per-stream workspace)
     args.library_workspace = 1 if gemm_type in (_lib.DG_GEMM_NORMAL, _lib.DG_GEMM_BATCHED) else 0
     args.split_k = split_k
+    forced = os.environ.get('DG_FORCE_BLOCK')   # the tuning override the calls honour
+    if forced:
+        args.block_m, args.block_n = (int(x) for x in forced.split('x'))
     info = _lib.LaunchInfo()
     lib = _lib.load()
     _lib.check(lib.dg_launch_plan(args, ctypes.byref(info)), lib)

@@ -1,0 +1,61 @@
+"""GPU parity of the anchored tiles of M-grouped psum GEMMs (csrc/gemm_kernel.hpp, anchored_tile):
+tiles of 384 rows that start at each group's first row, so the tile height need not divide the
+alignment.  Valid rows match the oracle (calc_diff < 1e-5, the reference's bar,
+tests/test_fp8_gemm.py:21), the padding rows of every group and the rows past the last group are
+exact zeros, and nothing outside D's rows is written (a NaN canary row after D)."""
+import os
+
+import pytest
+import torch
+
+import deep_gemm
+from oracle import gemm as og, layout as ol
+from helpers import gen, operand, calc_diff
+
+pytestmark = pytest.mark.gpu
+THRESH = 1e-5
+
+
+@pytest.mark.parametrize('block', ['384x192', '384x128'])
+@pytest.mark.parametrize('sizes,alignment,trailing', [
+    ([257, 240, 0, 272, 1, 384, 385, 900], 128, 0),     # typical MoE counts, an empty group, multi-chunk groups
+    ([100, 50, 300], 32, 64),                            # alignment 32, rows past the last group
+    ([700, 0, 256, 1, 513, 300], 256, 256),             # alignment 256
+    ([5], 128, 0),                                       # one tiny group
+])
+def test_anchored_m_grouped(monkeypatch, block, sizes, alignment, trailing):
+    print(f'anchored {block} sizes={sizes} alignment={alignment} trailing={trailing}', flush=True)
+    monkeypatch.setenv('DG_FORCE_BLOCK', block)
+    total, ps = ol.psum_from_sizes(sizes, alignment)
+    total += trailing
+    n, k = 448, 1024
+    g = gen(sum(sizes) + alignment)
+    a, sfa, a_deq = operand(total, k, 'e4m3', (1, 32), g)
+    for sl in ol.psum_pad_slices(ps, alignment):
+        a.view(torch.uint8)[sl] = 0
+        a_deq[sl] = 0
+    if trailing:
+        a.view(torch.uint8)[-trailing:] = 0
+        a_deq[-trailing:] = 0
+    b, sfb, b_deq = operand(n, k, 'e4m3', (1, 32), g, batch=len(sizes))
+    layout_t = torch.tensor(ps, dtype=torch.int32)
+    out_full = torch.full((total + 1, n), float('nan'), dtype=torch.bfloat16, device='cuda')
+    d = out_full[:total]
+    old = deep_gemm.get_mk_alignment_for_contiguous_layout()
+    deep_gemm.set_mk_alignment_for_contiguous_layout(alignment)
+    try:
+        plan = deep_gemm.launch_plan(total, n, k, gemm_type=2, num_groups=len(sizes))
+        print('plan', plan, flush=True)
+        deep_gemm.m_grouped_fp8_gemm_nt_contiguous((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d, layout_t.cuda())
+    finally:
+        deep_gemm.set_mk_alignment_for_contiguous_layout(old)
+    torch.cuda.synchronize()
+    res = out_full.cpu()
+    assert torch.isnan(res[total].float()).all(), 'wrote past D'
+    out = res[:total]
+    valid = torch.zeros(total, dtype=torch.bool)
+    for sl in ol.psum_slices(ps, alignment):
+        valid[sl] = True
+    assert torch.equal(out[~valid], torch.zeros_like(out[~valid])), 'padding rows must be exact zeros'
+    ref = og.m_grouped_contiguous(a_deq, b_deq, layout_t, True, alignment)
+    assert calc_diff(out[valid], ref[valid]) < THRESH
