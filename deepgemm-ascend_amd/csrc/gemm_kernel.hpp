@@ -848,7 +848,10 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
                        bool load_live) {
         constexpr int u = decltype(u_tag)::value;
         constexpr int buf = decltype(buf_tag)::value;
-        constexpr bool kLoadWave = decltype(loads_tag)::value != 0;
+        // loads_tag: bit 0 = this wave issues global->LDS loads, bit 1 = its rows are all past the
+        // group's valid rows (anchored tiles): it keeps the ring's loads and barriers, no MFMAs
+        constexpr bool kLoadWave = (decltype(loads_tag)::value & 1) != 0;
+        constexpr bool kDeadRows = (decltype(loads_tag)::value & 2) != 0;
         constexpr bool kLoads = kLoadWave && u == 0 && (!kLate || kSpread);
         constexpr int TNX = decltype(tnx_tag)::value;
         constexpr int kLPG = (NL + TNX - 1) / TNX;
@@ -878,7 +881,8 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
             }
             static_for<TM>([&](auto jm_c) {
                 constexpr int jm = decltype(jm_c)::value;
-                if constexpr (kBf16) {
+                if constexpr (kDeadRows) {
+                } else if constexpr (kBf16) {
                     const i32x4 b0 = {fb_cur[0], fb_cur[1], fb_cur[2], fb_cur[3]};
                     const i32x4 b1 = {fb_cur[4], fb_cur[5], fb_cur[6], fb_cur[7]};
                     const i32x4 a0 = {fa[buf][jm][0], fa[buf][jm][1], fa[buf][jm][2], fa[buf][jm][3]};
@@ -965,8 +969,21 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
             for (int c = 0; c < num_virtual; ++c) iteration(c, Int<0>{}, loads_tag, tnx_tag);
         }
     };
-    if (LW == NW || is_loader) main_loop(Int<1>{}, Int<TN_LAST>{});   // loaders = the last wave column
-    else main_loop(Int<0>{}, Int<TN>{});
+    // (anchored tiles: a wave whose rows all lie past the group's valid rows runs a copy of the
+    // loop without MFMAs; its accumulators stay zero)
+    const bool dead_rows = BM > 256 && m0 + wm * WM >= valid_end;
+    if constexpr (BM > 256) {
+        if (dead_rows) {
+            if (LW == NW || is_loader) main_loop(Int<3>{}, Int<TN_LAST>{});
+            else main_loop(Int<2>{}, Int<TN>{});
+        } else {
+            if (LW == NW || is_loader) main_loop(Int<1>{}, Int<TN_LAST>{});
+            else main_loop(Int<0>{}, Int<TN>{});
+        }
+    } else {
+        if (LW == NW || is_loader) main_loop(Int<1>{}, Int<TN_LAST>{});   // loaders = the last wave column
+        else main_loop(Int<0>{}, Int<TN>{});
+    }
     __builtin_amdgcn_s_waitcnt(0);
 
     // ------------------------------------------------------------------ split-K reduction
