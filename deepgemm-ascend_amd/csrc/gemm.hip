@@ -218,9 +218,10 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     // M-grouped psum layouts whose alignment rules out 256-row tiles take 384x192 tiles anchored at
     // each group's first row: a group of up to 384 rows streams its weights once instead of once
     // per 128-row block.  Measured (G = 32 routed top-8 counts, ~257 rows a group, alignment 128,
-    // cold us): N=4096 K=7168 345.6 vs 458.7 (128x256), N=7168 K=2048 200.3 vs 237.9.  With
-    // alignment 256 the 256-row tiles are faster (443 vs 526 at N=4096 K=7168).
-    if (a.gemm_type == kMGroupedPsum && a.alignment % 256 != 0 && a.kind != kBF16) {
+    // cold us): N=4096 K=7168 345.6 vs 458.7 (128x256), N=7168 K=2048 200.3 vs 237.9; bf16
+    // 635.6 vs 839.9 and 330.2 vs 408.5.  With alignment 256 the 256-row tiles are faster (443 vs
+    // 526 at N=4096 K=7168).
+    if (a.gemm_type == kMGroupedPsum && a.alignment % 256 != 0) {
         for (const TileCfg& tc : kTiles)
             if (tc.bm == 384 && tc.bn == 192) return {tc, 1, ceil_div(a.k, k_stage_elems(a.kind, tc)), 0, 0, 0};
     }

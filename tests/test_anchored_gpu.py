@@ -59,3 +59,35 @@ def test_anchored_m_grouped(monkeypatch, block, sizes, alignment, trailing):
     assert torch.equal(out[~valid], torch.zeros_like(out[~valid])), 'padding rows must be exact zeros'
     ref = og.m_grouped_contiguous(a_deq, b_deq, layout_t, True, alignment)
     assert calc_diff(out[valid], ref[valid]) < THRESH
+
+
+def test_anchored_m_grouped_bf16():
+    """bf16 operands take the same anchored tiles (the default plan at alignment 128)."""
+    alignment = 128
+    sizes = [257, 0, 130, 400, 1]
+    total, ps = ol.psum_from_sizes(sizes, alignment)
+    n, k = 320, 512
+    g = gen(11)
+    a = (torch.randn(total, k, generator=g) * 0.1).to(torch.bfloat16)
+    for sl in ol.psum_pad_slices(ps, alignment):
+        a[sl] = 0
+    b = (torch.randn(len(sizes), n, k, generator=g) * 0.1).to(torch.bfloat16)
+    layout_t = torch.tensor(ps, dtype=torch.int32)
+    d = torch.full((total, n), float('nan'), dtype=torch.bfloat16, device='cuda')
+    old = deep_gemm.get_mk_alignment_for_contiguous_layout()
+    deep_gemm.set_mk_alignment_for_contiguous_layout(alignment)
+    try:
+        plan = deep_gemm.launch_plan(total, n, k, kind=3, gemm_type=2, num_groups=len(sizes))
+        print('bf16 anchored plan', plan, flush=True)
+        assert (plan['block_m'], plan['block_n']) == (384, 192)
+        deep_gemm.m_grouped_bf16_gemm_nt_contiguous(a.cuda(), b.cuda(), d, layout_t.cuda())
+    finally:
+        deep_gemm.set_mk_alignment_for_contiguous_layout(old)
+    torch.cuda.synchronize()
+    out = d.cpu()
+    valid = torch.zeros(total, dtype=torch.bool)
+    for sl in ol.psum_slices(ps, alignment):
+        valid[sl] = True
+    assert torch.equal(out[~valid], torch.zeros_like(out[~valid]))
+    ref = og.m_grouped_contiguous(a.float(), b.float(), layout_t, True, alignment)
+    assert calc_diff(out[valid], ref[valid]) < THRESH
