@@ -12,6 +12,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <tuple>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -49,6 +50,8 @@ namespace dg {
 // csrc/status.hip: m_indices layout check of M-grouped launches (reports through the sticky error
 // words; with may_alloc false it never allocates them)
 int check_m_indices(const int32_t* idx, int m, int alignment, int num_groups, hipStream_t st, bool may_alloc);
+// csrc/status.hip: the run table of an m_indices layout (for anchored tiles)
+int m_indices_runs(const int32_t* idx, int m, int alignment, int32_t* runs, hipStream_t st);
 
 KernelFn lookup_kernel(int kind, int bm, int bn, int epi, bool persistent) {
     switch (kind) {
@@ -73,13 +76,13 @@ int device_cus() {
     return cached[dev];
 }
 
-// Tiles taller than 256 rows serve M-grouped psum layouts only, anchored at each group's first row
-// (gemm_kernel.hpp, anchored_tile); there BM need not divide the alignment.
+// Tiles taller than 256 rows serve M-grouped layouts only, anchored at each group's (psum) or run's
+// (m_indices) first row (gemm_kernel.hpp, anchored_tile); there BM need not divide the alignment.
 bool tile_anchored(int bm) { return bm > 256; }
 
 bool tile_allowed(const dg_gemm_args& a, int bm, int bn) {
     (void)bn;
-    if (tile_anchored(bm)) return a.gemm_type == kMGroupedPsum;
+    if (tile_anchored(bm)) return a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx;
     if (a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) {
         if (a.alignment % bm != 0) return false;
     }
@@ -105,7 +108,9 @@ bool split_capable(const dg_gemm_args& a) { return a.gemm_type == kNormal || a.g
 int64_t plan_tiles(const dg_gemm_args& a, const TileCfg& t) {
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
     // anchored tiles: each group's rows start a new tile, so at most one extra tile row per group
-    const int64_t mrows = ceil_div(a.m, t.bm) + (tile_anchored(t.bm) ? a.num_groups : 0);
+    const int64_t mrows = ceil_div(a.m, t.bm) + (!tile_anchored(t.bm) ? 0
+                                                 : a.gemm_type == kMGroupedIdx ? ceil_div(a.m, std::max(1, a.alignment))
+                                                                               : a.num_groups);
     return mrows * ceil_div(a.n, t.bn) * groups;
 }
 
@@ -215,13 +220,13 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     Plan skinny;
     if (skinny_kernel_plan(a, cus, allow_split, skinny_env(), skinny)) return skinny;
     if (skinny_plan(a, cus, allow_split, skinny)) return skinny;
-    // M-grouped psum layouts whose alignment rules out 256-row tiles take 384x192 tiles anchored at
-    // each group's first row: a group of up to 384 rows streams its weights once instead of once
+    // M-grouped layouts whose alignment rules out 256-row tiles take 384x192 tiles anchored at each
+    // group's (m_indices: each run's) first row: a group of up to 384 rows streams its weights once instead of once
     // per 128-row block.  Measured (G = 32 routed top-8 counts, ~257 rows a group, alignment 128,
     // cold us): N=4096 K=7168 345.6 vs 458.7 (128x256), N=7168 K=2048 200.3 vs 237.9; bf16
     // 635.6 vs 839.9 and 330.2 vs 408.5.  With alignment 256 the 256-row tiles are faster (443 vs
     // 526 at N=4096 K=7168).
-    if (a.gemm_type == kMGroupedPsum && a.alignment % 256 != 0) {
+    if ((a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) && a.alignment % 256 != 0) {
         for (const TileCfg& tc : kTiles)
             if (tc.bm == 384 && tc.bn == 192) return {tc, 1, ceil_div(a.k, k_stage_elems(a.kind, tc)), 0, 0, 0};
     }
@@ -407,13 +412,14 @@ struct StreamWorkspace {
     int64_t bytes = 0;
 };
 std::mutex g_stream_ws_mu;
-std::map<std::pair<int, hipStream_t>, StreamWorkspace> g_stream_ws;
+// Slot 0 holds the split-K workspace, slot 1 the run table of an anchored m_indices GEMM.
+std::map<std::tuple<int, hipStream_t, int>, StreamWorkspace> g_stream_ws;
 
-int stream_workspace(hipStream_t st, int64_t need, void** out) {
+int stream_workspace(hipStream_t st, int64_t need, void** out, int slot = 0) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return dg_set_error("dg_gemm: no current HIP device");
     std::lock_guard<std::mutex> lk(g_stream_ws_mu);
-    StreamWorkspace& w = g_stream_ws[{dev, st}];
+    StreamWorkspace& w = g_stream_ws[{dev, st, slot}];
     if (w.bytes >= need) {
         *out = w.ptr;
         return DG_OK;
@@ -422,7 +428,7 @@ int stream_workspace(hipStream_t st, int64_t need, void** out) {
     if (hipStreamIsCapturing(st, &cs) != hipSuccess) (void)hipGetLastError();
     if (cs != hipStreamCaptureStatusNone) {
         char buf[256];
-        snprintf(buf, sizeof(buf), "dg_gemm: this split-K call needs a %lld-byte workspace but the stream's is %lld "
+        snprintf(buf, sizeof(buf), "dg_gemm: this call needs a %lld-byte workspace but the stream's is %lld "
                  "bytes, and it cannot grow while the stream is being captured: run the same call once before "
                  "the capture", (long long)need, (long long)w.bytes);
         return dg_set_error(buf);
@@ -432,7 +438,7 @@ int stream_workspace(hipStream_t st, int64_t need, void** out) {
     hipError_t e = hipMalloc(&p, (size_t)bytes);
     if (e == hipSuccess) e = hipMemsetAsync(p, 0, (size_t)bytes, st);   // (never inside a capture: checked above)
     if (e != hipSuccess) {
-        std::string msg = std::string("dg_gemm: split-K workspace allocation failed: ") + hipGetErrorString(e);
+        std::string msg = std::string("dg_gemm: workspace allocation failed: ") + hipGetErrorString(e);
         return dg_set_error(msg.c_str());
     }
     w.ptr = p;
@@ -579,8 +585,8 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     p.num_m_blocks = ceil_div(a.m, cfg.bm);
     // anchored tiles (M-grouped psum, BM > 256): a tile row per BM rows plus one per group bounds
     // the tile count; the kernel maps tiles group by group and the spare workgroups exit
-    p.anchored = a.gemm_type == kMGroupedPsum && tile_anchored(cfg.bm);
-    if (p.anchored) p.num_m_blocks += a.num_groups;
+    p.anchored = (a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) && tile_anchored(cfg.bm);
+    if (p.anchored) p.num_m_blocks += a.gemm_type == kMGroupedIdx ? ceil_div(a.m, p.alignment) : a.num_groups;
     p.num_n_blocks = ceil_div(a.n, cfg.bn);
     p.kbytes_a = (int)kbytes_a; p.kbytes_b = (int)kbytes_b;
     static const int group_m_env = std::getenv("DG_GROUP_M") ? std::atoi(std::getenv("DG_GROUP_M")) : 0;   // tuning
@@ -621,8 +627,24 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         // m_indices layout check: a device kernel that sets the sticky DG_ERR_M_INDICES word
         // (no host synchronisation; without the words -- a call that may not allocate, before
         // any other call allocated them -- it is skipped)
-        const int rc = check_m_indices(a.grouped_layout, a.m, a.alignment, a.num_groups, st, !noalloc);
+        int rc = check_m_indices(a.grouped_layout, a.m, a.alignment, a.num_groups, st, !noalloc);
         if (rc != DG_OK) return rc;
+        if (p.anchored) {
+            // the layout's run table: in the caller's scratch for dg_gemm_noalloc (it splits no K),
+            // else in the library's per-stream buffer
+            const int64_t need = (1 + 2 * (int64_t)ceil_div(a.m, p.alignment)) * 4;
+            void* runs = nullptr;
+            if (noalloc) {
+                if (need > a.workspace_bytes) return dg_set_error("dg_gemm_noalloc: m_indices run table exceeds the scratch");
+                runs = a.workspace;
+            } else {
+                rc = stream_workspace(st, need, &runs, 1);
+                if (rc != DG_OK) return rc;
+            }
+            p.runs = reinterpret_cast<const int*>(runs);
+            rc = m_indices_runs(a.grouped_layout, a.m, p.alignment, reinterpret_cast<int32_t*>(runs), st);
+            if (rc != DG_OK) return rc;
+        }
     }
     if (jit) return jit_run(a, cfg, epi_kind, plan.split, p, grid, st, compile_only);
     const hipError_t e = launch_module_kernel(reinterpret_cast<const void*>(fn), (unsigned)grid, (unsigned)threads, p, st);
@@ -642,7 +664,7 @@ extern "C" int dg_stream_workspace(void* stream, void** ptr, int64_t* bytes) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return dg_set_error("dg_stream_workspace: no current HIP device");
     std::lock_guard<std::mutex> lk(g_stream_ws_mu);
-    auto it = g_stream_ws.find({dev, reinterpret_cast<hipStream_t>(stream)});
+    auto it = g_stream_ws.find({dev, reinterpret_cast<hipStream_t>(stream), 0});
     *ptr = it == g_stream_ws.end() ? nullptr : it->second.ptr;
     *bytes = it == g_stream_ws.end() ? 0 : it->second.bytes;
     return DG_OK;

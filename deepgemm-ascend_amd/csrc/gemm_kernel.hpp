@@ -61,6 +61,7 @@ struct KParams {
     // M-grouped psum GEMMs with tiles anchored at each group's first row (BM need not divide the
     // alignment): an upper bound of the tile count is launched; the grid's extra workgroups exit.
     int anchored;
+    const int* runs;           // anchored m_indices GEMMs: the run table of the layout (m_indices_runs)
     // FP8 output: per-(row, 32 columns) UE8M0 exponents, packed in pairs into int16
     // sfd[(batch * n + col) / 64 * sfd_ld + row], lower byte = the even 32-column block.
     uint8_t* sfd;
@@ -254,24 +255,72 @@ __device__ __forceinline__ void expert_major_tile(const int* psum, int num_group
     mb = min(nm - 1, first + l % rest);
 }
 
-// Anchored tiles of an M-grouped psum GEMM: group e's rows [align(psum[e-1]), align(psum[e])) are
-// cut into chunks of BM rows starting at the group's first row, so a tile never mixes groups and a
-// group of up to BM rows is one tile row (its weight tile streamed once, whatever the alignment).
-// Tiles run expert-major as in expert_major_tile; then chunks of the rows past the last group's
-// aligned end (zero tiles).  Outputs: the group (-1: zero tile, -2: no tile), the tile's first row,
-// N-block, the end of its rows (rows at or past it belong to another tile) and of its valid rows.
-__device__ __forceinline__ void anchored_tile(const int* psum, int num_groups, int alignment, int t, int bm, int m_total,
-                                              int nn, int& group, int& m0, int& nb, int& tile_end, int& valid_end) {
+// Segments of anchored tiles: with `runs` null, group e of a psum layout, rows
+// [align(psum[e-1]), align(psum[e])), valid rows up to psum[e]; else run e of an m_indices layout
+// (csrc/status.hip, m_indices_runs: runs[0] = count, then first row and group id per run), rows up
+// to the next run's first row (the last: m_total), every row valid as far as the tile goes (rows
+// of another id are zeroed by the epilogue).
+struct Segment {
+    int start, end, valid, group;
+};
+__device__ __forceinline__ int segment_count(const int* psum, int num_groups, const int* runs) {
+    return runs != nullptr ? runs[0] : num_groups;
+}
+__device__ __forceinline__ Segment segment_at(const int* psum, int alignment, const int* runs, int count, int e,
+                                              int m_total) {
+    Segment sg;
+    if (runs != nullptr) {
+        sg.start = runs[1 + 2 * e];
+        sg.end = e + 1 < count ? runs[3 + 2 * e] : m_total;
+        sg.valid = sg.end;
+        sg.group = runs[2 + 2 * e];
+    } else {
+        sg.start = e == 0 ? 0 : align_up(psum[e - 1], alignment);
+        sg.end = align_up(psum[e], alignment);
+        sg.valid = psum[e];
+        sg.group = e;
+    }
+    return sg;
+}
+
+// Number of anchored tiles of a launch (the tiles of every segment, then -- psum layouts -- the zero
+// tiles of the rows past the last group): the grid is an upper bound, and only this many
+// workgroups take a tile.
+__device__ __forceinline__ int anchored_total(const int* psum, int num_groups, const int* runs, int alignment, int bm,
+                                              int m_total, int nn) {
     const int lane = threadIdx.x & 63;
-    int before = 0;
-    for (int base = 0; base < num_groups; base += 64) {
+    const int count = segment_count(psum, num_groups, runs);
+    int chunks = 0;
+    for (int base = 0; base < count; base += 64) {
         const int e = base + lane;
-        int start = 0, end = 0;
-        if (e < num_groups) {
-            start = e == 0 ? 0 : align_up(psum[e - 1], alignment);
-            end = align_up(psum[e], alignment);
+        if (e < count) {
+            const Segment sg = segment_at(psum, alignment, runs, count, e, m_total);
+            chunks += ceil_div(max(0, sg.end - sg.start), bm);
         }
-        const int chunks = ceil_div(max(0, end - start), bm);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) chunks += __shfl_xor(chunks, off, 64);
+    if (runs == nullptr) chunks += ceil_div(max(0, m_total - align_up(psum[num_groups - 1], alignment)), bm);
+    return chunks * nn;
+}
+
+// Anchored tiles of an M-grouped GEMM: each segment's rows are cut into chunks of BM rows starting
+// at its first row, so a tile never mixes groups and a group of up to BM rows is one tile row
+// (its weight tile streamed once, whatever the alignment).  Tiles run segment-major as in
+// expert_major_tile; then (psum) chunks of the rows past the last group's aligned end (zero
+// tiles).  Outputs: the group (-1: zero tile, -2: no tile), the tile's first row, N-block, the end
+// of its rows (rows at or past it belong to another tile) and of its valid rows.
+__device__ __forceinline__ void anchored_tile(const int* psum, int num_groups, const int* runs, int alignment, int t,
+                                              int bm, int m_total, int nn, int& group, int& m0, int& nb, int& tile_end,
+                                              int& valid_end) {
+    const int lane = threadIdx.x & 63;
+    const int count = segment_count(psum, num_groups, runs);
+    int before = 0;
+    for (int base = 0; base < count; base += 64) {
+        const int e = base + lane;
+        Segment sg = {0, 0, 0, -1};
+        if (e < count) sg = segment_at(psum, alignment, runs, count, e, m_total);
+        const int chunks = ceil_div(max(0, sg.end - sg.start), bm);
         const int tiles = chunks * nn;
         int incl = tiles;
 #pragma unroll
@@ -279,22 +328,22 @@ __device__ __forceinline__ void anchored_tile(const int* psum, int num_groups, i
             const int v = __shfl_up(incl, off, 64);
             if (lane >= off) incl += v;
         }
-        const uint64_t hit = __ballot(e < num_groups && t < before + incl);
+        const uint64_t hit = __ballot(e < count && t < before + incl);
         if (hit != 0) {
             const int src = __builtin_ctzll(hit);
             const int l = t - before - __shfl(incl - tiles, src, 64);
             const int ch = __shfl(chunks, src, 64);
-            group = base + src;
+            group = __shfl(sg.group, src, 64);
             nb = l / ch;
-            m0 = __shfl(start, src, 64) + (l % ch) * bm;
-            tile_end = min(m0 + bm, __shfl(end, src, 64));
-            valid_end = min(tile_end, psum[group]);
-            if (valid_end <= m0) group = -1;
+            m0 = __shfl(sg.start, src, 64) + (l % ch) * bm;
+            tile_end = min(m0 + bm, __shfl(sg.end, src, 64));
+            valid_end = min(tile_end, __shfl(sg.valid, src, 64));
+            if (valid_end <= m0 || group < 0 || group >= num_groups) group = -1;
             return;
         }
         before += __shfl(incl, 63, 64);
     }
-    const int last = align_up(psum[num_groups - 1], alignment);
+    const int last = runs != nullptr ? m_total : align_up(psum[num_groups - 1], alignment);
     const int chunks = ceil_div(max(0, m_total - last), bm);
     const int l = t - before;
     if (chunks == 0 || l >= chunks * nn) {
@@ -306,25 +355,6 @@ __device__ __forceinline__ void anchored_tile(const int* psum, int num_groups, i
     m0 = last + (l % chunks) * bm;
     tile_end = min(m0 + bm, m_total);
     valid_end = m0;
-}
-
-// Number of anchored tiles of a launch (the tiles of every group, then the zero tiles of the rows
-// past the last group): the grid is an upper bound, and only this many workgroups take a tile.
-__device__ __forceinline__ int anchored_total(const int* psum, int num_groups, int alignment, int bm, int m_total,
-                                              int nn) {
-    const int lane = threadIdx.x & 63;
-    int chunks = 0;
-    for (int base = 0; base < num_groups; base += 64) {
-        const int e = base + lane;
-        if (e < num_groups) {
-            const int start = e == 0 ? 0 : align_up(psum[e - 1], alignment);
-            chunks += ceil_div(max(0, align_up(psum[e], alignment) - start), bm);
-        }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) chunks += __shfl_xor(chunks, off, 64);
-    const int last = align_up(psum[num_groups - 1], alignment);
-    return (chunks + ceil_div(max(0, m_total - last), bm)) * nn;
 }
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -565,13 +595,16 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     }
     const int M = CM > 0 ? CM : p.m, N = CN > 0 ? CN : p.n;
     int mb = 0, nb = 0, m0, anchor_group = -1, tile_end = M, anchor_valid = M;
-    const bool anchored = gemm_type == kMGroupedPsum && p.anchored && p.num_groups > 0;
+    const bool anchored = (gemm_type == kMGroupedPsum || gemm_type == kMGroupedIdx) && p.anchored && p.num_groups > 0;
     if (anchored) {
+        const int* runs = gemm_type == kMGroupedIdx ? p.runs : nullptr;
         // the launch's real tiles spread over the XCDs as xcd_remap spreads a full grid
-        const int total = __builtin_amdgcn_readfirstlane(anchored_total(p.layout, p.num_groups, p.alignment, BM, M, nn));
+        const int total =
+            __builtin_amdgcn_readfirstlane(anchored_total(p.layout, p.num_groups, runs, p.alignment, BM, M, nn));
         if ((int)blockIdx.x >= total) return;
         t = xcd_remap(blockIdx.x, total);
-        anchored_tile(p.layout, p.num_groups, p.alignment, t, BM, M, nn, anchor_group, m0, nb, tile_end, anchor_valid);
+        anchored_tile(p.layout, p.num_groups, runs, p.alignment, t, BM, M, nn, anchor_group, m0, nb, tile_end,
+                      anchor_valid);
         anchor_group = __builtin_amdgcn_readfirstlane(anchor_group);
         if (anchor_group == -2) return;   // past the last tile of this launch
         m0 = __builtin_amdgcn_readfirstlane(m0);

@@ -82,6 +82,52 @@ int check_m_indices(const int32_t* idx, int m, int alignment, int num_groups, hi
     return DG_OK;
 }
 
+// Runs of an m_indices layout: maximal sequences of `alignment`-row blocks whose first rows carry
+// the same group id (-1: padding).  Output: runs[0] = the number of runs, then (first row, group)
+// per run; a run ends where the next begins (the last at m).  One workgroup: each thread takes a
+// contiguous span of blocks, counts the runs starting there, and a workgroup prefix sum places
+// them.
+constexpr int kRunThreads = 1024;
+__global__ __launch_bounds__(kRunThreads) void m_indices_runs_kernel(const int32_t* idx, int m, int alignment,
+                                                                    int32_t* runs) {
+    __shared__ int counts[kRunThreads];
+    const int tid = threadIdx.x;
+    const int nblk = (m + alignment - 1) / alignment;
+    const int per = (nblk + kRunThreads - 1) / kRunThreads;
+    const int b0 = min(nblk, tid * per), b1 = min(nblk, b0 + per);
+    int n = 0;
+    for (int b = b0; b < b1; ++b)
+        if (b == 0 || idx[(int64_t)b * alignment] != idx[(int64_t)(b - 1) * alignment]) ++n;
+    counts[tid] = n;
+    __syncthreads();
+    for (int off = 1; off < kRunThreads; off <<= 1) {
+        const int v = tid >= off ? counts[tid - off] : 0;
+        __syncthreads();
+        counts[tid] += v;
+        __syncthreads();
+    }
+    int r = counts[tid] - n;   // runs before this thread's span
+    for (int b = b0; b < b1; ++b) {
+        const int g = idx[(int64_t)b * alignment];
+        if (b == 0 || g != idx[(int64_t)(b - 1) * alignment]) {
+            runs[1 + 2 * r] = b * alignment;
+            runs[2 + 2 * r] = g;
+            ++r;
+        }
+    }
+    if (tid == kRunThreads - 1) runs[0] = counts[tid];
+}
+
+int m_indices_runs(const int32_t* idx, int m, int alignment, int32_t* runs, hipStream_t st) {
+    hipLaunchKernelGGL(m_indices_runs_kernel, dim3(1), dim3(kRunThreads), 0, st, idx, m, alignment, runs);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        dg_set_error(hipGetErrorString(e));
+        return DG_ELAUNCH;
+    }
+    return DG_OK;
+}
+
 }  // namespace dg
 
 extern "C" uint32_t dg_take_errors(void) {

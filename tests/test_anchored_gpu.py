@@ -1,6 +1,6 @@
-"""GPU parity of the anchored tiles of M-grouped psum GEMMs (csrc/gemm_kernel.hpp, anchored_tile):
-tiles of 384 rows that start at each group's first row, so the tile height need not divide the
-alignment.  Valid rows match the oracle (calc_diff < 1e-5, the reference's bar,
+"""GPU parity of the anchored tiles of M-grouped GEMMs (csrc/gemm_kernel.hpp, anchored_tile):
+tiles of 384 rows that start at each group's (psum) or run's (m_indices) first row, so the tile
+height need not divide the alignment.  Valid rows match the oracle (calc_diff < 1e-5, the reference's bar,
 tests/test_fp8_gemm.py:21), the padding rows of every group and the rows past the last group are
 exact zeros, and nothing outside D's rows is written (a NaN canary row after D)."""
 import os
@@ -91,3 +91,55 @@ def test_anchored_m_grouped_bf16():
     assert torch.equal(out[~valid], torch.zeros_like(out[~valid]))
     ref = og.m_grouped_contiguous(a.float(), b.float(), layout_t, True, alignment)
     assert calc_diff(out[valid], ref[valid]) < THRESH
+
+
+def _runs_layout(blocks, alignment, fill):
+    """m_indices from a list of (group, rows) alignment blocks in the given order (rows < alignment:
+    the rest of the block is -1 padding)."""
+    idx = []
+    for grp, rows in blocks:
+        idx += [grp] * rows + [-1] * (alignment - rows)
+    return torch.tensor(idx, dtype=torch.int32)
+
+
+@pytest.mark.parametrize('case', ['sorted', 'unsorted', 'split_group', 'padding_blocks'])
+def test_anchored_m_indices(case):
+    """m_indices layouts: the run table (csrc/status.hip) drives the anchored tiles whether groups
+    are sorted, out of order, split into several runs, or separated by padding-only blocks."""
+    alignment, g_num = 128, 4
+    if case == 'sorted':
+        blocks = [(0, 128), (0, 128), (0, 1), (1, 100), (2, 128), (2, 128), (2, 128), (2, 128), (3, 5)]
+    elif case == 'unsorted':
+        blocks = [(3, 128), (3, 7), (0, 128), (2, 64), (1, 128), (1, 128), (1, 128), (1, 2)]
+    elif case == 'split_group':
+        blocks = [(1, 128), (1, 30), (0, 128), (1, 128), (1, 128), (1, 128), (1, 17), (2, 90)]
+    else:
+        blocks = [(-1, 0), (0, 128), (0, 60), (-1, 0), (-1, 0), (3, 128), (3, 128), (3, 128), (3, 128), (-1, 0)]
+    idx = _runs_layout(blocks, alignment, -1)
+    total = idx.numel()
+    n, k = 448, 512
+    g = gen(len(blocks) * 7 + alignment)
+    a, sfa, a_deq = operand(total, k, 'e4m3', (1, 32), g)
+    pad = idx < 0
+    a.view(torch.uint8)[pad] = 0
+    a_deq[pad] = 0
+    b, sfb, b_deq = operand(n, k, 'e4m3', (1, 32), g, batch=g_num)
+    d = torch.full((total, n), float('nan'), dtype=torch.bfloat16, device='cuda')
+    old = deep_gemm.get_mk_alignment_for_contiguous_layout()
+    deep_gemm.set_mk_alignment_for_contiguous_layout(alignment)
+    try:
+        plan = deep_gemm.launch_plan(total, n, k, gemm_type=3, num_groups=g_num)
+        print(f'anchored m_indices {case} plan={plan}', flush=True)
+        assert (plan['block_m'], plan['block_n']) == (384, 192)
+        deep_gemm.m_grouped_fp8_gemm_nt_contiguous((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d, idx.cuda(),
+                                                   use_psum_layout=False)
+    finally:
+        deep_gemm.set_mk_alignment_for_contiguous_layout(old)
+    torch.cuda.synchronize()
+    from deep_gemm import _lib
+    assert _lib.load().dg_take_errors() == 0, 'a valid m_indices layout must not be reported'
+    out = d.cpu()
+    assert torch.equal(out[pad], torch.zeros_like(out[pad])), 'padding rows must be exact zeros'
+    ref = og.m_grouped_contiguous(a_deq, b_deq, idx, False, alignment)
+    assert calc_diff(out[~pad], ref[~pad]) < THRESH
+
