@@ -81,8 +81,8 @@ def test_grouped_requires_layout(lib):
 
 
 def test_select_config_respects_grouped_alignment(lib):
-    """m_indices layouts take a block_m dividing the alignment; psum layouts too, except the tiles
-    anchored at each group's first row (384 rows), taken when the alignment rules out 256-row tiles."""
+    """M-grouped layouts take a block_m dividing the alignment, except the tiles anchored at each
+    group's or run's first row (384 rows), taken when the alignment rules out 256-row tiles."""
     for gemm_type in (2, 3):
         for align in (256, 128, 64, 32):
             args = _lib.GemmArgs()
@@ -90,7 +90,7 @@ def test_select_config_respects_grouped_alignment(lib):
             args.alignment, args.num_cus = align, 256
             bm, bn = ctypes.c_int32(), ctypes.c_int32()
             assert lib.dg_select_config(ctypes.byref(args), ctypes.byref(bm), ctypes.byref(bn)) == 0
-            if gemm_type == 2 and align < 256:
+            if align < 256:
                 assert (bm.value, bn.value) == (384, 192)
             else:
                 assert align % bm.value == 0 and bn.value > 0
