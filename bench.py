@@ -267,6 +267,17 @@ def run_suite(groups):
             _line('grouped', f'm_grouped_contiguous G=32 rows={total} (valid {valid}) N={n} K={k}', us,
                   2.0 * valid * n * k, total * k + g_ * n * k + 2 * total * n, padded_tflops=round(
                       2.0 * total * n * k / (us * 1e-6) / 1e12, 1))
+            # the same rows with an m_indices layout (-1 on padding rows)
+            idx = torch.full((total,), -1, dtype=torch.int32)
+            start = 0
+            for gi, ps in enumerate(psum):
+                idx[start:ps] = gi
+                start = -(-ps // align) * align
+            idx = idx.to(dev)
+            us = _time_cold(lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous((a, sfa), (b, sfb), d, idx,
+                                                                              use_psum_layout=False))
+            _line('grouped', f'm_grouped_contiguous m_indices G=32 rows={total} (valid {valid}) N={n} K={k}', us,
+                  2.0 * valid * n * k, total * k + g_ * n * k + 2 * total * n)
             mmax = 256
             masked = torch.tensor([min(c, mmax) for c in counts], dtype=torch.int32, device=dev)
             am, sfam = fp8_operand(mmax, k, 1, batch=g_)
