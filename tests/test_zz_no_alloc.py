@@ -83,3 +83,41 @@ def test_noalloc_rejects_oversize_and_a_workspace():
     args.workspace, args.workspace_bytes = d.data_ptr(), 16
     assert lib.dg_gemm_noalloc(ctypes.byref(args), ctypes.c_void_p(stream)) != 0
     assert b'library provides the workspace' in lib.dg_last_error()
+
+
+def test_noalloc_m_indices_run_table_in_scratch():
+    """M-grouped m_indices GEMMs below alignment 256 take the anchored tiles, whose run table
+    dg_gemm_noalloc keeps in its scratch array: bit-identical to dg_gemm (which keeps it in the
+    library's per-stream buffer), on two calls in a row, the second with fewer rows."""
+    from oracle import layout as ol
+    lib = _lib.load()
+    alignment, g_num, n, k = 128, 4, 320, 512
+    for sizes, seed in (([257, 0, 130, 400], 3), ([5, 128], 4)):
+        total, ps = ol.psum_from_sizes(sizes, alignment)
+        idx = ol.m_indices_from_psum(ps, alignment, total).cuda()
+        g = gen(seed)
+        a, sfa, a_deq = operand(total, k, 'e4m3', (1, 32), g)
+        b, sfb, b_deq = operand(n, k, 'e4m3', (1, 32), g, batch=g_num)
+        a, b = a.cuda(), b.cuda()
+        sfa_t = deep_gemm.transform_sf_into_required_layout(sfa.cuda(), total, k, (1, 32), is_sfa=True)
+        sfb_t = deep_gemm.transform_sf_into_required_layout(sfb.cuda(), n, k, (1, 32), num_groups=g_num, is_sfa=False)
+        args = _lib.GemmArgs()
+        args.kind, args.gemm_type = _lib.DG_KIND_FP8_FP8, _lib.DG_GEMM_MGROUPED_IDX
+        args.m, args.n, args.k, args.num_groups = total, n, k, g_num
+        args.a, args.b, args.sfa, args.sfb = a.data_ptr(), b.data_ptr(), sfa_t.data_ptr(), sfb_t.data_ptr()
+        args.lda, args.ldb, args.ldd = a.stride(0), b.stride(1), n
+        args.batch_stride_b, args.sfb_batch_stride = b.stride(0), sfb_t.stride(0)
+        args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
+        args.grouped_layout = idx.data_ptr()
+        args.d_dtype, args.alpha, args.alignment = _lib.DG_DTYPE_BF16, 1.0, alignment
+        info = _lib.LaunchInfo()
+        _lib.check(lib.dg_launch_plan(ctypes.byref(args), ctypes.byref(info)), lib)
+        print(f'noalloc m_indices sizes={sizes} block={info.block_m}x{info.block_n}', flush=True)
+        assert (info.block_m, info.block_n) == (384, 192)
+        d_noalloc = _run(lib, args, True)
+        d_lib = _run(lib, args, False)
+        assert torch.equal(d_noalloc, d_lib)
+        valid = idx.cpu() >= 0
+        ref = og.m_grouped_contiguous(a_deq, b_deq, idx.cpu(), False, alignment)
+        assert calc_diff(d_noalloc[valid], ref[valid]) < 1e-5
+        assert torch.equal(d_noalloc[~valid], torch.zeros_like(d_noalloc[~valid]))
