@@ -97,6 +97,7 @@ struct Plan {
     int skinny_nw;      // > 0: the skinny-M kernel with this many waves (tile = 32 mt x 32 nb)
     int skinny_d;       // its ring depth
     int skinny_ar;      // and rows of A it stages
+    int skinny_rows;    // 1: the shared-ring decode kernel (skinny_rows_kernel, skinny_nw = mt x nb waves, ring skinny_d)
 };
 
 // K elements of one kernel stage of tile t
@@ -162,9 +163,15 @@ bool skinny_plan(const dg_gemm_args& a, int cus, bool allow_split, Plan& out) {
 struct SkinnyEnv {
     int mode;   // -1 default, 0 off, 1 forced configuration
     int mt, nb, nw, d, ar, split;
+    int rows, rmt, rnb, rd, rsplit;   // DG_SKINNY_ROWS: -1 default, 0 off, 1 forced "mt,nb,d[,split]"
 };
 SkinnyEnv skinny_env() {
-    SkinnyEnv e = {-1, 0, 0, 0, 0, 0, 0};
+    SkinnyEnv e = {-1, 0, 0, 0, 0, 0, 0, -1, 0, 0, 0, 0};
+    const char* rs = std::getenv("DG_SKINNY_ROWS");
+    if (rs != nullptr && *rs != '\0') {
+        if (std::strcmp(rs, "0") == 0) e.rows = 0;
+        else if (std::sscanf(rs, "%d,%d,%d,%d", &e.rmt, &e.rnb, &e.rd, &e.rsplit) >= 3) e.rows = 1;
+    }
     const char* s = std::getenv("DG_SKINNY");
     if (s == nullptr || *s == '\0') return e;
     if (std::strcmp(s, "0") == 0) { e.mode = 0; return e; }
@@ -183,6 +190,35 @@ SkinnyEnv skinny_env() {
 bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const SkinnyEnv& env, Plan& out) {
     if (env.mode == 0 || !(a.gemm_type == kNormal || a.gemm_type == kBatched || a.gemm_type == kMasked)) return false;
     const int groups0 = a.gemm_type == kNormal ? 1 : a.num_groups;
+    // Decode shapes with 64 < M <= 128 and K <= 8192 (dense or batched) take the shared-ring kernel:
+    // its waves own the tile's four 32-row blocks and fetch each group of B and A once per
+    // workgroup, four groups deep.  Measured on MI355X (fp8, cold L2, event us, skinny kernel in
+    // brackets): 128x2112x7168 21.9 (24.8), 128x4096x7168 26.8 (30.0), 128x7168x2048 15.0 (17.0),
+    // 96x4096x7168 24.5 (27.6); slower at K = 16384 (87.5 vs 74.5) and for M <= 64 (64x2112x7168
+    // 18.6 vs 17.4), which keep the skinny kernel.
+    SkinnyEnv rows_env = env;
+    if (env.rows == -1 && env.mode == -1 && a.m > 64 && a.m <= 128 && a.k <= 8192 &&
+        (a.gemm_type == kNormal || a.gemm_type == kBatched) && (int64_t)ceil_div(a.n, 32) * groups0 <= 2 * (int64_t)cus) {
+        rows_env.rows = 1;
+        rows_env.rmt = 4; rows_env.rnb = 1; rows_env.rd = 4; rows_env.rsplit = 0;
+    }
+    if (rows_env.rows == 1 && a.m <= 32 * rows_env.rmt &&
+        lookup_skinny_rows(a.kind, rows_env.rmt, rows_env.rnb, rows_env.rd, kEpiBf16) != nullptr) {
+        const SkinnyEnv& env = rows_env;
+        // shared-ring decode kernel: K split across workgroups while the strips leave CUs idle,
+        // each range keeping at least eight 64-K blocks
+        const int64_t strips = (int64_t)ceil_div(a.n, 32 * env.rnb) * groups0;
+        const int nk64 = std::max(1, ceil_div(a.k, 64));
+        int sp = 1;
+        if (allow_split && strips <= kMaxSplitTiles) {
+            sp = env.rsplit > 0 ? env.rsplit : (int)std::min<int64_t>(std::max<int64_t>(1, cus / strips), std::max(1, nk64 / 8));
+            sp = std::max(1, std::min(sp, std::min(16, nk64)));
+        }
+        const int ss = ceil_div(nk64, sp);
+        out = {{32 * env.rmt, 32 * env.rnb, 0, env.rmt * env.rnb, 0, 0, 0, 0, 0}, ceil_div(nk64, ss), ss,
+               env.rmt * env.rnb, env.rd, 32 * env.rmt, 1};
+        return true;
+    }
     int mt = a.m <= 32 ? 1 : (a.m <= 64 ? 2 : 4), nb = 1, nw = 4, d = 2, ar = a.m <= 16 ? 16 : 32 * mt;
     // long K over at most one strip per CU: eight waves per strip keep more of it in flight
     // (M = 1, 7168x16384: 24.4 vs 26.9 us)
@@ -552,7 +588,8 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
                             a.k > 0 && a.gemm_type != kKGrouped && a_span <= 0x7fffffffLL &&
                             b_span <= 0x7fffffffLL && sfa_span <= 0x7fffffffLL && sfb_span <= 0x7fffffffLL;
     KernelFn fn = jit ? nullptr
-                : skinny ? lookup_skinny(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_nw, plan.skinny_d, plan.skinny_ar, epi_kind)
+                : skinny ? (plan.skinny_rows ? lookup_skinny_rows(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_d, epi_kind)
+                                             : lookup_skinny(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_nw, plan.skinny_d, plan.skinny_ar, epi_kind))
                          : lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind, persistent);
     if (fn == nullptr && !jit) {
         char buf[160];
@@ -619,7 +656,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         info->tiles = tiles;
         info->split_k = plan.split;
         info->persistent = persistent ? 1 : 0;
-        info->skinny = skinny ? 1 : 0;
+        info->skinny = skinny ? (plan.skinny_rows ? 2 : 1) : 0;
         return DG_OK;
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);

@@ -110,6 +110,15 @@ constexpr SkinnyCfg kSkinny[] = {{1, 1, 4, 2, 16}, {1, 1, 4, 3, 16}, {1, 1, 4, 2
 constexpr int kNumSkinny = sizeof(kSkinny) / sizeof(kSkinny[0]);
 KernelFn lookup_skinny(int kind, int mt, int nb, int nw, int d, int ar, int epi);
 
+// Shared-ring decode kernels (skinny_rows_kernel): MT x NB waves, one 32x32 block each, a ring
+// of d group slots shared by the workgroup.
+struct SkinnyRowsCfg {
+    int mt, nb, d;
+};
+constexpr SkinnyRowsCfg kSkinnyRows[] = {{4, 1, 3}, {4, 1, 4}, {4, 1, 5}, {4, 2, 4}, {2, 1, 4}, {2, 2, 4}};
+constexpr int kNumSkinnyRows = sizeof(kSkinnyRows) / sizeof(kSkinnyRows[0]);
+KernelFn lookup_skinny_rows(int kind, int mt, int nb, int d, int epi);
+
 KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi, bool persistent);
 KernelFn lookup_kernel_fp8fp4(int bm, int bn, int epi, bool persistent);
 KernelFn lookup_kernel_fp4fp4(int bm, int bn, int epi, bool persistent);

@@ -426,3 +426,290 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
 }
 
 }  // namespace dg
+
+
+namespace dg {
+
+// Decode kernel with one shared ring (M <= 32 MT).  The tile is 32 MT x 32 NB like skinny_kernel's,
+// but its NW = MT x NB waves split the tile instead of K: wave w owns the 32x32 output block
+// (w % MT, w / MT) over the workgroup's whole K range.  All waves walk the same groups of G 64-K
+// blocks through one ring of D group slots (B rows of the strip, all 32 MT rows of A, and the
+// packed scale rows of both) that they fill together, so every byte is fetched once per
+// workgroup, the ring keeps D - 1 groups in flight, and no wave reduction is needed at the end.
+// One workgroup barrier per group certifies that the group has landed (every wave waited for its
+// own share of the loads) and that the slot it refills was read by every wave.  Every load of the
+// loop goes global -> LDS, so no vector-memory result lands in a register and the only waits are
+// the explicit per-group ones.
+template <int KIND, int MT, int NB, int D, int EPI>
+__device__ __forceinline__ void skinny_rows_body(const KParams& p) {
+    constexpr bool kAFp4 = KIND == kFP4FP4;
+    constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
+    constexpr bool kBf16 = KIND == kBF16;
+    constexpr int kFmtA = kAFp4 ? kFmtE2M1 : kFmtE4M3;
+    constexpr int kFmtB = kBFp4 ? kFmtE2M1 : kFmtE4M3;
+    constexpr int NW = MT * NB;
+    constexpr int BM = 32 * MT, BN = 32 * NB;
+    static_assert(BM <= 128 && BN <= 128, "one scale dword per lane covers 128 rows");
+    constexpr int RBA = kBf16 ? 128 : (kAFp4 ? 32 : 64);   // bytes of one row per 64-K block
+    constexpr int RBB = kBf16 ? 128 : (kBFp4 ? 32 : 64);
+    constexpr int PA = RBA / 32, PB = RBB / 32;            // 16-byte pieces per lane and block
+    constexpr SkinnyShape kShape = skinny_shape(KIND, MT, NB, BM);
+    constexpr int G = kShape.g, RG = kShape.rg, RGA = kShape.rga;
+    constexpr int SPR = RG / 16, SPRA = RGA / 16;           // 16-byte slots of a B / A row
+    constexpr int RPI = 64 / SPR, RPIA = 64 / SPRA;         // rows per load instruction
+    constexpr int NDMA = BN / RPI, NDMAA = BM / RPIA;       // row-load instructions per group slot
+    constexpr int NLR = NDMA + NDMAA;
+    constexpr int NSF = kBf16 ? 0 : 2 * G;                  // scale-row loads per group (A, B per 64-K block)
+    constexpr int LPR = (NLR + NW - 1) / NW;                // row loads per wave and group
+    constexpr int LPS = (NSF + NW - 1) / NW;                // scale loads per wave and group
+    constexpr int PG = LPR + LPS;                           // vector-memory instructions per wave and group
+    constexpr int SLOTB = BN * RG;
+    constexpr int SCOFF = SLOTB + BM * RGA;                 // scale rows: A blocks, then B blocks, 256 B each
+    constexpr int SLOT = SCOFF + NSF * 256;
+    constexpr int SPARE = (NLR % NW != 0 || NSF % NW != 0) ? 1024 : 0;   // lands dead loads
+    static_assert(BM % RPIA == 0 && BN % RPI == 0, "slot rows");
+    static_assert(D >= 3 && (D - 2) * PG <= 63, "vmcnt range");
+    static_assert(D * SLOT + SPARE <= 160 * 1024, "LDS budget");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[D * SLOT + SPARE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wjm = w % MT, wjn = w / MT;
+    const int r = lane & 31, q = lane >> 5;
+
+    // ------------------------------------------------------------------ strip and K range
+    const int split_k = p.split_k;
+    int t, split = 0;
+    if (split_k > 1) {
+        // grid = 8 * ceil(strips / 8) * split_k; all splits of a strip share blockIdx % 8 (XCD)
+        const int b = blockIdx.x, rr = b >> 3;
+        t = (rr / split_k) * 8 + (b & 7);
+        split = rr % split_k;
+        if (p.split_spread) {
+            t = b / split_k;
+            split = b % split_k;
+        }
+        if (t >= p.num_tiles) return;
+    } else {
+        t = blockIdx.x;
+    }
+    const int tile_id = t;
+    const int nn = p.num_n_blocks;
+    int batch = 0;
+    if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
+        batch = t / nn;
+        t -= batch * nn;
+    }
+    const int n0 = t * BN;
+    const int N = p.n;
+    const int M = __builtin_amdgcn_readfirstlane(p.gemm_type == kMasked ? min(p.m, p.layout[batch]) : p.m);
+    if (M <= 0) return;
+    const uint8_t* a_base = p.a;
+    const uint8_t* b_base = p.b + (int64_t)n0 * p.ldb;
+    const uint16_t* sfa = p.sfa;
+    const uint16_t* sfb = p.sfb;
+    uint8_t* d_base = p.d;
+    if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
+        a_base += (int64_t)batch * p.bsa;
+        b_base += (int64_t)batch * p.bsb;
+        d_base += (int64_t)batch * p.bsd * p.out_esize;
+        if (!kBf16) {
+            sfa += (int64_t)batch * p.sfa_bs;
+            sfb += (int64_t)batch * p.sfb_bs;
+        }
+    }
+    const int rows_a = min(BM, M), rows_b = min(BN, N - n0);
+    const int nk64 = ceil_div(p.k, 64);
+    const int kb0 = split * p.split_stages;
+    const int kb1 = split_k > 1 ? min(nk64, kb0 + p.split_stages) : nk64;
+    const int ng = ceil_div(max(kb1 - kb0, 0), G);   // groups of the workgroup (every wave walks all)
+    const int kbytes_a = p.kbytes_a, kbytes_b = p.kbytes_b;
+
+    // Row loads: the group's NLR instructions are dealt to the waves (wave w issues w, w + NW, ...);
+    // instruction i < NDMA fills B rows [i RPI, +RPI) of the slot, the others A rows.  Everything
+    // wave-uniform about load j (its tensor, LDS offset, row bytes per 64-K block, K row bytes) is
+    // fixed here; a load past NLR is dead (out of range, into the spare kilobyte).
+    // (arrays or conditional expressions of buffer-resource type lose the kernel's host stub, so
+    // each load keeps its tensor's base and size and builds the resource at issue)
+    const uint8_t* ld_base[LPR];
+    int64_t ld_size[LPR];
+    int ld_lds[LPR], ld_rb[LPR], ld_kb[LPR], ld_lk[LPR];
+    uint32_t ld_v[LPR];
+#pragma unroll
+    for (int j = 0; j < LPR; ++j) {
+        const int i = w + j * NW;
+        const bool is_a = i >= NDMA;
+        ld_base[j] = is_a ? a_base : b_base;
+        ld_size[j] = is_a ? (int64_t)rows_a * p.lda : (int64_t)rows_b * p.ldb;
+        ld_rb[j] = is_a ? RBA : RBB;
+        ld_kb[j] = i < NLR ? (is_a ? kbytes_a : kbytes_b) : 0;
+        const int spr = is_a ? SPRA : SPR;
+        const int row = (is_a ? (i - NDMA) * RPIA : i * RPI) + lane / spr;
+        const int sw = is_a ? slot_swizzle<SPRA>(row) : slot_swizzle<SPR>(row);
+        ld_lk[j] = ((lane % spr) ^ sw) * 16;
+        const bool row_ok = row < (is_a ? rows_a : rows_b);
+        ld_v[j] = i < NLR && row_ok ? (uint32_t)(row * (is_a ? p.lda : p.ldb) + ld_lk[j]) : kOOBOffset;
+        ld_lds[j] = i >= NLR ? D * SLOT : (is_a ? SLOTB + (i - NDMA) * 1024 : i * 1024);
+    }
+    // Scale loads: load j of this wave is scale row s = w + j NW of the group (s < G: A's packed
+    // int16 pairs of 64-K block s, else B's of block s - G), one dword = two rows per lane.
+    const uint16_t* sc_base[LPS > 0 ? LPS : 1];
+    int64_t sc_size[LPS > 0 ? LPS : 1];
+    int sc_lds[LPS > 0 ? LPS : 1], sc_blk[LPS > 0 ? LPS : 1], sc_step[LPS > 0 ? LPS : 1];
+    uint32_t sc_v[LPS > 0 ? LPS : 1];
+    if constexpr (LPS > 0) {
+#pragma unroll
+        for (int j = 0; j < LPS; ++j) {
+            const int s = w + j * NW;
+            const bool is_a = s < G;
+            sc_base[j] = is_a ? sfa : sfb + n0;
+            sc_size[j] = is_a ? (int64_t)nk64 * p.sfa_ld * 2 : ((int64_t)nk64 * p.sfb_ld - n0) * 2;
+            sc_step[j] = (int)(is_a ? p.sfa_ld : p.sfb_ld) * 2;
+            sc_blk[j] = is_a ? s : s - G;
+            sc_v[j] = s < NSF && 2 * lane < (is_a ? rows_a : rows_b) ? (uint32_t)(lane * 4) : kOOBOffset;
+            sc_lds[j] = s < NSF ? SCOFF + s * 256 : D * SLOT;
+        }
+    }
+
+    // Group gi (64-K blocks kb0 + gi G + j) into ring slot `slot`; a group past the range (or a
+    // piece past K or past the split's end) loads zeros with no memory traffic.
+    auto load_group = [&](int slot, int gi) {
+        const bool live = gi < ng;
+        const int kbg = kb0 + gi * G;
+        uint8_t* const sbase = smem + slot * SLOT;
+#pragma unroll
+        for (int j = 0; j < LPR; ++j) {
+            const int left = live ? ld_kb[j] - kbg * ld_rb[j] : 0;
+            const int kend = (kb1 - kbg) * ld_rb[j];
+            const uint32_t v = ld_lk[j] < left && ld_lk[j] < kend ? ld_v[j] : kOOBOffset;
+            uint8_t* dst = ld_lds[j] >= D * SLOT ? smem + D * SLOT : sbase + ld_lds[j];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(ld_base[j], ld_size[j]), (lds_void*)dst, 16, v,
+                                                     __builtin_amdgcn_readfirstlane(kbg * ld_rb[j]), 0, 0);
+        }
+        if constexpr (LPS > 0) {
+#pragma unroll
+            for (int j = 0; j < LPS; ++j) {
+                const int kb = kbg + sc_blk[j];
+                const bool on = live && kb < kb1;
+                uint8_t* dst = sc_lds[j] >= D * SLOT ? smem + D * SLOT : sbase + sc_lds[j];
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(sc_base[j], sc_size[j]), (lds_void*)dst, 4,
+                                                         on ? sc_v[j] : kOOBOffset,
+                                                         __builtin_amdgcn_readfirstlane(on ? kb * sc_step[j] : 0), 0, 0);
+            }
+        }
+    };
+
+    f32x16 acc = f32x16{};
+    const int RBr = wjn * 32 + r, RAr = wjm * 32 + r;
+    auto compute = [&](int slot) {
+        const uint8_t* sb_ = smem + slot * SLOT;
+        i32x4 fb[G][PB], fa[G][PA];
+        int sca[G], scb[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+#pragma unroll
+            for (int P = 0; P < PB; ++P) {
+                const int sl = (j * RBB + 32 * P) / 16 + q;
+                fb[j][P] = *reinterpret_cast<const i32x4*>(sb_ + RBr * RG + ((sl ^ slot_swizzle<SPR>(RBr)) << 4));
+            }
+#pragma unroll
+            for (int P = 0; P < PA; ++P) {
+                const int sl = (j * RBA + 32 * P) / 16 + q;
+                fa[j][P] = *reinterpret_cast<const i32x4*>(sb_ + SLOTB + RAr * RGA + ((sl ^ slot_swizzle<SPRA>(RAr)) << 4));
+            }
+            if constexpr (!kBf16) {
+                sca[j] = sb_[SCOFF + j * 256 + RAr * 2 + q];
+                scb[j] = sb_[SCOFF + (G + j) * 256 + RBr * 2 + q];
+            }
+        }
+        static_for<G>([&](auto j_c) {
+            constexpr int j = decltype(j_c)::value;
+            if constexpr (kBf16) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fb[j][s]),
+                                                                  __builtin_bit_cast(bf16x8, fa[j][s]), acc, 0, 0, 0);
+            } else {
+                const i32x4 b0 = fb[j][0], a0 = fa[j][0];
+                i32x4 b1 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+                if constexpr (PB > 1) b1 = fb[j][1];
+                if constexpr (PA > 1) a1 = fa[j][1];
+                const i32x8 bf = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+                const i32x8 af = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+                acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf, af, acc, kFmtB, kFmtA, 0, scb[j], 0, sca[j]);
+            }
+        });
+    };
+
+    // ------------------------------------------------------------------ main loop
+    // Groups 0 .. D-2 in flight; then per group g: wait for this wave's share of g, barrier (g is
+    // complete in LDS and slot (g - 1) % D is read by every wave), refill that slot with group
+    // g + D - 1, compute g.  The wait count holds because every wave issues exactly PG
+    // vector-memory instructions per group, in group order.
+    for (int g = 0; g < D - 1; ++g) load_group(g, g);
+    int slot = 0;
+    for (int g = 0; g < ng; ++g) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((D - 2) * PG) : "memory");
+        stage_barrier();
+        load_group(slot == 0 ? D - 1 : slot - 1, g + D - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(slot);
+        __builtin_amdgcn_sched_barrier(0);
+        slot = slot + 1 == D ? 0 : slot + 1;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    const int m = wjm * 32 + r;
+    // ------------------------------------------------------------------ split-K across workgroups
+    if (split_k > 1) {
+        constexpr int NBLK = NW;
+        float* const tile_ws = p.ws + (int64_t)tile_id * split_k * (NBLK * 1024);
+        const __amdgpu_buffer_rsrc_t rs_ws = make_rsrc(tile_ws, (int64_t)split_k * NBLK * 1024 * 4);
+        const int blk = wjn * MT + wjm;
+        auto part_off = [&](int sp) -> uint32_t {
+            return m < M ? (uint32_t)((sp * NBLK + blk) * 1024 + lane * 16) * 4u : kOOBOffset;
+        };
+        {
+            const uint32_t off = part_off(split);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(u32x4, f32x4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]}), rs_ws,
+                    off + 16 * g, 0, kCacheSc1);
+        }
+        // Arrival count: device-scope partial stores and loads, no fence (the memory-model argument
+        // of skinny_kernel's split-K).
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        int* flag = reinterpret_cast<int*>(smem);
+        if (tid == 0)
+            *flag = __hip_atomic_fetch_add(p.counters + tile_id, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (*flag != split_k - 1) return;
+        acc = f32x16{};
+        for (int sp = 0; sp < split_k; ++sp) {
+            const uint32_t off = part_off(sp);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 v =
+                    __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_ws, off + 16 * g, 0, kCacheSc1));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[4 * g + i] += v[i];
+            }
+        }
+        if (tid == 0) __hip_atomic_store(p.counters + tile_id, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // ------------------------------------------------------------------ epilogue
+    epilogue_block<EPI>(p, acc, d_base, m, m < M, false, n0 + wjn * 32, N, batch, q);
+}
+
+// (the body lives in a device function: written directly in the kernel, clang's host pass at -O1
+// and above emitted no launch stub for it)
+template <int KIND, int MT, int NB, int D, int EPI>
+__global__ __launch_bounds__(MT * NB * 64, 1) void skinny_rows_kernel(const KParams p) {
+    skinny_rows_body<KIND, MT, NB, D, EPI>(p);
+}
+
+}  // namespace dg

@@ -31,7 +31,41 @@ KernelFn skinny_find(int mt, int nb, int nw, int d, int ar, int epi) {
     }
 }
 
+template <int I, int KIND>
+KernelFn rows_epi(int epi) {
+    constexpr SkinnyRowsCfg c = kSkinnyRows[I];
+    switch (epi) {
+        case kEpiF32: return &skinny_rows_kernel<KIND, c.mt, c.nb, c.d, kEpiF32>;
+        case kEpiBf16: return &skinny_rows_kernel<KIND, c.mt, c.nb, c.d, kEpiBf16>;
+        case kEpiBf16SR: return &skinny_rows_kernel<KIND, c.mt, c.nb, c.d, kEpiBf16SR>;
+        case kEpiFp8:
+            if constexpr (KIND == kFP8FP8) return &skinny_rows_kernel<KIND, c.mt, c.nb, c.d, kEpiFp8>;
+            else return nullptr;
+        default: return nullptr;
+    }
+}
+
+template <int KIND, int I = 0>
+KernelFn rows_find(int mt, int nb, int d, int epi) {
+    if constexpr (I == kNumSkinnyRows) {
+        return nullptr;
+    } else {
+        if (mt == kSkinnyRows[I].mt && nb == kSkinnyRows[I].nb && d == kSkinnyRows[I].d) return rows_epi<I, KIND>(epi);
+        return rows_find<KIND, I + 1>(mt, nb, d, epi);
+    }
+}
+
 }  // namespace
+
+KernelFn lookup_skinny_rows(int kind, int mt, int nb, int d, int epi) {
+    switch (kind) {
+        case kFP8FP8: return rows_find<kFP8FP8>(mt, nb, d, epi);
+        case kFP8FP4: return rows_find<kFP8FP4>(mt, nb, d, epi);
+        case kFP4FP4: return rows_find<kFP4FP4>(mt, nb, d, epi);
+        case kBF16: return rows_find<kBF16>(mt, nb, d, epi);
+        default: return nullptr;
+    }
+}
 
 KernelFn lookup_skinny(int kind, int mt, int nb, int nw, int d, int ar, int epi) {
     switch (kind) {

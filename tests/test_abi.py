@@ -133,6 +133,13 @@ def test_launch_plan_without_device(lib):
     small = _lib.LaunchInfo()
     assert lib.dg_launch_plan(_plan_args(1, 2112, 7168, 64), ctypes.byref(small)) == 0, lib.dg_last_error()
     assert small.skinny == 1 and small.persistent == 0
+    # decode shapes with 64 < M <= 128 and K <= 8192 take the shared-ring decode kernel
+    mid = _lib.LaunchInfo()
+    assert lib.dg_launch_plan(_plan_args(128, 2112, 7168, 0), ctypes.byref(mid)) == 0, lib.dg_last_error()
+    assert mid.skinny == 2 and mid.threads == 256 and mid.block_m == 128 and mid.block_n == 32
+    long_k = _lib.LaunchInfo()
+    assert lib.dg_launch_plan(_plan_args(128, 7168, 16384, 0), ctypes.byref(long_k)) == 0, lib.dg_last_error()
+    assert long_k.skinny == 1
     assert lib.dg_launch_plan(None, None) == -1
 
 
