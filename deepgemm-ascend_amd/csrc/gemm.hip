@@ -190,14 +190,15 @@ SkinnyEnv skinny_env() {
 bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const SkinnyEnv& env, Plan& out) {
     if (env.mode == 0 || !(a.gemm_type == kNormal || a.gemm_type == kBatched || a.gemm_type == kMasked)) return false;
     const int groups0 = a.gemm_type == kNormal ? 1 : a.num_groups;
-    // Decode shapes with 64 < M <= 128 and K <= 8192 (dense or batched) take the shared-ring kernel:
+    // FP8 decode shapes with 64 < M <= 128 and K <= 8192 (dense or batched) take the shared-ring kernel:
     // its waves own the tile's four 32-row blocks and fetch each group of B and A once per
     // workgroup, four groups deep.  Measured on MI355X (fp8, cold L2, event us, skinny kernel in
     // brackets): 128x2112x7168 21.9 (24.8), 128x4096x7168 26.8 (30.0), 128x7168x2048 15.0 (17.0),
     // 96x4096x7168 24.5 (27.6); slower at K = 16384 (87.5 vs 74.5) and for M <= 64 (64x2112x7168
-    // 18.6 vs 17.4), which keep the skinny kernel.
+    // 18.6 vs 17.4), which keep the skinny kernel, as do bf16 and FP4-B operands (no gain measured:
+    // bf16 128x4096x7168 29.9 vs 29.0 kernel us).
     SkinnyEnv rows_env = env;
-    if (env.rows == -1 && env.mode == -1 && a.m > 64 && a.m <= 128 && a.k <= 8192 &&
+    if (env.rows == -1 && env.mode == -1 && a.kind == kFP8FP8 && a.m > 64 && a.m <= 128 && a.k <= 8192 &&
         (a.gemm_type == kNormal || a.gemm_type == kBatched) && (int64_t)ceil_div(a.n, 32) * groups0 <= 2 * (int64_t)cus) {
         rows_env.rows = 1;
         rows_env.rmt = 4; rows_env.rnb = 1; rows_env.rd = 4; rows_env.rsplit = 0;
