@@ -536,9 +536,19 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     if (kbytes_a % 16 || kbytes_b % 16 || lda_b % 16 || ldb_b % 16 ||
         (reinterpret_cast<uintptr_t>(a.a) & 15) || (reinterpret_cast<uintptr_t>(a.b) & 15))
         return dg_set_error("dg_gemm: K rows and strides must be 16-byte aligned (host pads otherwise)");
-    if (lda_b < kbytes_a || ldb_b < kbytes_b || a.ldd < a.n)
+    // MN-major operands ([K][MN] storage, read in place by the 128-K-stage tile kernels)
+    const bool amn = a.a_mn_major != 0, bmn = a.b_mn_major != 0;
+    if ((amn || bmn) && (a.kind != kFP8FP8 || a.jit ||
+                         !(a.gemm_type == kNormal || a.gemm_type == kBatched || a.gemm_type == kKGrouped))) {
+        dg_set_error("dg_gemm: MN-major operands are read in place only by e4m3 dense, batched and K-grouped "
+                     "ahead-of-time kernels");
+        return DG_ENOKERNEL;
+    }
+    if ((amn ? lda_b < a.m : lda_b < kbytes_a) || (bmn ? ldb_b < a.n : ldb_b < kbytes_b) || a.ldd < a.n)
         return dg_set_error("dg_gemm: leading dimension smaller than the row");
-    if ((int64_t)256 * lda_b > 0x7fffffffLL || (int64_t)256 * ldb_b > 0x7fffffffLL)
+    // (an MN-major operand's whole K extent must fit a buffer range below the dead-load offset)
+    if ((amn ? (int64_t)a.k * lda_b >= 0x40000000LL : (int64_t)256 * lda_b > 0x7fffffffLL) ||
+        (bmn ? (int64_t)a.k * ldb_b >= 0x40000000LL : (int64_t)256 * ldb_b > 0x7fffffffLL))
         return dg_set_error("dg_gemm: row stride too large for 32-bit tile offsets");
     if (!bf16 && ((a.sfa_ld | a.sfb_ld | a.sfa_batch_stride | a.sfb_batch_stride) & 1))
         return dg_set_error("dg_gemm: SF leading dimensions and batch strides must be even (int16 elements)");
@@ -562,6 +572,12 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     }
     const TileCfg cfg = plan.tile;
     if (cfg.bm == 0) return dg_set_error("dg_gemm: no tile shape fits this problem");
+    if ((amn || bmn) && (plan.skinny_nw > 0 || plan.split != 1 || cfg.km != 2 || cfg.stages != 2 || cfg.bm > 256 ||
+                         cfg.bn > 256 || tile_anchored(cfg.bm))) {
+        dg_set_error("dg_gemm: MN-major operands need a 128-K-stage tile plan (large M and N); this problem "
+                     "plans another kernel");
+        return DG_ENOKERNEL;
+    }
     if (!tile_allowed(a, cfg.bm, cfg.bn)) return dg_set_error("dg_gemm: block_m must divide the M-grouped alignment");
     // Direct register stores measured faster than staging the tile through LDS.
     const int epi_kind = a.d_dtype == DG_DTYPE_F32 ? kEpiF32
@@ -585,12 +601,13 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     // one tile per workgroup at full occupancy (the same ring, the epilogue still not overlapped).
     static const char* persist_env = std::getenv("DG_PERSISTENT");
     const bool want_persistent = cus_capped(cus) || (persist_env != nullptr && persist_env[0] == '1');
-    const bool persistent = want_persistent && !jit && !skinny && plan.split == 1 && tile_persistable(cfg) &&
+    const bool persistent = want_persistent && !jit && !skinny && !amn && !bmn && plan.split == 1 && tile_persistable(cfg) &&
                             a.k > 0 && a.gemm_type != kKGrouped && a_span <= 0x7fffffffLL &&
                             b_span <= 0x7fffffffLL && sfa_span <= 0x7fffffffLL && sfb_span <= 0x7fffffffLL;
     KernelFn fn = jit ? nullptr
                 : skinny ? (plan.skinny_rows ? lookup_skinny_rows(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_d, epi_kind)
                                              : lookup_skinny(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_nw, plan.skinny_d, plan.skinny_ar, epi_kind))
+                : (amn || bmn) ? lookup_kernel_fp8fp8_mn(cfg.bm, cfg.bn, epi_kind, amn, bmn)
                          : lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind, persistent);
     if (fn == nullptr && !jit) {
         char buf[160];

@@ -502,7 +502,7 @@ __device__ __forceinline__ void epilogue_block(const KParams& p, const f32x16& a
 // time (-1 / 0 = read from the arguments): the ahead-of-time menu reads everything from the
 // arguments, the JIT compiles one body per problem (csrc/jit.hip).
 template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI, int CT = -1,
-          int CS = 0, int CM = 0, int CN = 0, int CK = 0>
+          int CS = 0, int CM = 0, int CN = 0, int CK = 0, bool AMN = false, bool BMN = false>
 __device__ __forceinline__ void gemm_body(const KParams& p) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
@@ -547,7 +547,14 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     static_assert((NW == 4 || NW == 8) && WGM * WGN == NW && TM >= 1 && TN >= 1 && TM * 32 == WM &&
                       TN_LAST >= 1 && (WGN - 1) * WN + TN_LAST * 32 == BN, "wave tiling");
     static_assert(!kRagged || (NW == 8 && LW == 4 && WGM == 4 && WGN == 2), "ragged tiling needs the loader waves as its last column");
-    constexpr int A_BYTES = BM * RBA, B_BYTES = BN * RBB;
+    // MN-major operands (AMN / BMN: A [K][M] / B [K][N], MN contiguous; e4m3, 128-K stages): a stage
+    // holds the tile's 128 K rows of up to 256 MN bytes each, in 256-byte LDS rows whose 16-byte
+    // pieces are XOR-swizzled by 2 (k % 8); fragments are read with ds_read_b64_tr_b8, which hands
+    // each lane 8 consecutive K of one MN row, so the MFMA operands equal the K-major path's.
+    static_assert((!AMN && !BMN) || (KIND == kFP8FP8 && KM == 2 && NSTAGE == 2 && BM <= 256 && BN <= 256),
+                  "MN-major operands: e4m3, 128-K stages, tiles of at most 256 x 256");
+    constexpr int MN_PITCH = 256, MN_KROWS = 64 * KM;     // an MN-major stage: 128 K rows x 256 bytes
+    constexpr int A_BYTES = AMN ? MN_KROWS * MN_PITCH : BM * RBA, B_BYTES = BMN ? MN_KROWS * MN_PITCH : BN * RBB;
     constexpr int SCA = kBf16 ? 0 : (BM * 2 + 255) / 256 * 256;   // one packed int16 per row and sub-step
     constexpr int SCB = kBf16 ? 0 : (BN * 2 + 255) / 256 * 256;
     constexpr int SCU = SCA + SCB;                                 // scale bytes of one sub-step
@@ -638,8 +645,8 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         const int ks = batch == 0 ? 0 : align_up(p.layout[batch - 1], p.alignment);
         k_len = __builtin_amdgcn_readfirstlane(max(0, p.layout[batch] - ks));
         const int kso = __builtin_amdgcn_readfirstlane(ks);
-        a_base += (int64_t)kso * (kAFp4 ? 1 : (kBf16 ? 4 : 2)) / 2;
-        b_base += (int64_t)kso * (kBFp4 ? 1 : (kBf16 ? 4 : 2)) / 2;
+        a_base += AMN ? (int64_t)kso * p.lda : (int64_t)kso * (kAFp4 ? 1 : (kBf16 ? 4 : 2)) / 2;
+        b_base += BMN ? (int64_t)kso * p.ldb : (int64_t)kso * (kBFp4 ? 1 : (kBf16 ? 4 : 2)) / 2;
         if (!kBf16) {
             sfa += (int64_t)(kso / 64) * p.sfa_ld;
             sfb += (int64_t)(kso / 64) * p.sfb_ld;
@@ -715,8 +722,12 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     const int rows_a = anchored ? min(BM, valid_end - m0) : min(BM, M - m0);
     const int rows_b = min(BN, N - n0);
     const int64_t lda = p.lda, ldb = p.ldb;
-    const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(a_base + (int64_t)m0 * lda, (int64_t)rows_a * lda);
-    const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(b_base + (int64_t)n0 * ldb, (int64_t)rows_b * ldb);
+    // (MN-major: the tile's first column is the base and the K rows of the contraction bound the
+    // range, so K rows past the end read zeros)
+    const __amdgpu_buffer_rsrc_t rs_a = AMN ? make_rsrc(a_base + m0, (int64_t)k_len * lda - m0)
+                                            : make_rsrc(a_base + (int64_t)m0 * lda, (int64_t)rows_a * lda);
+    const __amdgpu_buffer_rsrc_t rs_b = BMN ? make_rsrc(b_base + n0, (int64_t)k_len * ldb - n0)
+                                            : make_rsrc(b_base + (int64_t)n0 * ldb, (int64_t)rows_b * ldb);
     // (bytes of one K row: storage bytes per two K elements x K / 2)
     const int kbytes_a = gemm_type == kKGrouped || CK > 0 ? k_len * (kAFp4 ? 1 : (kBf16 ? 4 : 2)) / 2 : p.kbytes_a;
     const int kbytes_b = gemm_type == kKGrouped || CK > 0 ? k_len * (kBFp4 ? 1 : (kBf16 ? 4 : 2)) / 2 : p.kbytes_b;
@@ -735,7 +746,7 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     // Operand rows: each wave-level buffer_load_dwordx4 ... lds fills 1 KB (64 lanes x 16 B)
     // of a stage; lane slots map to swizzled (row, 16-byte K piece) positions.  The stage's K
     // offset rides in the scalar soffset, so the per-lane voffset is stage-invariant.
-    constexpr int SLA = BM * SPRA, SLB = BN * SPRB;                    // 16-byte slots per stage
+    constexpr int SLA = AMN ? MN_KROWS * 16 : BM * SPRA, SLB = BMN ? MN_KROWS * 16 : BN * SPRB;   // 16-byte slots per stage
     constexpr int NLA = (SLA + LT - 1) / LT, NLB = (SLB + LT - 1) / LT;  // per-thread loads
     // Packed SF rows: one buffer_load_dword ... lds per 128 rows of the tile and sub-step,
     // issued by waves 0 .. NSCA-1 (A) and NSCA .. NSCA+NSCB-1 (B).
@@ -754,9 +765,15 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         lk_b = ((ltid % SPRB) ^ slot_swizzle<SPRB>(row_b)) * 16;
         vbase_a = row_a < rows_a ? (uint32_t)(row_a * lda + lk_a) : kOOBOffset;
         vbase_b = row_b < rows_b ? (uint32_t)(row_b * ldb + lk_b) : kOOBOffset;
+        // MN-major: LDS slot ltid = K row ltid / 16, piece ltid % 16 of the swizzled 256-byte row,
+        // which holds MN bytes [16 pp, 16 pp + 16) with pp = piece ^ 2 (k % 8); pieces past the
+        // tile's MN extent read zeros
+        const int kr = ltid / 16, pp = (ltid % 16) ^ ((kr & 7) << 1);
+        if constexpr (AMN) vbase_a = pp * 16 < rows_a ? (uint32_t)(kr * lda + pp * 16) : kOOBOffset;
+        if constexpr (BMN) vbase_b = pp * 16 < rows_b ? (uint32_t)(kr * ldb + pp * 16) : kOOBOffset;
     }
-    const int vstep_a = __builtin_amdgcn_readfirstlane((int)((LT / SPRA) * lda));
-    const int vstep_b = __builtin_amdgcn_readfirstlane((int)((LT / SPRB) * ldb));
+    const int vstep_a = __builtin_amdgcn_readfirstlane((int)(AMN ? (LT / 16) * lda : (LT / SPRA) * lda));
+    const int vstep_b = __builtin_amdgcn_readfirstlane((int)(BMN ? (LT / 16) * ldb : (LT / SPRB) * ldb));
     // Per-wave packed-SF load of a stage: loader wave w < NSCA fetches A rows [128 w, 128 w + 128),
     // loader waves NSCA .. NSCA+NSCB-1 the B rows; the other waves issue a dead (out-of-range) load
     // into an idle word so that every wave runs the same branch-free instruction stream.
@@ -790,11 +807,13 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
             constexpr int SL = kIsA ? SLA : SLB;
             constexpr int RB = kIsA ? RBA : RBB;
             if (SL % LT != 0 && it * LT + lwave * 64 >= SL) return;
-            const int kb = c * RB;
-            const int krem = (kIsA ? kbytes_a : kbytes_b) - kb;
+            constexpr bool kMN = kIsA ? AMN : BMN;
+            const int kb = kMN ? c * MN_KROWS * (int)(kIsA ? lda : ldb) : c * RB;
+            const int krem = (kIsA ? kbytes_a : kbytes_b) - c * RB;
             // Rows past a ragged tile's edge fall outside the tile's buffer range and read zeros.
-            // The item's row step rides in the scalar offset with the stage's K offset.
-            const uint32_t voff = (kIsA ? lk_a : lk_b) < krem ? (kIsA ? vbase_a : vbase_b) : kOOBOffset;
+            // The item's row step rides in the scalar offset with the stage's K offset.  (MN-major:
+            // K rows past the end fall outside the range instead.)
+            const uint32_t voff = kMN || (kIsA ? lk_a : lk_b) < krem ? (kIsA ? vbase_a : vbase_b) : kOOBOffset;
             const int soff = kb + it * (kIsA ? vstep_a : vstep_b);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 kIsA ? rs_a : rs_b, (lds_void*)(sbase + (kIsA ? 0 : A_BYTES) + (it * LT + lwave * 64) * 16), 16,
@@ -833,6 +852,25 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
             return i32x8{lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
         }
     };
+    // MN-major operand block starting at MN row R0 (its lane (r, q) = row R0 + r): four
+    // ds_read_b64_tr_b8 reads.  In each 16-lane group (lanes 16 g + i, g = 2 q + h) lane s supplies
+    // the 8-byte chunk of K row kb + s / 2 at MN bytes R0 + 16 h + 8 (s % 2); the read hands lane i
+    // byte i % 8 of chunk 2 j + i / 8 as its byte j, i.e. K kb .. kb + 7 of MN row R0 + 16 h + i.
+    // The four reads cover K [16 q, +8), [16 q + 8, +8), [32 + 16 q, +8), [40 + 16 q, +8) of the
+    // sub-step: the K-major fragment's bytes in order.
+    auto load_frag_mn = [&](const uint8_t* base, int R0, auto u_tag) -> i32x8 {
+        constexpr int u = decltype(u_tag)::value;
+        const int s16 = lane & 15, h = (lane >> 4) & 1;
+        const int pp = ((R0 + 16 * h) >> 4) ^ (((s16 >> 1) & 7) << 1);
+        const uint8_t* b0 = base + (u * 64 + 16 * q + (s16 >> 1)) * MN_PITCH + (pp << 4) + (s16 & 1) * 8;
+        typedef int v2i __attribute__((ext_vector_type(2)));
+        typedef __attribute__((address_space(3))) v2i lds_v2i;
+        const v2i e0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0));
+        const v2i e1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0 + 8 * MN_PITCH));
+        const v2i e2 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0 + 32 * MN_PITCH));
+        const v2i e3 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0 + 40 * MN_PITCH));
+        return i32x8{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+    };
     // UE8M0 byte of K-block q of row R (one packed int16 per row in the sub-step's scale area,
     // K-block 0 in the low byte): a byte read, consumed by the MFMA as it is.
     auto load_scale = [&](const uint8_t* sc, int R) -> int { return sc[R * 2 + q]; };
@@ -857,10 +895,12 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         const uint8_t* sc = st + A_BYTES + B_BYTES + u * SCU;
         if constexpr (part < TM) {
             const int R = wm * WM + part * 32 + r;
-            return Pair<i32x8, int>{load_frag(st, R, Int<SPRA>{}, u_tag), kBf16 ? 0 : load_scale(sc, R)};
+            if constexpr (AMN) return Pair<i32x8, int>{load_frag_mn(st, R - r, u_tag), load_scale(sc, R)};
+            else return Pair<i32x8, int>{load_frag(st, R, Int<SPRA>{}, u_tag), kBf16 ? 0 : load_scale(sc, R)};
         } else {
             const int R = wn * WN + r;
-            return Pair<i32x8, int>{load_frag(st + A_BYTES, R, Int<SPRB>{}, u_tag),
+            if constexpr (BMN) return Pair<i32x8, int>{load_frag_mn(st + A_BYTES, R - r, u_tag), load_scale(sc + SCA, R)};
+            else return Pair<i32x8, int>{load_frag(st + A_BYTES, R, Int<SPRB>{}, u_tag),
                                          kBf16 ? 0 : load_scale(sc + SCA, R)};
         }
     };
@@ -898,7 +938,8 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
             i32x8 fb_next = fb_cur;
             int sb_next = sb_cur;
             if constexpr (jn + 1 < TNX) {
-                fb_next = load_frag(sB, wn * WN + (jn + 1) * 32 + r, Int<SPRB>{}, u_tag);
+                if constexpr (BMN) fb_next = load_frag_mn(sB, wn * WN + (jn + 1) * 32, u_tag);
+                else fb_next = load_frag(sB, wn * WN + (jn + 1) * 32 + r, Int<SPRB>{}, u_tag);
                 if constexpr (!kBf16) sb_next = load_scale(sSB, wn * WN + (jn + 1) * 32 + r);
             }
             if constexpr (kLate && u + 1 == KM && jn + 1 == TNX) {
@@ -1140,9 +1181,10 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
 }
 
 // The ahead-of-time kernel of one tile shape: everything from the arguments.
-template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI>
+template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI, bool AMN = false,
+          bool BMN = false>
 __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KParams p) {
-    gemm_body<BM, BN, WGM, NW, LW, NSTAGE, KM, OCC, KIND, EPI>(p);
+    gemm_body<BM, BN, WGM, NW, LW, NSTAGE, KM, OCC, KIND, EPI, -1, 0, 0, 0, 0, AMN, BMN>(p);
 }
 
 }  // namespace dg

@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = ('dg_gemm', 'dg_transform_sf', 'dg_transform_k_grouped_sf', '
 
 # Sticky error bits kernels report through host-mapped words (DG_ERR_* in the header)
 DG_ERR_SF_INVALID, DG_ERR_M_INDICES = 1, 2
+DG_ENOKERNEL = -3   # dg_gemm: no compiled kernel for the requested configuration
 
 
 class GemmArgs(ctypes.Structure):
@@ -48,6 +49,7 @@ class GemmArgs(ctypes.Structure):
         ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_int64),
         ('epilogue', ctypes.c_int32), ('sfd', ctypes.c_void_p), ('sfd_ld', ctypes.c_int64),
         ('jit', ctypes.c_int32), ('compiled_dims', ctypes.c_int32), ('library_workspace', ctypes.c_int32),
+        ('a_mn_major', ctypes.c_int32), ('b_mn_major', ctypes.c_int32),
     ]
 
 

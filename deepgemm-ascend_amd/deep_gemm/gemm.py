@@ -108,6 +108,51 @@ def _transpose_to_k_major(t: torch.Tensor, k: int) -> torch.Tensor:
     return out
 
 
+def _mn_in_place(t: torch.Tensor, k: int) -> bool:
+    """An e4m3 MN-major operand ([.., MN, K] view with stride(-2) == 1) that the tile kernels can read
+    in place: 16-byte aligned K rows and K a multiple of 16.  DG_MN_COPY=1 (tuning, tests) always
+    copies instead."""
+    if t.dtype != torch.float8_e4m3fn or _major_is_k(t) or os.environ.get('DG_MN_COPY') == '1':
+        return False
+    if k % 16 or t.size(-1) < 2 or t.stride(-2) != 1 or t.stride(-1) % 16 or t.stride(-1) < t.size(-2):
+        return False
+    return t.data_ptr() % 16 == 0 and (t.dim() == 2 or t.stride(0) % 16 == 0)
+
+
+def _launch_operands(args: _lib.GemmArgs, d: torch.Tensor, a: torch.Tensor, b: torch.Tensor, k: int,
+                     batched: bool) -> None:
+    """Set A and B (strides, batch strides, K) and launch.  e4m3 MN-major operands are read in place
+    by the 128-K-stage tile kernels (the reference takes operand majors as kernel parameters,
+    deep_gemm/include/deep_gemm/fp8_gemm.hpp:18-35); a plan with another kernel (DG_ENOKERNEL) and
+    every other operand get a K-major copy."""
+    if args.kind == _lib.DG_KIND_FP8_FP8 and not get_dry_run() and not args.jit:
+        a_mn, b_mn = _mn_in_place(a, k), _mn_in_place(b, k)
+        if a_mn or b_mn:
+            a_k = a if a_mn else _to_kernel_operand(a, k)
+            b_k = b if b_mn else _to_kernel_operand(b, k)
+            if (a_mn or a_k.size(-1) == k) and (b_mn or b_k.size(-1) == k):
+                args.k = k
+                args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
+                args.lda = a_k.stride(-1) if a_mn else a_k.stride(-2)
+                args.ldb = b_k.stride(-1) if b_mn else b_k.stride(-2)
+                if batched:
+                    args.batch_stride_a, args.batch_stride_b = a_k.stride(0), b_k.stride(0)
+                args.a_mn_major, args.b_mn_major = int(a_mn), int(b_mn)
+                if _launch(args, d, allow_no_kernel=True):
+                    return
+                args.a_mn_major = args.b_mn_major = 0
+    a_k = _to_kernel_operand(a, k)
+    b_k = _to_kernel_operand(b, k)
+    k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
+    a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
+    args.k = k_kernel
+    args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
+    args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
+    if batched:
+        args.batch_stride_a, args.batch_stride_b = a_k.stride(0), b_k.stride(0)
+    _launch(args, d)
+
+
 _raw_stream = getattr(torch._C, '_cuda_getCurrentRawStream', None)
 
 
@@ -175,7 +220,9 @@ def _fast_gemm(gemm_type, a, sfa, b, sfb, d, c, layout, recipes) -> bool:
                     _stream(d))
 
 
-def _launch(args: _lib.GemmArgs, d: torch.Tensor) -> None:
+def _launch(args: _lib.GemmArgs, d: torch.Tensor, allow_no_kernel: bool = False) -> bool:
+    """Launch (or, in a dry run, compile); with allow_no_kernel a plan without a compiled kernel
+    returns False instead of raising."""
     _lib.raise_pending()
     if get_dry_run():
         # the reference's dry run compiles the kernel without loading or launching it
@@ -183,7 +230,7 @@ def _launch(args: _lib.GemmArgs, d: torch.Tensor) -> None:
         if args.jit:
             lib = _lib.load()
             _lib.check(lib.dg_jit_compile(args), lib)
-        return
+        return True
     lib = _lib.load()
     stream = _stream(d)
     forced = os.environ.get('DG_SPLIT_K')   # tuning override: 1 = never split, n > 1 = split n ways
@@ -193,7 +240,11 @@ def _launch(args: _lib.GemmArgs, d: torch.Tensor) -> None:
         # split-K partials and tile counters go to the library's workspace of this stream (grown
         # only outside graph capture, never freed)
         args.library_workspace = 1
-    _lib.check(lib.dg_gemm(args, stream), lib)
+    rc = lib.dg_gemm(args, stream)
+    if allow_no_kernel and rc == _lib.DG_ENOKERNEL:
+        return False
+    _lib.check(rc, lib)
+    return True
 
 
 def _fill_common(args, d, k_kernel, alpha, kind, dims: str = 'nk'):
@@ -290,24 +341,13 @@ def _dense_gemm(a, sfa, b, sfb, d, c, recipe, recipe_a, recipe_b, disable_ue8m0_
         sfb_t = transform_sf_into_required_layout(sfb, n, k, rb, None, False, disable_ue8m0_cast)
         args.sfa, args.sfb = sfa_t.data_ptr(), sfb_t.data_ptr()
         args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
-    a_k = _to_kernel_operand(a, k)
-    b_k = _to_kernel_operand(b, k)
-    k_kernel = a_k.size(-1) * (2 if _is_fp4(a_k) else 1)
-    k_kernel_b = b_k.size(-1) * (2 if _is_fp4(b_k) else 1)
-    k_kernel = max(k_kernel, k_kernel_b)
-    if k_kernel != a_k.size(-1) * (2 if _is_fp4(a_k) else 1) or k_kernel != k_kernel_b:
-        # keep both operands on the same padded K
-        a_k = _pad_k(a_k, k_kernel)
-        b_k = _pad_k(b_k, k_kernel)
-    _fill_common(args, d, k_kernel, alpha_v, kind, dims)
+    _fill_common(args, d, k, alpha_v, kind, dims)
     args.gemm_type = _lib.DG_GEMM_NORMAL
-    args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
-    args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
     args.m, args.n, args.num_groups = m, n, 1
     args.accumulate = 1 if is_cd_same else 0
     args.bias = c.data_ptr() if with_bias else None
     _apply_epilogue(args, epi)
-    _launch(args, d)
+    _launch_operands(args, d, a, b, k, batched=False)
 
 
 def _pad_k(t: torch.Tensor, k: int) -> torch.Tensor:
@@ -575,19 +615,13 @@ def _batched(a, sfa, b, sfb, d, c, recipe, bf16: bool, epilogue=None, dims: str 
         args.sfa_batch_stride, args.sfb_batch_stride = sfa_t.stride(0), sfb_t.stride(0)
     if c is not None and not is_cd_same:
         d.copy_(c)   # the reference's legacy accumulation path (csrc/utils/layout.hpp:82-84)
-    a_k = _to_kernel_operand(a, k)
-    b_k = _to_kernel_operand(b, k)
-    k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
-    a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
-    _fill_common(args, d, k_kernel, None, kind, dims)
+    _fill_common(args, d, k, None, kind, dims)
     args.gemm_type = _lib.DG_GEMM_BATCHED
-    args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
-    args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
-    args.batch_stride_a, args.batch_stride_b, args.batch_stride_d = a_k.stride(0), b_k.stride(0), d.stride(0)
+    args.batch_stride_d = d.stride(0)
     args.m, args.n, args.num_groups = m, n, bs
     args.accumulate = 1 if c is not None else 0
     _apply_epilogue(args, epi)
-    _launch(args, d)
+    _launch_operands(args, d, a, b, k, batched=True)
 
 
 def _k_grouped(a, sfa, b, sfb, d, grouped_layout, c, recipe, use_psum_layout, epilogue, bf16: bool, dims: str = 'mn'):
@@ -634,21 +668,15 @@ def _k_grouped(a, sfa, b, sfb, d, grouped_layout, c, recipe, use_psum_layout, ep
         args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
     if c is not None and not is_cd_same:
         d.copy_(c)
-    a_k = _to_kernel_operand(a_t, k)
-    b_k = _to_kernel_operand(b_t, k)
-    k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
-    a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
-    _fill_common(args, d, k_kernel, None, kind, dims)
+    _fill_common(args, d, k, None, kind, dims)
     args.alignment = alignment
     args.gemm_type = _lib.DG_GEMM_KGROUPED
-    args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
-    args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
     args.batch_stride_d = d.stride(0)
     args.grouped_layout = grouped_layout.data_ptr()
     args.m, args.n, args.num_groups = m, n, g
     args.accumulate = 1 if c is not None else 0
     _apply_epilogue(args, epi)
-    _launch(args, d)
+    _launch_operands(args, d, a_t, b_t, k, batched=False)
 
 
 def k_grouped_fp8_gemm_tn_contiguous(a, b, d, ks_cpu, grouped_layout, c=None, recipe=(1, 1, 32),

@@ -113,6 +113,13 @@ typedef struct dg_gemm_args {
                                      need, zero-filled, only ever grown and never freed (a captured
                                      graph may hold it).  Growing it while the stream is being
                                      captured is an error: run the call once before the capture. */
+    int32_t a_mn_major;           /* 1: A is stored [K][M] (M contiguous; lda = stride between its K
+                                     rows, in elements), read in place.  e4m3 x e4m3 dense, batched
+                                     and K-grouped GEMMs on the 256-row 128-K-stage tiles only; any
+                                     other plan fails with DG_ENOKERNEL (callers then copy to K-major).
+                                     The reference's operand majors: deep_gemm/include/deep_gemm/
+                                     fp8_gemm.hpp:18-35.                                            */
+    int32_t b_mn_major;           /* 1: B is stored [K][N], likewise                                 */
 } dg_gemm_args;
 
 #define DG_COMPILED_M 1
