@@ -44,9 +44,10 @@ def parse():
                          '(cold-L2 kernel times) instead of the north-star line')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a 256 MiB device copy (reference kernel for FETCH_SIZE / WRITE_SIZE scaling)')
-    ap.add_argument('--profile-case', choices=('north', 'grouped', 'decode'), default=None,
+    ap.add_argument('--profile-case', choices=('north', 'north_tn', 'grouped', 'decode'), default=None,
                     help='launch one workload 20 times and exit (the command rocprofv3 wraps for the profiles/ '
-                         'summaries): north = fp8_gemm_nt 4096x7168x2048, grouped = m_grouped contiguous G=32 '
+                         'summaries): north = fp8_gemm_nt 4096x7168x2048, north_tn = fp8_gemm_tn at that shape (MN-major '
+                         'A and B), grouped = m_grouped contiguous G=32 '
                          'N=4096 K=7168, decode = fp8_gemm_nt 128x2112x7168')
     return ap.parse_args()
 
@@ -361,7 +362,14 @@ def profile_case(case):
     import deep_gemm
     dev = torch.device('cuda:0')
     gen = torch.Generator(device=dev).manual_seed(0)
-    if case in ('north', 'decode'):
+    if case == 'north_tn':
+        # the north-star shape as fp8_gemm_tn: A [K, M] and B [K, N] MN-major, read in place
+        m, n, k = 4096, 7168, 2048
+        a, sfa = _gpu_codes((k, m), dev, gen), _gpu_sf((k // 128, m), dev, gen)
+        b, sfb = _gpu_codes((k, n), dev, gen), _gpu_sf((k // 128, -(-n // 128)), dev, gen)
+        d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        fn = lambda: deep_gemm.fp8_gemm_tn((a, sfa), (b, sfb), d, recipe_a=(1, 128), recipe_b=(128, 128))
+    elif case in ('north', 'decode'):
         m, n, k = (4096, 7168, 2048) if case == 'north' else (128, 2112, 7168)
         a, sfa = _gpu_codes((m, k), dev, gen), _gpu_sf((m, k // 128), dev, gen)
         b, sfb = _gpu_codes((n, k), dev, gen), _gpu_sf((-(-n // 128), k // 128), dev, gen)
