@@ -538,13 +538,13 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         return dg_set_error("dg_gemm: K rows and strides must be 16-byte aligned (host pads otherwise)");
     // MN-major operands ([K][MN] storage, read in place by the 128-K-stage tile kernels)
     const bool amn = a.a_mn_major != 0, bmn = a.b_mn_major != 0;
-    if ((amn || bmn) && (a.kind != kFP8FP8 || a.jit ||
+    if ((amn || bmn) && ((a.kind != kFP8FP8 && a.kind != kBF16) || a.jit ||
                          !(a.gemm_type == kNormal || a.gemm_type == kBatched || a.gemm_type == kKGrouped))) {
-        dg_set_error("dg_gemm: MN-major operands are read in place only by e4m3 dense, batched and K-grouped "
-                     "ahead-of-time kernels");
+        dg_set_error("dg_gemm: MN-major operands are read in place only by e4m3 / bf16 dense, batched and "
+                     "K-grouped ahead-of-time kernels");
         return DG_ENOKERNEL;
     }
-    if ((amn ? lda_b < a.m : lda_b < kbytes_a) || (bmn ? ldb_b < a.n : ldb_b < kbytes_b) || a.ldd < a.n)
+    if ((amn ? lda_b < a.m * esz_a : lda_b < kbytes_a) || (bmn ? ldb_b < a.n * esz_b : ldb_b < kbytes_b) || a.ldd < a.n)
         return dg_set_error("dg_gemm: leading dimension smaller than the row");
     // (an MN-major operand's whole K extent must fit a buffer range below the dead-load offset)
     if ((amn ? (int64_t)a.k * lda_b >= 0x40000000LL : (int64_t)256 * lda_b > 0x7fffffffLL) ||
@@ -574,7 +574,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     if (cfg.bm == 0) return dg_set_error("dg_gemm: no tile shape fits this problem");
     if ((amn || bmn) && (plan.skinny_nw > 0 || plan.split != 1 || cfg.km != 2 || cfg.stages != 2 || cfg.bm > 256 ||
                          cfg.bn > 256 || tile_anchored(cfg.bm))) {
-        dg_set_error("dg_gemm: MN-major operands need a 128-K-stage tile plan (large M and N); this problem "
+        dg_set_error("dg_gemm: MN-major operands need a 128-byte-stage tile plan (large M and N); this problem "
                      "plans another kernel");
         return DG_ENOKERNEL;
     }
@@ -607,7 +607,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     KernelFn fn = jit ? nullptr
                 : skinny ? (plan.skinny_rows ? lookup_skinny_rows(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_d, epi_kind)
                                              : lookup_skinny(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_nw, plan.skinny_d, plan.skinny_ar, epi_kind))
-                : (amn || bmn) ? lookup_kernel_fp8fp8_mn(cfg.bm, cfg.bn, epi_kind, amn, bmn)
+                : (amn || bmn) ? lookup_kernel_mn(a.kind, cfg.bm, cfg.bn, epi_kind, amn, bmn)
                          : lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind, persistent);
     if (fn == nullptr && !jit) {
         char buf[160];

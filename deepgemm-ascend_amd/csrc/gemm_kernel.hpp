@@ -547,13 +547,19 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     static_assert((NW == 4 || NW == 8) && WGM * WGN == NW && TM >= 1 && TN >= 1 && TM * 32 == WM &&
                       TN_LAST >= 1 && (WGN - 1) * WN + TN_LAST * 32 == BN, "wave tiling");
     static_assert(!kRagged || (NW == 8 && LW == 4 && WGM == 4 && WGN == 2), "ragged tiling needs the loader waves as its last column");
-    // MN-major operands (AMN / BMN: A [K][M] / B [K][N], MN contiguous; e4m3, 128-K stages): a stage
-    // holds the tile's 128 K rows of up to 256 MN bytes each, in 256-byte LDS rows whose 16-byte
-    // pieces are XOR-swizzled by 2 (k % 8); fragments are read with ds_read_b64_tr_b8, which hands
-    // each lane 8 consecutive K of one MN row, so the MFMA operands equal the K-major path's.
-    static_assert((!AMN && !BMN) || (KIND == kFP8FP8 && KM == 2 && NSTAGE == 2 && BM <= 256 && BN <= 256),
-                  "MN-major operands: e4m3, 128-K stages, tiles of at most 256 x 256");
-    constexpr int MN_PITCH = 256, MN_KROWS = 64 * KM;     // an MN-major stage: 128 K rows x 256 bytes
+    // MN-major operands (AMN / BMN: A [K][M] / B [K][N], MN contiguous; e4m3 or bf16, 128-byte stages):
+    // a stage holds the tile's K rows (128 e4m3 / 64 bf16) of up to 256 MN elements each, in LDS rows
+    // of 256 elements whose 16-byte pieces are XOR-swizzled (e4m3: by 2 (k % 8), bf16: by 4 (k % 4));
+    // fragments are read with ds_read_b64_tr_b8 / _b16, which hand each lane consecutive K of one MN
+    // row, so the MFMA operands equal the K-major path's.
+    static_assert((!AMN && !BMN) || ((KIND == kFP8FP8 || KIND == kBF16) && KM == 2 && NSTAGE == 2 && BM <= 256 && BN <= 256),
+                  "MN-major operands: e4m3 or bf16, 128-byte stages, tiles of at most 256 x 256");
+    constexpr int MN_E = kBf16 ? 2 : 1;                    // bytes per element
+    constexpr int MN_PITCH = 256 * MN_E, MN_KROWS = KS;   // an MN-major stage: KS K rows x 256 elements
+    constexpr int MN_PPR = MN_PITCH / 16;                 // 16-byte pieces per LDS row
+    // piece swizzle of MN-major LDS row k: the K rows one transposing read touches (8 for e4m3, 4 for
+    // bf16) land on distinct bank groups, and so do the two 16-lane groups served together
+    auto mn_swizzle = [](int k) -> int { return kBf16 ? (k & 3) << 2 : (k & 7) << 1; };
     constexpr int A_BYTES = AMN ? MN_KROWS * MN_PITCH : BM * RBA, B_BYTES = BMN ? MN_KROWS * MN_PITCH : BN * RBB;
     constexpr int SCA = kBf16 ? 0 : (BM * 2 + 255) / 256 * 256;   // one packed int16 per row and sub-step
     constexpr int SCB = kBf16 ? 0 : (BN * 2 + 255) / 256 * 256;
@@ -647,6 +653,7 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         const int kso = __builtin_amdgcn_readfirstlane(ks);
         a_base += AMN ? (int64_t)kso * p.lda : (int64_t)kso * (kAFp4 ? 1 : (kBf16 ? 4 : 2)) / 2;
         b_base += BMN ? (int64_t)kso * p.ldb : (int64_t)kso * (kBFp4 ? 1 : (kBf16 ? 4 : 2)) / 2;
+        // (p.lda / p.ldb are in bytes: an MN-major K row is lda bytes)
         if (!kBf16) {
             sfa += (int64_t)(kso / 64) * p.sfa_ld;
             sfb += (int64_t)(kso / 64) * p.sfb_ld;
@@ -724,9 +731,9 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     const int64_t lda = p.lda, ldb = p.ldb;
     // (MN-major: the tile's first column is the base and the K rows of the contraction bound the
     // range, so K rows past the end read zeros)
-    const __amdgpu_buffer_rsrc_t rs_a = AMN ? make_rsrc(a_base + m0, (int64_t)k_len * lda - m0)
+    const __amdgpu_buffer_rsrc_t rs_a = AMN ? make_rsrc(a_base + m0 * MN_E, (int64_t)k_len * lda - m0 * MN_E)
                                             : make_rsrc(a_base + (int64_t)m0 * lda, (int64_t)rows_a * lda);
-    const __amdgpu_buffer_rsrc_t rs_b = BMN ? make_rsrc(b_base + n0, (int64_t)k_len * ldb - n0)
+    const __amdgpu_buffer_rsrc_t rs_b = BMN ? make_rsrc(b_base + n0 * MN_E, (int64_t)k_len * ldb - n0 * MN_E)
                                             : make_rsrc(b_base + (int64_t)n0 * ldb, (int64_t)rows_b * ldb);
     // (bytes of one K row: storage bytes per two K elements x K / 2)
     const int kbytes_a = gemm_type == kKGrouped || CK > 0 ? k_len * (kAFp4 ? 1 : (kBf16 ? 4 : 2)) / 2 : p.kbytes_a;
@@ -746,7 +753,7 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     // Operand rows: each wave-level buffer_load_dwordx4 ... lds fills 1 KB (64 lanes x 16 B)
     // of a stage; lane slots map to swizzled (row, 16-byte K piece) positions.  The stage's K
     // offset rides in the scalar soffset, so the per-lane voffset is stage-invariant.
-    constexpr int SLA = AMN ? MN_KROWS * 16 : BM * SPRA, SLB = BMN ? MN_KROWS * 16 : BN * SPRB;   // 16-byte slots per stage
+    constexpr int SLA = AMN ? MN_KROWS * MN_PPR : BM * SPRA, SLB = BMN ? MN_KROWS * MN_PPR : BN * SPRB;   // 16-byte slots per stage
     constexpr int NLA = (SLA + LT - 1) / LT, NLB = (SLB + LT - 1) / LT;  // per-thread loads
     // Packed SF rows: one buffer_load_dword ... lds per 128 rows of the tile and sub-step,
     // issued by waves 0 .. NSCA-1 (A) and NSCA .. NSCA+NSCB-1 (B).
@@ -765,15 +772,15 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         lk_b = ((ltid % SPRB) ^ slot_swizzle<SPRB>(row_b)) * 16;
         vbase_a = row_a < rows_a ? (uint32_t)(row_a * lda + lk_a) : kOOBOffset;
         vbase_b = row_b < rows_b ? (uint32_t)(row_b * ldb + lk_b) : kOOBOffset;
-        // MN-major: LDS slot ltid = K row ltid / 16, piece ltid % 16 of the swizzled 256-byte row,
-        // which holds MN bytes [16 pp, 16 pp + 16) with pp = piece ^ 2 (k % 8); pieces past the
+        // MN-major: LDS slot ltid = K row ltid / MN_PPR, piece ltid % MN_PPR of the swizzled row,
+        // which holds MN bytes [16 pp, 16 pp + 16) with pp = piece ^ mn_swizzle(k); pieces past the
         // tile's MN extent read zeros
-        const int kr = ltid / 16, pp = (ltid % 16) ^ ((kr & 7) << 1);
-        if constexpr (AMN) vbase_a = pp * 16 < rows_a ? (uint32_t)(kr * lda + pp * 16) : kOOBOffset;
-        if constexpr (BMN) vbase_b = pp * 16 < rows_b ? (uint32_t)(kr * ldb + pp * 16) : kOOBOffset;
+        const int kr = ltid / MN_PPR, pp = (ltid % MN_PPR) ^ mn_swizzle(kr);
+        if constexpr (AMN) vbase_a = pp * 16 < rows_a * MN_E ? (uint32_t)(kr * lda + pp * 16) : kOOBOffset;
+        if constexpr (BMN) vbase_b = pp * 16 < rows_b * MN_E ? (uint32_t)(kr * ldb + pp * 16) : kOOBOffset;
     }
-    const int vstep_a = __builtin_amdgcn_readfirstlane((int)(AMN ? (LT / 16) * lda : (LT / SPRA) * lda));
-    const int vstep_b = __builtin_amdgcn_readfirstlane((int)(BMN ? (LT / 16) * ldb : (LT / SPRB) * ldb));
+    const int vstep_a = __builtin_amdgcn_readfirstlane((int)(AMN ? (LT / MN_PPR) * lda : (LT / SPRA) * lda));
+    const int vstep_b = __builtin_amdgcn_readfirstlane((int)(BMN ? (LT / MN_PPR) * ldb : (LT / SPRB) * ldb));
     // Per-wave packed-SF load of a stage: loader wave w < NSCA fetches A rows [128 w, 128 w + 128),
     // loader waves NSCA .. NSCA+NSCB-1 the B rows; the other waves issue a dead (out-of-range) load
     // into an idle word so that every wave runs the same branch-free instruction stream.
@@ -852,8 +859,8 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
             return i32x8{lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
         }
     };
-    // MN-major operand block starting at MN row R0 (its lane (r, q) = row R0 + r): four
-    // ds_read_b64_tr_b8 reads.  In each 16-lane group (lanes 16 g + i, g = 2 q + h) lane s supplies
+    // MN-major operand block starting at MN row R0 (its lane (r, q) = row R0 + r): four transposing
+    // reads.  e4m3 (ds_read_b64_tr_b8):  In each 16-lane group (lanes 16 g + i, g = 2 q + h) lane s supplies
     // the 8-byte chunk of K row kb + s / 2 at MN bytes R0 + 16 h + 8 (s % 2); the read hands lane i
     // byte i % 8 of chunk 2 j + i / 8 as its byte j, i.e. K kb .. kb + 7 of MN row R0 + 16 h + i.
     // The four reads cover K [16 q, +8), [16 q + 8, +8), [32 + 16 q, +8), [40 + 16 q, +8) of the
@@ -861,15 +868,33 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     auto load_frag_mn = [&](const uint8_t* base, int R0, auto u_tag) -> i32x8 {
         constexpr int u = decltype(u_tag)::value;
         const int s16 = lane & 15, h = (lane >> 4) & 1;
-        const int pp = ((R0 + 16 * h) >> 4) ^ (((s16 >> 1) & 7) << 1);
-        const uint8_t* b0 = base + (u * 64 + 16 * q + (s16 >> 1)) * MN_PITCH + (pp << 4) + (s16 & 1) * 8;
         typedef int v2i __attribute__((ext_vector_type(2)));
-        typedef __attribute__((address_space(3))) v2i lds_v2i;
-        const v2i e0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0));
-        const v2i e1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0 + 8 * MN_PITCH));
-        const v2i e2 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0 + 32 * MN_PITCH));
-        const v2i e3 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0 + 40 * MN_PITCH));
-        return i32x8{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+        if constexpr (!kBf16) {
+            const int pp = ((R0 + 16 * h) >> 4) ^ mn_swizzle(s16 >> 1);
+            const uint8_t* b0 = base + (u * 64 + 16 * q + (s16 >> 1)) * MN_PITCH + (pp << 4) + (s16 & 1) * 8;
+            typedef __attribute__((address_space(3))) v2i lds_v2i;
+            const v2i e0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0));
+            const v2i e1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0 + 8 * MN_PITCH));
+            const v2i e2 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0 + 32 * MN_PITCH));
+            const v2i e3 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0 + 40 * MN_PITCH));
+            return i32x8{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+        } else {
+            // ds_read_b64_tr_b16 (probed on gfx950): in each 16-lane group lane i receives element
+            // i % 4 of the 4-element chunk addressed by source lane 4 j + i / 4 as its element j.  With
+            // lane s addressing K row kb + s / 4 at MN elements R0 + 16 h + 4 (s % 4), lane i receives
+            // K kb .. kb + 3 of MN row R0 + 16 h + i; four reads cover K [8 q, +8) and [16 + 8 q, +8) of
+            // the sub-step's 32 K (the two 32x32x16 steps' operands).
+            const int col = R0 + 16 * h + 4 * (s16 & 3);
+            const int pp = (col >> 3) ^ mn_swizzle(s16 >> 2);
+            const uint8_t* b0 = base + (u * 32 + 8 * q + (s16 >> 2)) * MN_PITCH + (pp << 4) + ((col >> 2) & 1) * 8;
+            typedef short v4s __attribute__((ext_vector_type(4)));
+            typedef __attribute__((address_space(3))) v4s lds_v4s;
+            const v2i e0 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(b0)));
+            const v2i e1 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(b0 + 4 * MN_PITCH)));
+            const v2i e2 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(b0 + 16 * MN_PITCH)));
+            const v2i e3 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(b0 + 20 * MN_PITCH)));
+            return i32x8{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+        }
     };
     // UE8M0 byte of K-block q of row R (one packed int16 per row in the sub-step's scale area,
     // K-block 0 in the low byte): a byte read, consumed by the MFMA as it is.
@@ -895,11 +920,11 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         const uint8_t* sc = st + A_BYTES + B_BYTES + u * SCU;
         if constexpr (part < TM) {
             const int R = wm * WM + part * 32 + r;
-            if constexpr (AMN) return Pair<i32x8, int>{load_frag_mn(st, R - r, u_tag), load_scale(sc, R)};
+            if constexpr (AMN) return Pair<i32x8, int>{load_frag_mn(st, R - r, u_tag), kBf16 ? 0 : load_scale(sc, R)};
             else return Pair<i32x8, int>{load_frag(st, R, Int<SPRA>{}, u_tag), kBf16 ? 0 : load_scale(sc, R)};
         } else {
             const int R = wn * WN + r;
-            if constexpr (BMN) return Pair<i32x8, int>{load_frag_mn(st + A_BYTES, R - r, u_tag), load_scale(sc + SCA, R)};
+            if constexpr (BMN) return Pair<i32x8, int>{load_frag_mn(st + A_BYTES, R - r, u_tag), kBf16 ? 0 : load_scale(sc + SCA, R)};
             else return Pair<i32x8, int>{load_frag(st + A_BYTES, R, Int<SPRB>{}, u_tag),
                                          kBf16 ? 0 : load_scale(sc + SCA, R)};
         }

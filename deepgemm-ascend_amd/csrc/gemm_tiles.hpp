@@ -123,8 +123,8 @@ KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi, bool persistent);
 KernelFn lookup_kernel_fp8fp4(int bm, int bn, int epi, bool persistent);
 KernelFn lookup_kernel_fp4fp4(int bm, int bn, int epi, bool persistent);
 KernelFn lookup_kernel_bf16(int bm, int bn, int epi, bool persistent);
-// e4m3 x e4m3 tile kernels reading MN-major A and / or B in place (the 128-K-stage tiles of at most
-// 256 x 256; nullptr otherwise)
-KernelFn lookup_kernel_fp8fp8_mn(int bm, int bn, int epi, bool a_mn, bool b_mn);
+// e4m3 x e4m3 and bf16 x bf16 tile kernels reading MN-major A and / or B in place (the 128-byte-stage
+// tiles of at most 256 x 256; nullptr otherwise)
+KernelFn lookup_kernel_mn(int kind, int bm, int bn, int epi, bool a_mn, bool b_mn);
 
 }  // namespace dg

@@ -134,3 +134,83 @@ def test_mn_major_k_grouped(monkeypatch, no_copy, block, g_, m, n, ks):
             assert torch.equal(dc[gi], torch.zeros_like(dc[gi])), gi
         else:
             assert calc_diff(dc[gi], ref[gi]) < THRESH, gi
+
+
+def _bf16_layout_call(layout, m, n, k, seed, block, monkeypatch, no_copy):
+    g = gen(seed)
+    a = (torch.randn(m, k, generator=g) * 0.1).bfloat16()
+    b = (torch.randn(n, k, generator=g) * 0.1).bfloat16()
+    ref = og.gemm_nt(a.float(), b.float())
+    a, b = a.cuda(), b.cuda()
+
+    def mn_major(x):   # [rows, K] -> [K, rows] view over a buffer whose K rows are 16-byte aligned
+        rows = x.size(0)
+        buf = torch.zeros(x.size(1), -(-rows // 8) * 8, dtype=torch.bfloat16, device='cuda')
+        buf[:, :rows] = x.t()
+        return buf[:, :rows]
+    if layout[0] == 't':
+        a = mn_major(a)
+    if layout[1] == 'n':
+        b = mn_major(b)
+    if block:
+        monkeypatch.setenv('DG_FORCE_BLOCK', block)
+    fn = getattr(deep_gemm, f'bf16_gemm_{layout}')
+    d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
+    # (bf16 nn copies B by design: only A MN-major operands are read in place for bf16)
+    no_copy(layout in ('tn', 'tt'))
+    fn(a, b, d)
+    torch.cuda.synchronize()
+    no_copy(False)
+    if block:
+        monkeypatch.setenv('DG_FORCE_BLOCK', block)
+    monkeypatch.setenv('DG_MN_COPY', '1')
+    d_copy = torch.empty_like(d)
+    fn(a, b, d_copy)
+    torch.cuda.synchronize()
+    return d.cpu(), d_copy.cpu(), ref
+
+
+@pytest.mark.parametrize('layout', ['nn', 'tn', 'tt'])
+@pytest.mark.parametrize('block', ['256x256', '256x224', '256x160'])
+@pytest.mark.parametrize('m,n,k', [(512, 448, 512), (300, 200, 384), (260, 500, 320)])
+def test_mn_major_bf16_layouts(monkeypatch, no_copy, layout, block, m, n, k):
+    print(f'mn-major bf16_gemm_{layout} {block} m={m} n={n} k={k}', flush=True)
+    d, d_copy, ref = _bf16_layout_call(layout, m, n, k, 81, block, monkeypatch, no_copy)
+    assert torch.equal(d.view(torch.int16), d_copy.view(torch.int16))
+    assert calc_diff(d, ref) < THRESH
+
+
+@pytest.mark.parametrize('layout', ['nn', 'tn'])
+def test_mn_major_bf16_baseline_shape(monkeypatch, no_copy, layout):
+    """BASELINE config 3's M=4096 shape on its default plan (nn: B copied, tn: both in place)."""
+    m, n, k = 4096, 7168, 2048
+    print(f'mn-major bf16_gemm_{layout} default plan m={m} n={n} k={k}', flush=True)
+    d, d_copy, ref = _bf16_layout_call(layout, m, n, k, 82, None, monkeypatch, no_copy)
+    assert torch.equal(d.view(torch.int16), d_copy.view(torch.int16))
+    assert calc_diff(d, ref) < THRESH
+
+
+@pytest.mark.parametrize('block', ['256x256', '256x224'])
+def test_mn_major_bf16_k_grouped(monkeypatch, no_copy, block):
+    m, n, ks = 304, 528, [700, 0, 256, 96]
+    print(f'mn-major k_grouped bf16 {block} m={m} n={n} ks={ks}', flush=True)
+    total, psum = ol.psum_from_sizes(ks, 256)
+    g = gen(83)
+    keep = torch.zeros(total, 1)
+    for sl in ol.psum_slices(psum, 256):
+        keep[sl] = 1
+    a = (torch.randn(total, m, generator=g) * keep).bfloat16()
+    b = (torch.randn(total, n, generator=g) * keep).bfloat16()
+    a_dev, b_dev = a.cuda(), b.cuda()
+    a_dev[keep.squeeze(1) == 0] = float('nan')   # padding K rows: never read in place
+    b_dev[keep.squeeze(1) == 0] = float('nan')
+    c = torch.randn(len(ks), m, n, generator=g)
+    d = c.clone().cuda()
+    monkeypatch.setenv('DG_FORCE_BLOCK', block)
+    no_copy(True)
+    deep_gemm.k_grouped_bf16_gemm_tn_contiguous(a_dev, b_dev, d, ks, torch.tensor(psum, dtype=torch.int32, device='cuda'), c=d)
+    torch.cuda.synchronize()
+    no_copy(False)
+    ref = og.k_grouped_tn(a.float(), b.float(), psum, 256, c, torch.float32)
+    assert torch.equal(d[1].cpu(), c[1])
+    assert calc_diff(d.cpu(), ref) < THRESH
