@@ -114,8 +114,9 @@ typedef struct dg_gemm_args {
                                      graph may hold it).  Growing it while the stream is being
                                      captured is an error: run the call once before the capture. */
     int32_t a_mn_major;           /* 1: A is stored [K][M] (M contiguous; lda = stride between its K
-                                     rows, in elements), read in place.  e4m3 x e4m3 dense, batched
-                                     and K-grouped GEMMs on the 256-row 128-K-stage tiles only; any
+                                     rows, in elements), read in place.  e4m3 x e4m3 and bf16 x bf16
+                                     dense, batched and K-grouped GEMMs on the 256-row 128-byte-stage
+                                     tiles only; any
                                      other plan fails with DG_ENOKERNEL (callers then copy to K-major).
                                      The reference's operand majors: deep_gemm/include/deep_gemm/
                                      fp8_gemm.hpp:18-35.                                            */
