@@ -538,10 +538,11 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         return dg_set_error("dg_gemm: K rows and strides must be 16-byte aligned (host pads otherwise)");
     // MN-major operands ([K][MN] storage, read in place by the 128-K-stage tile kernels)
     const bool amn = a.a_mn_major != 0, bmn = a.b_mn_major != 0;
-    if ((amn || bmn) && ((a.kind != kFP8FP8 && a.kind != kBF16) || a.jit ||
-                         !(a.gemm_type == kNormal || a.gemm_type == kBatched || a.gemm_type == kKGrouped))) {
+    const bool mgrouped = a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx;
+    if ((amn || bmn) && ((a.kind != kFP8FP8 && a.kind != kBF16) || a.jit || (mgrouped && amn) ||
+                         !(a.gemm_type == kNormal || a.gemm_type == kBatched || a.gemm_type == kKGrouped || mgrouped))) {
         dg_set_error("dg_gemm: MN-major operands are read in place only by e4m3 / bf16 dense, batched and "
-                     "K-grouped ahead-of-time kernels");
+                     "K-grouped ahead-of-time kernels (M-grouped: B only)");
         return DG_ENOKERNEL;
     }
     if ((amn ? lda_b < a.m * esz_a : lda_b < kbytes_a) || (bmn ? ldb_b < a.n * esz_b : ldb_b < kbytes_b) || a.ldd < a.n)
@@ -572,8 +573,8 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     }
     const TileCfg cfg = plan.tile;
     if (cfg.bm == 0) return dg_set_error("dg_gemm: no tile shape fits this problem");
-    if ((amn || bmn) && (plan.skinny_nw > 0 || plan.split != 1 || cfg.km != 2 || cfg.stages != 2 || cfg.bm > 256 ||
-                         cfg.bn > 256 || tile_anchored(cfg.bm))) {
+    if ((amn || bmn) && (plan.skinny_nw > 0 || plan.split != 1 || cfg.km != 2 || cfg.stages != 2 ||
+                         cfg.bm > 256 || cfg.bn > 256)) {
         dg_set_error("dg_gemm: MN-major operands need a 128-byte-stage tile plan (large M and N); this problem "
                      "plans another kernel");
         return DG_ENOKERNEL;

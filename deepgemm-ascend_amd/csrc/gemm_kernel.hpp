@@ -552,8 +552,9 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     // of 256 elements whose 16-byte pieces are XOR-swizzled (e4m3: by 2 (k % 8), bf16: by 4 (k % 4));
     // fragments are read with ds_read_b64_tr_b8 / _b16, which hand each lane consecutive K of one MN
     // row, so the MFMA operands equal the K-major path's.
-    static_assert((!AMN && !BMN) || ((KIND == kFP8FP8 || KIND == kBF16) && KM == 2 && NSTAGE == 2 && BM <= 256 && BN <= 256),
-                  "MN-major operands: e4m3 or bf16, 128-byte stages, tiles of at most 256 x 256");
+    static_assert((!AMN && !BMN) || ((KIND == kFP8FP8 || KIND == kBF16) && KM == 2 && NSTAGE == 2 &&
+                                     (!AMN || BM <= 256) && (!BMN || BN <= 256)),
+                  "MN-major operands: e4m3 or bf16, 128-byte stages, at most 256 MN rows per operand tile");
     constexpr int MN_E = kBf16 ? 2 : 1;                    // bytes per element
     constexpr int MN_PITCH = 256 * MN_E, MN_KROWS = KS;   // an MN-major stage: KS K rows x 256 elements
     constexpr int MN_PPR = MN_PITCH / 16;                 // 16-byte pieces per LDS row

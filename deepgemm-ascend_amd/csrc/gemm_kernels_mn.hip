@@ -9,6 +9,7 @@ namespace {
 template <int I, int KIND, bool AMN, bool BMN>
 KernelFn mn_epi(int epi) {
     constexpr TileCfg t = kTiles[I];
+    // (the anchored 384-row tiles leave no LDS for a 256-element MN-major B row)
     if constexpr (t.km != 2 || t.stages != 2 || t.bm > 256 || t.bn > 256) {
         return nullptr;
     } else {

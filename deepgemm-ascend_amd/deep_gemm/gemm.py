@@ -121,16 +121,17 @@ def _mn_in_place(t: torch.Tensor, k: int) -> bool:
 
 
 def _launch_operands(args: _lib.GemmArgs, d: torch.Tensor, a: torch.Tensor, b: torch.Tensor, k: int,
-                     batched: bool) -> None:
+                     batch_a: bool, batch_b: bool) -> None:
     """Set A and B (strides, batch strides, K) and launch.  e4m3 / bf16 MN-major operands are read in
     place by the 128-byte-stage tile kernels (the reference takes operand majors as kernel parameters,
     deep_gemm/include/deep_gemm/fp8_gemm.hpp:18-35); a plan with another kernel (DG_ENOKERNEL) and
     every other operand get a K-major copy."""
     if args.kind in (_lib.DG_KIND_FP8_FP8, _lib.DG_KIND_BF16) and not get_dry_run() and not args.jit:
         a_mn, b_mn = _mn_in_place(a, k), _mn_in_place(b, k)
-        if args.kind == _lib.DG_KIND_BF16 and not a_mn:
-            # bf16 with only B MN-major (nn) measured faster with B copied (4096x2112x7168: 176.0 vs
-            # 199.5 us; tn / tt gain in place: 183.9 vs 207.3, 172.1 vs 190.5)
+        if args.kind == _lib.DG_KIND_BF16 and not a_mn and args.gemm_type == _lib.DG_GEMM_NORMAL:
+            # dense bf16 with only B MN-major (nn) measured faster with B copied (4096x2112x7168: 176.0
+            # vs 199.5 us; tn / tt gain in place: 183.9 vs 207.3, 172.1 vs 190.5).  M-grouped B is the
+            # whole expert-weight tensor, read in place.
             b_mn = False
         if a_mn or b_mn:
             a_k = a if a_mn else _to_kernel_operand(a, k)
@@ -140,8 +141,10 @@ def _launch_operands(args: _lib.GemmArgs, d: torch.Tensor, a: torch.Tensor, b: t
                 args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
                 args.lda = a_k.stride(-1) if a_mn else a_k.stride(-2)
                 args.ldb = b_k.stride(-1) if b_mn else b_k.stride(-2)
-                if batched:
-                    args.batch_stride_a, args.batch_stride_b = a_k.stride(0), b_k.stride(0)
+                if batch_a:
+                    args.batch_stride_a = a_k.stride(0)
+                if batch_b:
+                    args.batch_stride_b = b_k.stride(0)
                 args.a_mn_major, args.b_mn_major = int(a_mn), int(b_mn)
                 if _launch(args, d, allow_no_kernel=True):
                     return
@@ -153,8 +156,10 @@ def _launch_operands(args: _lib.GemmArgs, d: torch.Tensor, a: torch.Tensor, b: t
     args.k = k_kernel
     args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
     args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
-    if batched:
-        args.batch_stride_a, args.batch_stride_b = a_k.stride(0), b_k.stride(0)
+    if batch_a:
+        args.batch_stride_a = a_k.stride(0)
+    if batch_b:
+        args.batch_stride_b = b_k.stride(0)
     _launch(args, d)
 
 
@@ -352,7 +357,7 @@ def _dense_gemm(a, sfa, b, sfb, d, c, recipe, recipe_a, recipe_b, disable_ue8m0_
     args.accumulate = 1 if is_cd_same else 0
     args.bias = c.data_ptr() if with_bias else None
     _apply_epilogue(args, epi)
-    _launch_operands(args, d, a, b, k, batched=False)
+    _launch_operands(args, d, a, b, k, batch_a=False, batch_b=False)
 
 
 def _pad_k(t: torch.Tensor, k: int) -> torch.Tensor:
@@ -456,20 +461,13 @@ def _grouped_contiguous(a, sfa, b, sfb, d, grouped_layout, recipe, recipe_a, rec
         args.sfa, args.sfb = sfa_t.data_ptr(), sfb_t.data_ptr()
         args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
         args.sfb_batch_stride = sfb_t.stride(0)
-    a_k = _to_kernel_operand(a, k)
-    b_k = _to_kernel_operand(b, k)
-    k_kernel = max(a_k.size(-1) * (2 if _is_fp4(a_k) else 1), b_k.size(-1) * (2 if _is_fp4(b_k) else 1))
-    a_k, b_k = _pad_k(a_k, k_kernel), _pad_k(b_k, k_kernel)
-    _fill_common(args, d, k_kernel, None, kind, dims)
+    _fill_common(args, d, k, None, kind, dims)
     args.alignment = alignment
     args.gemm_type = _lib.DG_GEMM_MGROUPED_PSUM if use_psum_layout else _lib.DG_GEMM_MGROUPED_IDX
-    args.a, args.b = a_k.data_ptr(), b_k.data_ptr()
-    args.lda, args.ldb = a_k.stride(-2), b_k.stride(-2)
-    args.batch_stride_b = b_k.stride(0)
     args.grouped_layout = grouped_layout.data_ptr()
     args.m, args.n, args.num_groups = m, n, g
     _apply_epilogue(args, epi)
-    _launch(args, d)
+    _launch_operands(args, d, a, b, k, batch_a=False, batch_b=True)
 
 
 def _make_m_grouped_fp8_fp4(trans_b: bool):
@@ -626,7 +624,7 @@ def _batched(a, sfa, b, sfb, d, c, recipe, bf16: bool, epilogue=None, dims: str 
     args.m, args.n, args.num_groups = m, n, bs
     args.accumulate = 1 if c is not None else 0
     _apply_epilogue(args, epi)
-    _launch_operands(args, d, a, b, k, batched=True)
+    _launch_operands(args, d, a, b, k, batch_a=True, batch_b=True)
 
 
 def _k_grouped(a, sfa, b, sfb, d, grouped_layout, c, recipe, use_psum_layout, epilogue, bf16: bool, dims: str = 'mn'):
@@ -681,7 +679,7 @@ def _k_grouped(a, sfa, b, sfb, d, grouped_layout, c, recipe, use_psum_layout, ep
     args.m, args.n, args.num_groups = m, n, g
     args.accumulate = 1 if c is not None else 0
     _apply_epilogue(args, epi)
-    _launch_operands(args, d, a_t, b_t, k, batched=False)
+    _launch_operands(args, d, a_t, b_t, k, batch_a=False, batch_b=False)
 
 
 def k_grouped_fp8_gemm_tn_contiguous(a, b, d, ks_cpu, grouped_layout, c=None, recipe=(1, 1, 32),

@@ -214,3 +214,53 @@ def test_mn_major_bf16_k_grouped(monkeypatch, no_copy, block):
     ref = og.k_grouped_tn(a.float(), b.float(), psum, 256, c, torch.float32)
     assert torch.equal(d[1].cpu(), c[1])
     assert calc_diff(d.cpu(), ref) < THRESH
+
+
+@pytest.mark.parametrize('psum', [True, False])
+@pytest.mark.parametrize('dtype', ['e4m3', 'bf16'])
+def test_mn_major_m_grouped_nn(monkeypatch, no_copy, psum, dtype):
+    """m_grouped_*_gemm_nn_contiguous at alignment 256 (256-row tiles): B [G, K, N] read in place;
+    padding rows exact zeros, bit-identical to the copy path, oracle parity."""
+    sizes, n, k, alignment = [200, 512, 0, 300], 384, 512, 256
+    print(f'mn-major m_grouped nn {dtype} psum={psum} sizes={sizes} n={n} k={k}', flush=True)
+    g = gen(91)
+    total, ps = ol.psum_from_sizes(sizes, alignment)
+    if dtype == 'e4m3':
+        a, sfa, a_deq = operand(total, k, 'e4m3', (1, 128), g, 'randn')
+        b, sfb, b_deq = operand(n, k, 'e4m3', (128, 128), g, 'randn', batch=len(sizes))
+    else:
+        a_deq = (torch.randn(total, k, generator=g) * 0.1).bfloat16().float()
+        b_deq = (torch.randn(len(sizes), n, k, generator=g) * 0.1).bfloat16().float()
+        a, b = a_deq.bfloat16(), b_deq.bfloat16()
+    for sl in ol.psum_pad_slices(ps, alignment):
+        a.view(torch.uint8 if dtype == 'e4m3' else torch.int16)[sl] = 0
+        a_deq[sl] = 0
+    layout_t = torch.tensor(ps, dtype=torch.int32) if psum else ol.m_indices_from_psum(ps, alignment, total)
+    ref = og.m_grouped_contiguous(a_deq, b_deq, layout_t, psum, alignment)
+    b_kn = b.cuda().transpose(1, 2).contiguous()   # [G, K, N] storage: N contiguous
+    b_view = b_kn.transpose(1, 2)                   # logical [G, N, K], MN-major
+
+    def run(copy):
+        d = torch.full((total, n), float('nan'), dtype=torch.bfloat16, device='cuda')
+        no_copy(not copy)
+        # the problem is small enough to plan 128-row tiles; force a 256x256 tile (alignment 256)
+        monkeypatch.setenv('DG_FORCE_BLOCK', '256x256')
+        if copy:
+            monkeypatch.setenv('DG_MN_COPY', '1')
+        if dtype == 'e4m3':
+            deep_gemm.m_grouped_fp8_gemm_nn_contiguous((a.cuda(), sfa.cuda()), (b_kn, sfb.cuda().transpose(1, 2)), d,
+                                                       layout_t.cuda(), recipe_a=(1, 128), recipe_b=(128, 128),
+                                                       use_psum_layout=psum)
+        else:
+            deep_gemm.m_grouped_bf16_gemm_nn_contiguous(a.cuda(), b_kn, d, layout_t.cuda(), use_psum_layout=psum)
+        torch.cuda.synchronize()
+        no_copy(False)
+        return d.cpu()
+    out = run(False)
+    out_copy = run(True)
+    assert torch.equal(out.view(torch.int16), out_copy.view(torch.int16))
+    valid = torch.zeros(total, dtype=torch.bool)
+    for sl in ol.psum_slices(ps, alignment):
+        valid[sl] = True
+    assert torch.equal(out[~valid], torch.zeros_like(out[~valid]))
+    assert calc_diff(out[valid], ref[valid]) < THRESH
