@@ -502,7 +502,7 @@ __device__ __forceinline__ void epilogue_block(const KParams& p, const f32x16& a
 // time (-1 / 0 = read from the arguments): the ahead-of-time menu reads everything from the
 // arguments, the JIT compiles one body per problem (csrc/jit.hip).
 template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI, int CT = -1,
-          int CS = 0, int CM = 0, int CN = 0, int CK = 0, bool AMN = false, bool BMN = false>
+          int CS = 0, int CM = 0, int CN = 0, int CK = 0, bool AMN = false, bool BMN = false, int NSB_ = 0>
 __device__ __forceinline__ void gemm_body(const KParams& p) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
@@ -568,9 +568,23 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     constexpr int NSCA = kBf16 ? 0 : (BM + 127) / 128, NSCB = kBf16 ? 0 : (BN + 127) / 128;
     // 256 idle bytes per stage that take the dead SF loads of waves without an SF row to fetch
     constexpr int SPARE = (!kBf16 && NSCA + NSCB < LW) ? 256 : 0;
-    constexpr int STAGE = A_BYTES + B_BYTES + KM * SCU + SPARE;
-    static_assert(NSTAGE >= 2 && NSTAGE * STAGE * OCC <= 160 * 1024, "LDS budget");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * STAGE];
+    // Split ring (NSB = 3 B slots beside a two-slot late-sync ring of A + SF): B rows get a ring of
+    // their own, one slot deeper, and each late sync issues A / SF of stage c + 2 and B of stage
+    // c + 3.  A CU's load rate follows the bytes it keeps in flight (measured on MI355X), and the
+    // deeper B ring holds ~1.5x the bytes of one stage in flight within the 160 KB of LDS.
+    // NSB_ requests it; the kernel takes it where it fits the LDS (otherwise one shared ring).
+    constexpr int STAGE = A_BYTES + B_BYTES + KM * SCU + SPARE;     // unified ring slot
+    constexpr bool kSplitRing = NSB_ == 3 && NSTAGE == 2 && KM == 2 && !AMN && !BMN &&
+                                (NSTAGE * (STAGE - B_BYTES) + NSB_ * B_BYTES) * OCC <= 160 * 1024;
+    constexpr int NSB = kSplitRing ? NSB_ : NSTAGE;
+    constexpr int STAGE_A = kSplitRing ? A_BYTES + KM * SCU + SPARE : STAGE;   // slot of A (+ SF)
+    constexpr int SC_OFF = kSplitRing ? A_BYTES : A_BYTES + B_BYTES;          // SF area within it
+    constexpr int RING_A = NSTAGE * STAGE_A;
+    constexpr int LDS_BYTES = kSplitRing ? RING_A + NSB * B_BYTES : NSTAGE * STAGE;
+    static_assert(NSTAGE >= 2 && LDS_BYTES * OCC <= 160 * 1024, "LDS budget");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_BYTES];
+    auto a_slot = [&](int s) -> uint8_t* { return smem + s * STAGE_A; };
+    auto b_slot = [&](int sb) -> uint8_t* { return kSplitRing ? smem + RING_A + sb * B_BYTES : smem + sb * STAGE + A_BYTES; };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -798,17 +812,17 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         const int row = w * 128 + 2 * lane;
         sc_voff = (sc_live && row < (is_a ? rows_a : rows_b)) ? (uint32_t)(row * 2) : kOOBOffset;
         sc_step = __builtin_amdgcn_readfirstlane((int)((is_a ? p.sfa_ld : p.sfb_ld) * 2));
-        sc_lds = __builtin_amdgcn_readfirstlane(sc_live ? A_BYTES + B_BYTES + (is_a ? 0 : SCA) + w * 256
-                                                        : A_BYTES + B_BYTES + KM * SCU);
+        sc_lds = __builtin_amdgcn_readfirstlane(sc_live ? SC_OFF + (is_a ? 0 : SCA) + w * 256 : SC_OFF + KM * SCU);
     }
     constexpr int kDeadOffset = 0x40000000;   // scalar offset that moves every lane out of range
 
     // Load item IDX of stage c into ring slot s.  `live == false` turns it into an
     // out-of-range load (zeros into an idle slot, no memory traffic) so that every wave keeps
     // the same instruction stream and the code stays branch-free for the scheduler.
+    // (split ring: s is the B slot for B items)
     auto issue_item = [&](auto idx_tag, int c, int s, bool live) {
         constexpr int IDX = decltype(idx_tag)::value;
-        uint8_t* sbase = smem + s * STAGE;
+        uint8_t* sbase = a_slot(s);
         if constexpr (IDX < NLA + NLB) {
             constexpr bool kIsA = IDX < NLA;
             constexpr int it = kIsA ? IDX : IDX - NLA;
@@ -824,7 +838,7 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
             const uint32_t voff = kMN || (kIsA ? lk_a : lk_b) < krem ? (kIsA ? vbase_a : vbase_b) : kOOBOffset;
             const int soff = kb + it * (kIsA ? vstep_a : vstep_b);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                kIsA ? rs_a : rs_b, (lds_void*)(sbase + (kIsA ? 0 : A_BYTES) + (it * LT + lwave * 64) * 16), 16,
+                kIsA ? rs_a : rs_b, (lds_void*)((kIsA ? sbase : b_slot(s)) + (it * LT + lwave * 64) * 16), 16,
                 voff, __builtin_amdgcn_readfirstlane(live ? soff : kDeadOffset), 0, 0);
         } else if constexpr (!kBf16) {
             // packed-SF row of sub-step u of stage c (its k64 index is c * KM + u); a dead load
@@ -840,6 +854,14 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     auto issue_stage = [&](int c, int s, bool live) {
         static_for<NL>([&](auto i) { issue_item(i, c, s, live); });
     };
+    // split ring: A rows and SF of stage c into A slot s, then B rows of stage cb into B slot sb
+    // (issue order A, SF, B: a wait that leaves the last B items in flight covers A and SF)
+    auto issue_split = [&](int c, int s, bool live, int cb, int sb, bool live_b) {
+        static_for<NLA>([&](auto i) { issue_item(i, c, s, live); });
+        static_for<NL - NLA - NLB>([&](auto i) { issue_item(Int<NLA + NLB + decltype(i)::value>{}, c, s, live); });
+        static_for<NLB>([&](auto i) { issue_item(Int<NLA + decltype(i)::value>{}, cb, sb, live_b); });
+    };
+    constexpr int kMinLoadsB = SLB / LT;   // B items every loader wave issues per stage
 
     // ------------------------------------------------------------------ fragments
     auto frag_addr = [&](int R, int slot, auto spr_tag) -> int {
@@ -914,26 +936,26 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     int sa[2][TM];
     i32x8 fb0[2];
     int sb0[2];
-    auto load_ahead = [&](int s, auto part_tag, auto u_tag) {
+    auto load_ahead = [&](int s, int sb, auto part_tag, auto u_tag) {
         constexpr int part = decltype(part_tag)::value;   // TM: the B block, else A block `part`
         constexpr int u = decltype(u_tag)::value;
-        const uint8_t* st = smem + s * STAGE;
-        const uint8_t* sc = st + A_BYTES + B_BYTES + u * SCU;
+        const uint8_t* st = a_slot(s);
+        const uint8_t* sc = st + SC_OFF + u * SCU;
         if constexpr (part < TM) {
             const int R = wm * WM + part * 32 + r;
             if constexpr (AMN) return Pair<i32x8, int>{load_frag_mn(st, R - r, u_tag), kBf16 ? 0 : load_scale(sc, R)};
             else return Pair<i32x8, int>{load_frag(st, R, Int<SPRA>{}, u_tag), kBf16 ? 0 : load_scale(sc, R)};
         } else {
             const int R = wn * WN + r;
-            if constexpr (BMN) return Pair<i32x8, int>{load_frag_mn(st + A_BYTES, R - r, u_tag), kBf16 ? 0 : load_scale(sc + SCA, R)};
-            else return Pair<i32x8, int>{load_frag(st + A_BYTES, R, Int<SPRB>{}, u_tag),
+            if constexpr (BMN) return Pair<i32x8, int>{load_frag_mn(b_slot(sb), R - r, u_tag), kBf16 ? 0 : load_scale(sc + SCA, R)};
+            else return Pair<i32x8, int>{load_frag(b_slot(sb), R, Int<SPRB>{}, u_tag),
                                          kBf16 ? 0 : load_scale(sc + SCA, R)};
         }
     };
-    auto prefetch = [&](int s, auto buf_tag, auto part_tag, auto u_tag) {
+    auto prefetch = [&](int s, int sb, auto buf_tag, auto part_tag, auto u_tag) {
         constexpr int buf = decltype(buf_tag)::value;
         constexpr int part = decltype(part_tag)::value;
-        const auto v = load_ahead(s, part_tag, u_tag);
+        const auto v = load_ahead(s, sb, part_tag, u_tag);
         if constexpr (part < TM) { fa[buf][part] = v.first; sa[buf][part] = v.second; }
         else { fb0[buf] = v.first; sb0[buf] = v.second; }
     };
@@ -943,8 +965,10 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
     // crosses stages) into the other set, and -- in sub-step 0 -- issues the loads of stage cl
     // into slot sl, all interleaved with the MFMA groups (one group = the TM blocks of one jn).
     // TNX = the wave's number of 32-column blocks (TN, or TN_LAST in the last wave column).
+    // (sb / sbn: B slots of this and the next stage -- s / sn unless the ring is split -- and, split,
+    // B stage cl + 1 goes to B slot sb)
     auto compute = [&](int s, auto u_tag, auto buf_tag, auto loads_tag, auto tnx_tag, int sn, int cl, int sl,
-                       bool load_live) {
+                       bool load_live, int sb, int sbn, bool load_live_b) {
         constexpr int u = decltype(u_tag)::value;
         constexpr int buf = decltype(buf_tag)::value;
         // loads_tag: bit 0 = this wave issues global->LDS loads, bit 1 = its rows are all past the
@@ -955,8 +979,8 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         constexpr int TNX = decltype(tnx_tag)::value;
         constexpr int kLPG = (NL + TNX - 1) / TNX;
         constexpr bool kAhead = u + 1 < KM || kCross;
-        const uint8_t* sB = smem + s * STAGE + A_BYTES;
-        const uint8_t* sSB = smem + s * STAGE + A_BYTES + B_BYTES + u * SCU + SCA;
+        const uint8_t* sB = b_slot(sb);
+        const uint8_t* sSB = a_slot(s) + SC_OFF + u * SCU + SCA;
         i32x8 fb_cur = fb0[buf];
         int sb_cur = sb0[buf];
         static_for<TNX>([&](auto jn_c) {
@@ -972,12 +996,17 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
                 // late sync: this stage's slot s is no longer read by anyone after the barrier
                 // and stage cl - 1 has landed; refill s with stage cl and read stage cl - 1's
                 // first fragments (slot sn) into the sub-step-0 registers
-                wait_vmcnt<0>();
+                // (split ring: B of stage cl - 1, issued at the previous sync after A / SF of stage
+                // cl - 1, may stay in flight)
+                wait_vmcnt<kSplitRing ? kMinLoadsB : 0>();
                 stage_barrier();
-                static_for<TM + 1>([&](auto part_c) { prefetch(sn, Int<0>{}, part_c, Int<0>{}); });
+                static_for<TM + 1>([&](auto part_c) { prefetch(sn, sbn, Int<0>{}, part_c, Int<0>{}); });
                 // (the reads go out before this group's MFMAs, which then cover their latency)
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (kLoadWave && !kSpread) issue_stage(cl, sl, load_live);
+                if constexpr (kLoadWave && !kSpread) {
+                    if constexpr (kSplitRing) issue_split(cl, sl, load_live, cl + 1, sb, load_live_b);
+                    else issue_stage(cl, sl, load_live);
+                }
             }
             static_for<TM>([&](auto jm_c) {
                 constexpr int jm = decltype(jm_c)::value;
@@ -1004,8 +1033,8 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
                     constexpr int part = decltype(part_c)::value;
                     constexpr int grp = part < TM ? part * TNX / TM : TNX - 1;
                     if constexpr (grp == jn) {
-                        if constexpr (u + 1 < KM) prefetch(s, Int<buf ^ 1>{}, Int<part>{}, Int<u + 1>{});
-                        else prefetch(sn, Int<buf ^ 1>{}, Int<part>{}, Int<0>{});
+                        if constexpr (u + 1 < KM) prefetch(s, sb, Int<buf ^ 1>{}, Int<part>{}, Int<u + 1>{});
+                        else prefetch(sn, sbn, Int<buf ^ 1>{}, Int<part>{}, Int<0>{});
                     }
                 });
             }
@@ -1028,10 +1057,15 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         constexpr int st = decltype(i)::value;
         if (is_loader) issue_stage(c0 + st - shift, st, st >= shift && st < num_virtual);
     });
+    if constexpr (kSplitRing) {
+        // (split ring: B of stage 2 into B slot 2 as well; stages 0 and 1 went out whole)
+        if (is_loader)
+            static_for<NLB>([&](auto i) { issue_item(Int<NLA + decltype(i)::value>{}, c0 + 2, 2, 2 < num_virtual); });
+    }
     if constexpr (kCross || kLate) {
-        wait_vmcnt<(kPro - 1) * kMinLoadsPerStage>();
+        wait_vmcnt<(kPro - 1) * kMinLoadsPerStage + (kSplitRing ? kMinLoadsB : 0)>();
         stage_barrier();
-        static_for<TM + 1>([&](auto part_c) { prefetch(0, Int<0>{}, part_c, Int<0>{}); });
+        static_for<TM + 1>([&](auto part_c) { prefetch(0, 0, Int<0>{}, part_c, Int<0>{}); });
     }
 
     // Cross-stage ring: stage c + 1 must have landed before the barrier of iteration c (its ahead
@@ -1050,12 +1084,12 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         const int cl = c + (kLate && !kSpread ? 2 : NSTAGE - 1);
         constexpr int buf0 = KM == 1 ? decltype(pbuf_tag)::value : 0;
         if constexpr (!kCross && !kLate)
-            static_for<TM + 1>([&](auto part_c) { prefetch(c % NSTAGE, Int<buf0>{}, part_c, Int<0>{}); });
+            static_for<TM + 1>([&](auto part_c) { prefetch(c % NSTAGE, c % NSTAGE, Int<buf0>{}, part_c, Int<0>{}); });
         static_for<KM>([&](auto u_c) {
             constexpr int u = decltype(u_c)::value;
             constexpr int buf = KM == 1 ? decltype(pbuf_tag)::value : u;
             compute(c % NSTAGE, u_c, Int<buf>{}, loads_tag, tnx_tag, (c + 1) % NSTAGE, c0 + cl - shift, cl % NSTAGE,
-                    cl < num_virtual);
+                    cl < num_virtual, c % NSB, (c + 1) % NSB, cl + 1 < num_virtual);
         });
     };
     // Loader and non-loader waves run separate copies of the loop, each branch-free.
@@ -1208,9 +1242,9 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
 
 // The ahead-of-time kernel of one tile shape: everything from the arguments.
 template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI, bool AMN = false,
-          bool BMN = false>
+          bool BMN = false, int NSB = 0>
 __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KParams p) {
-    gemm_body<BM, BN, WGM, NW, LW, NSTAGE, KM, OCC, KIND, EPI, -1, 0, 0, 0, 0, AMN, BMN>(p);
+    gemm_body<BM, BN, WGM, NW, LW, NSTAGE, KM, OCC, KIND, EPI, -1, 0, 0, 0, 0, AMN, BMN, NSB>(p);
 }
 
 }  // namespace dg

@@ -23,6 +23,8 @@ struct TileCfg {
     int occ;      // workgroups per CU (2: LDS ring and registers sized for two co-resident
                   // workgroups, whose prologues and epilogues then overlap each other's main loops)
     int stage_cycles;   // measured cycles per 64 K with every CU busy (fp8, MI355X)
+    int nsb = 0;        // 3: B rows get a ring of three slots beside the two of A + SF, where that fits
+                        // the LDS for the kind (0: one shared ring)
 };
 
 // Measured on MI355X (fp8, cold L2): 4096x7168x2048 256x224 70 us, 256x256 72 us; 4096x2112x7168 256x160
@@ -30,9 +32,9 @@ struct TileCfg {
 // experts, ~257 rows each, alignment 128) N=4096 K=7168: 128x256 as 8 waves / one workgroup per CU 572 us, as
 // 4 waves / two workgroups per CU 509 us; skinny M=128, N=7168, K=16384: 128x128 split 4 57 us.
 constexpr TileCfg kTiles[] = {
-    {256, 256, 4, 8, 4, 2, 2, 1, 1380}, {256, 224, 4, 8, 4, 2, 2, 1, 1250}, {256, 128, 4, 8, 8, 4, 1, 1, 937},
+    {256, 256, 4, 8, 4, 2, 2, 1, 1380, 3}, {256, 224, 4, 8, 4, 2, 2, 1, 1250, 3}, {256, 128, 4, 8, 8, 4, 1, 1, 937},
     {128, 256, 2, 4, 4, 3, 1, 2, 985},  {128, 128, 2, 4, 4, 4, 1, 1, 1056}, {64, 128, 2, 4, 4, 6, 1, 2, 588},
-    {32, 128, 1, 4, 4, 6, 1, 2, 643},  {256, 160, 4, 8, 4, 2, 2, 1, 950},
+    {32, 128, 1, 4, 4, 6, 1, 2, 643},  {256, 160, 4, 8, 4, 2, 2, 1, 950, 3},
     // tiles anchored at each group's first row (M-grouped psum layouts only)
     {384, 192, 4, 8, 8, 2, 2, 1, 1250}, {384, 128, 4, 8, 4, 2, 2, 1, 1000},
 };
@@ -46,12 +48,12 @@ template <int I, int KIND>
 KernelFn pick_epi(int epi) {
     constexpr TileCfg t = kTiles[I];
     switch (epi) {
-        case kEpiF32: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiF32>;
-        case kEpiBf16: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiBf16>;
-        case kEpiBf16SR: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiBf16SR>;
+        case kEpiF32: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiF32, false, false, t.nsb>;
+        case kEpiBf16: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiBf16, false, false, t.nsb>;
+        case kEpiBf16SR: return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiBf16SR, false, false, t.nsb>;
         case kEpiFp8:
             // FP8 output exists for e4m3 x e4m3 batched / dense GEMMs only (fp8_bmm)
-            if constexpr (KIND == kFP8FP8) return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiFp8>;
+            if constexpr (KIND == kFP8FP8) return &gemm_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiFp8, false, false, t.nsb>;
             else return nullptr;
         default: return nullptr;
     }

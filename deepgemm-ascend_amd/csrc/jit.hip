@@ -125,10 +125,10 @@ std::string source_of(const Spec& s) {
     snprintf(buf, sizeof(buf),
              "#include \"gemm_kernel.hpp\"\n"
              "extern \"C\" __global__ __launch_bounds__(%d, %d) void dg_jit_kernel(const dg::KParams p) {\n"
-             "    dg::gemm_body<%d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d>(p);\n"
+             "    dg::gemm_body<%d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, false, false, %d>(p);\n"
              "}\n",
              s.t.nw * 64, s.t.occ * s.t.nw / 4, s.t.bm, s.t.bn, s.t.wgm, s.t.nw, s.t.lw, s.t.stages, s.t.km, s.t.occ,
-             s.kind, s.epi, s.ct, s.cs, s.cm, s.cn, s.ck);
+             s.kind, s.epi, s.ct, s.cs, s.cm, s.cn, s.ck, s.t.nsb);
     return buf;
 }
 
