@@ -114,6 +114,63 @@ __global__ __launch_bounds__(256) void transpose_to_k_major_kernel(const Transpo
     }
 }
 
+
+// FP4 (e2m1) operand packed along MN -> packed along K.  Source byte (b, k, j) holds MN 2j (low
+// nibble) and 2j + 1 (high nibble) of K row k; output byte (b, mn, j) holds K 2j (low) and 2j + 1
+// (high) of MN row mn, zero past k.  One workgroup moves 64 K x 128 MN: it loads 64 source rows
+// of 64 bytes (16 bytes a thread, one coalesced line per 4 threads) into LDS, then each thread
+// gathers the 32 nibble pairs of 16 output bytes of one MN row and stores them at once.
+struct Fp4RepackParams {
+    const uint8_t* src;
+    uint8_t* dst;
+    int64_t src_bs, src_ld, dst_bs, dst_ld;   // bytes
+    int k, mn, k_padded;                      // elements
+};
+
+__global__ __launch_bounds__(256) void fp4_repack_k_major_kernel(const Fp4RepackParams p) {
+    constexpr int TK = 64, TMN = 128, PITCH = TMN / 2 + 4;   // (+4: rows 16 lanes apart on other banks)
+    __shared__ __align__(16) uint8_t tile[TK][PITCH];
+    const int tid = threadIdx.x;
+    const int k0 = blockIdx.x * TK, mn0 = blockIdx.y * TMN, b = blockIdx.z;
+    const uint8_t* src = p.src + (int64_t)b * p.src_bs;
+    uint8_t* dst = p.dst + (int64_t)b * p.dst_bs;
+    const int mnb = (p.mn + 1) / 2;                            // source bytes of a K row
+    {
+        const int kr = tid / 4, cb = (tid % 4) * 16;           // K row of the tile, byte of its row
+        const int k = k0 + kr, j = mn0 / 2 + cb;
+        i32x4 w = {0, 0, 0, 0};
+        if (k < p.k) {
+            const uint8_t* s = src + (int64_t)k * p.src_ld + j;
+            if (j + 16 <= mnb && (reinterpret_cast<uintptr_t>(s) % 16) == 0) {
+                w = *reinterpret_cast<const i32x4*>(s);
+            } else {
+                uint8_t* wb = reinterpret_cast<uint8_t*>(&w);
+                for (int e = 0; e < 16; ++e)
+                    if (j + e < mnb) wb[e] = s[e];
+            }
+        }
+        *reinterpret_cast<i32x4*>(&tile[kr][cb]) = w;   // (PITCH keeps 16-byte alignment: 68 = 4 x 17)
+    }
+    __syncthreads();
+    const int r = tid / 2, half = tid % 2;                     // MN row of the tile, 32-K half
+    const int mn = mn0 + r, kb = k0 / 2 + half * 16;           // output byte of the row
+    if (mn >= p.mn || 2 * kb >= p.k_padded) return;
+    const int sh = (r & 1) * 4;
+    i32x4 o;
+    uint8_t* ob = reinterpret_cast<uint8_t*>(&o);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int kk = half * 32 + 2 * j;                      // K of the tile (rows past k hold zeros)
+        const uint32_t lo = (tile[kk][r / 2] >> sh) & 15u, hi = (tile[kk + 1][r / 2] >> sh) & 15u;
+        ob[j] = (uint8_t)(lo | (hi << 4));
+    }
+    uint8_t* d = dst + (int64_t)mn * p.dst_ld + kb;
+    if (2 * kb + 32 <= p.k_padded) {
+        *reinterpret_cast<i32x4*>(d) = o;
+    } else {
+        for (int j = 0; 2 * (kb + j) < p.k_padded; ++j) d[j] = ob[j];
+    }
+}
 }  // namespace dg
 
 extern "C" __attribute__((visibility("hidden"))) int dg_set_error(const char* msg);
@@ -142,6 +199,34 @@ extern "C" int dg_transpose_to_k_major(const void* src, int32_t elem_bytes, int3
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (elem_bytes == 1) hipLaunchKernelGGL(transpose_to_k_major_kernel<1>, grid, dim3(256), 0, st, p);
     else hipLaunchKernelGGL(transpose_to_k_major_kernel<2>, grid, dim3(256), 0, st, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        dg_set_error(hipGetErrorString(e));
+        return DG_ELAUNCH;
+    }
+    return DG_OK;
+}
+
+extern "C" int dg_fp4_to_k_major(const void* src, int32_t batches, int64_t src_batch_stride, int64_t src_ld, int32_t k,
+                                 int32_t mn, void* dst, int64_t dst_batch_stride, int64_t dst_ld, int32_t k_padded,
+                                 void* stream) {
+    using namespace dg;
+    if (src == nullptr || dst == nullptr) return dg_set_error("dg_fp4_to_k_major: null pointer");
+    if (batches < 1 || k < 0 || mn < 0 || k_padded < k || k_padded % 2)
+        return dg_set_error("dg_fp4_to_k_major: bad sizes");
+    if (src_ld < (mn + 1) / 2 || dst_ld * 2 < k_padded)
+        return dg_set_error("dg_fp4_to_k_major: leading dimension too small");
+    if (dst_ld % 16 || (reinterpret_cast<uintptr_t>(dst) % 16) || (batches > 1 && dst_batch_stride % 16))
+        return dg_set_error("dg_fp4_to_k_major: destination rows must be 16-byte aligned");
+    if (mn == 0 || k_padded == 0) return DG_OK;
+    Fp4RepackParams p;
+    p.src = reinterpret_cast<const uint8_t*>(src);
+    p.dst = reinterpret_cast<uint8_t*>(dst);
+    p.src_bs = src_batch_stride; p.src_ld = src_ld; p.dst_bs = dst_batch_stride; p.dst_ld = dst_ld;
+    p.k = k; p.mn = mn; p.k_padded = k_padded;
+    const dim3 grid((unsigned)ceil_div(k_padded, 64), (unsigned)ceil_div(mn, 128), (unsigned)batches);
+    if (grid.y > 65535u || grid.z > 65535u) return dg_set_error("dg_fp4_to_k_major: too many tiles");
+    hipLaunchKernelGGL(fp4_repack_k_major_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         dg_set_error(hipGetErrorString(e));

@@ -21,7 +21,7 @@ DG_SF_F32, DG_SF_I16 = 0, 1
 DG_COMPILED_M, DG_COMPILED_N, DG_COMPILED_K = 1, 2, 4
 
 # Every symbol include/deep_gemm_amd.h declares.
-EXPORTED_SYMBOLS = ('dg_gemm', 'dg_transform_sf', 'dg_transform_k_grouped_sf', 'dg_transpose_to_k_major', 'dg_device_num_cus', 'dg_select_config',
+EXPORTED_SYMBOLS = ('dg_gemm', 'dg_transform_sf', 'dg_transform_k_grouped_sf', 'dg_transpose_to_k_major', 'dg_fp4_to_k_major', 'dg_device_num_cus', 'dg_select_config',
                     'dg_gemm_workspace_size', 'dg_last_error', 'dg_version', 'dg_jit_compile', 'dg_jit_set_include_dir',
                     'dg_jit_stats', 'dg_launch_plan', 'dg_gemm_noalloc', 'dg_take_errors', 'dg_error_words',
                     'dg_stream_workspace')
@@ -100,6 +100,10 @@ def load(path=None) -> ctypes.CDLL:
             ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
             ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p]
         lib.dg_transpose_to_k_major.restype = ctypes.c_int
+        lib.dg_fp4_to_k_major.argtypes = [
+            ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+            ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p]
+        lib.dg_fp4_to_k_major.restype = ctypes.c_int
         lib.dg_device_num_cus.argtypes = [ctypes.c_int32]
         lib.dg_device_num_cus.restype = ctypes.c_int
         lib.dg_select_config.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(ctypes.c_int32),

@@ -62,13 +62,8 @@ def _to_kernel_operand(t: torch.Tensor, k: int) -> torch.Tensor:
     if fp4:
         t = _as_int8(t)
         if not k_major:
-            # packed along MN -> unpack the nibble pairs, re-pack along K
-            u = t.transpose(-2, -1).contiguous().view(torch.uint8)          # [..., K, MN/2]
-            lo, hi = u & 0x0f, u >> 4
-            codes = torch.stack((lo, hi), dim=-1).reshape(*u.shape[:-1], u.shape[-1] * 2)  # [..., K, MN]
-            codes = codes.transpose(-2, -1).contiguous()                      # [..., MN, K]
-            packed = codes[..., 0::2] | (codes[..., 1::2] << 4)
-            t = packed.view(torch.int8)
+            # packed along MN -> packed along K, one pass of the HIP repack kernel
+            return _fp4_to_k_major(t, k)
         kbytes, align_elems, esize = k // 2, 32, 1
     else:
         if not k_major:
@@ -85,6 +80,23 @@ def _to_kernel_operand(t: torch.Tensor, k: int) -> torch.Tensor:
     store_k = kpad // 2 if fp4 else kpad
     out = torch.zeros((*t.shape[:-1], store_k), dtype=t.dtype, device=t.device)
     out[..., :t.size(-1)] = t
+    return out
+
+
+def _fp4_to_k_major(t: torch.Tensor, k: int) -> torch.Tensor:
+    """FP4 operand packed along MN (an int8 [.., MN/2, K] view, stride(-2) == 1: bytes hold MN pairs)
+    -> new [.., MN, align(K, 32) / 2] int8 tensor packed along K (zero K padding)."""
+    if t.stride(-1) < t.size(-2) or (t.dim() == 3 and t.stride(0) < t.size(-2) * t.size(-1)):
+        t = t.transpose(-2, -1).contiguous().transpose(-2, -1)   # explicit [.., K, MN/2] rows
+    mn, kpad = t.size(-2) * 2, (k + 31) // 32 * 32
+    out = torch.empty((*t.shape[:-2], mn, kpad // 2), dtype=torch.int8, device=t.device)
+    if out.numel() == 0 or get_dry_run():
+        return out
+    batches = t.size(0) if t.dim() == 3 else 1
+    lib = _lib.load()
+    _lib.check(lib.dg_fp4_to_k_major(
+        t.data_ptr(), batches, t.stride(0) if t.dim() == 3 else 0, t.stride(-1), k, mn,
+        out.data_ptr(), mn * kpad // 2, kpad // 2, kpad, _stream(t)), lib)
     return out
 
 

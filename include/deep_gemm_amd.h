@@ -194,6 +194,18 @@ int dg_transpose_to_k_major(const void *src, int32_t elem_bytes, int32_t batches
                             int64_t src_ld, int32_t k, int32_t mn, void *dst, int64_t dst_batch_stride,
                             int64_t dst_ld, int32_t k_padded, void *stream);
 
+/*
+ * FP4 (e2m1) operand packed along MN -> packed along K (the reference takes FP4 operands of either
+ * major, deep_gemm/include/deep_gemm/fp8_gemm.hpp:18-35; this build's kernels read FP4 packed along K).
+ * src byte (b, k, j) = MN 2j (low nibble) and 2j + 1 (high) of K row k, at
+ * src[b*src_batch_stride + k*src_ld + j]; dst byte (b, mn, j) = K 2j (low) and 2j + 1 (high) of MN
+ * row mn, at dst[b*dst_batch_stride + mn*dst_ld + j], zero for K >= k up to k_padded (even).  Strides
+ * in bytes; dst rows and batches 16-byte aligned.
+ */
+int dg_fp4_to_k_major(const void *src, int32_t batches, int64_t src_batch_stride, int64_t src_ld, int32_t k,
+                      int32_t mn, void *dst, int64_t dst_batch_stride, int64_t dst_ld, int32_t k_padded,
+                      void *stream);
+
 /* Number of compute units of `device` (the reference's get_num_sms, csrc/apis/runtime.hpp:13-19). */
 int dg_device_num_cus(int32_t device);
 
