@@ -40,7 +40,7 @@ def parse():
     ap.add_argument('--n', type=int, default=N)
     ap.add_argument('--k', type=int, default=K)
     ap.add_argument('--suite', default=None,
-                    help='comma list of dense,bf16,fp4,grouped,kgrouped,einsum,host: one JSON line per shape '
+                    help='comma list of dense,decode,bf16,fp4,grouped,kgrouped,einsum,host: one JSON line per shape '
                          '(cold-L2 kernel times) instead of the north-star line')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a 256 MiB device copy (reference kernel for FETCH_SIZE / WRITE_SIZE scaling)')
@@ -215,8 +215,9 @@ def run_suite(groups):
         sf_shape = ((batch,) if batch else ()) + (-(-rows // gran_mn), -(-k // 128))
         return _gpu_codes(shape, dev, gen), _gpu_sf(sf_shape, dev, gen)
 
-    if 'dense' in groups:
-        for m in (1, 64, 128, 4096):
+    if 'dense' in groups or 'decode' in groups:
+        # ('decode': the M <= 4 rows alone, M = 1, 2, 4)
+        for m in ((1, 64, 128, 4096) if 'dense' in groups else (1, 2, 4)):
             for n, k in NK:
                 a, sfa = fp8_operand(m, k, 1)
                 b, sfb = fp8_operand(n, k, 128)

@@ -98,6 +98,7 @@ struct Plan {
     int skinny_d;       // its ring depth
     int skinny_ar;      // and rows of A it stages
     int skinny_rows;    // 1: the shared-ring decode kernel (skinny_rows_kernel, skinny_nw = mt x nb waves, ring skinny_d)
+    int gemv_mr;        // > 0: the decode GEMV kernel for M <= gemv_mr (split_stages = rows of B per wave)
 };
 
 // K elements of one kernel stage of tile t
@@ -422,7 +423,8 @@ namespace {
 std::mutex g_func_mu;
 std::unordered_map<const void*, hipFunction_t> g_funcs;
 
-hipError_t launch_module_kernel(const void* kernel, unsigned grid, unsigned threads, dg::KParams& p, hipStream_t st) {
+hipError_t launch_module_kernel(const void* kernel, unsigned grid, unsigned threads, dg::KParams& p, hipStream_t st,
+                                unsigned lds_bytes = 0) {
     hipFunction_t f = nullptr;
     {
         std::lock_guard<std::mutex> lk(g_func_mu);
@@ -436,7 +438,7 @@ hipError_t launch_module_kernel(const void* kernel, unsigned grid, unsigned thre
         }
     }
     void* params[] = {&p};
-    return hipModuleLaunchKernel(f, grid, 1, 1, threads, 1, 1, 0, st, params, nullptr);
+    return hipModuleLaunchKernel(f, grid, 1, 1, threads, 1, 1, lds_bytes, st, params, nullptr);
 }
 
 // Split-K workspaces the library owns, one per (device, stream): zero-filled when allocated, left
@@ -584,8 +586,40 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     const int epi_kind = a.d_dtype == DG_DTYPE_F32 ? kEpiF32
                        : a.d_dtype == DG_DTYPE_FP8_E4M3 ? kEpiFp8
                        : a.epilogue == DG_EPI_BF16_SR ? kEpiBf16SR : kEpiBf16;
+    // Decode GEMV kernel (e4m3 x e4m3, dense or batched, fp32 / bf16 D without an output
+    // epilogue): workgroups of 8 waves over groups of 8 rows of B, K split ks ways between the
+    // waves of a workgroup (never across workgroups); ks doubles (up to 8) while each K range keeps
+    // at least 8 steps of 128 bytes.  By default for M = 1 with K >= 4096, where it measured ahead
+    // of the MFMA decode kernel (MI355X, kernel us, cold L2: 1x2112x7168 7.3 vs 9.3, 1x4096x7168
+    // 8.9 vs 10.5, 1x7168x16384 24.4 vs 25.4); behind it at 1x7168x2048 (6.1 vs 5.8), 1x24576x1536
+    // (11.1 vs 10.4) and for M = 2 (2x2112x7168 9.5 vs 8.8), where the VALU work per byte of B
+    // doubles.  DG_GEMV forces it for M <= 4 (with ks = 1, 2, 4 or 8; "0" turns it off).  Not
+    // under a CU cap (set_num_sms) or a forced plan (tuning overrides).
+    int gemv_mr = 0, gemv_ks = 0;
+    {
+        const char* gemv_env = std::getenv("DG_GEMV");   // "0" = off, "1" / "2" / "4" / "8" = forced ks (tuning)
+        const int env_ks = gemv_env != nullptr && gemv_env[0] != '\0' ? std::atoi(gemv_env) : -1;
+        const int mr = a.m <= 1 ? 1 : a.m <= 2 ? 2 : 4;
+        const int groups_g = a.gemm_type == kBatched ? a.num_groups : 1;
+        const bool wanted = env_ks > 0 ? a.m <= 4 : env_ks == -1 && a.m == 1 && a.k >= 4096;
+        if (wanted && a.kind == kFP8FP8 && (a.gemm_type == kNormal || a.gemm_type == kBatched) && a.m >= 1 &&
+            a.k > 0 && !amn && !bmn && (epi_kind == kEpiF32 || epi_kind == kEpiBf16) && a.block_m <= 0 &&
+            a.split_k <= 1 && !cus_capped(cus) && skinny_env().mode == -1) {
+            const int pk = ceil_div(a.k, 128);
+            int ks = 1;
+            if (env_ks == 1 || env_ks == 2 || env_ks == 4 || env_ks == 8) ks = env_ks;
+            else
+                while (ks < 8 && pk >= 16 * ks) ks *= 2;
+            if (gemv_lds(mr, a.k, ks) <= 64 * 1024 && 64LL * ldb_b < 0x40000000LL &&
+                (int64_t)ceil_div(a.k, 64) * a.sfb_ld * 2 + 2 * (int64_t)a.n < 0x7fffffffLL &&
+                lookup_gemv(mr, epi_kind) != nullptr) {
+                gemv_mr = mr;
+                gemv_ks = ks;
+            }
+        }
+    }
     // (the skinny-M kernel is not specialised per problem: the JIT setting leaves it ahead-of-time)
-    const bool skinny = plan.skinny_nw > 0;
+    const bool skinny = plan.skinny_nw > 0 || gemv_mr > 0;
     const bool jit = a.jit && !skinny;
     if (skinny && compile_only && info == nullptr) return DG_OK;
     // Persistent launch (one workgroup per CU walking the tiles, the LDS ring running on across
@@ -648,11 +682,11 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     static const int group_m_env = std::getenv("DG_GROUP_M") ? std::atoi(std::getenv("DG_GROUP_M")) : 0;   // tuning
     p.group_m = group_m_env > 0 ? group_m_env : 4;
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
-    const int64_t tiles = (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
+    int64_t tiles = (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
     if (tiles <= 0) return DG_OK;
     // split-K grids are padded to whole groups of 8 tiles (one per XCD); persistent grids hold
     // one workgroup per CU (set_num_sms caps them)
-    const int64_t grid = persistent ? std::min<int64_t>(tiles, (int64_t)cus * cfg.occ)
+    int64_t grid = persistent ? std::min<int64_t>(tiles, (int64_t)cus * cfg.occ)
                        : plan.split > 1 ? align_up64(tiles, 8) * plan.split : tiles;
     p.a_span = a_span; p.b_span = b_span; p.sfa_span = sfa_span; p.sfb_span = sfb_span;
     if (grid > 0x7fffffffLL) return dg_set_error("dg_gemm: too many tiles");
@@ -666,16 +700,32 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         p.counters = reinterpret_cast<int*>(workspace);
         p.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + kCounterBytes);
     }
-    const int threads = skinny ? plan.skinny_nw * 64 : tile_threads(cfg.bm, cfg.bn);
+    int threads = skinny ? plan.skinny_nw * 64 : tile_threads(cfg.bm, cfg.bn);
+    unsigned lds_bytes = 0;
+    if (gemv_mr > 0) {
+        // workgroups of 64 / ks rows of B, dealt over the XCDs in contiguous runs
+        fn = lookup_gemv(gemv_mr, epi_kind);
+        const int groups_g = a.gemm_type == kBatched ? a.num_groups : 1;
+        p.split_k = 1;
+        p.split_stages = gemv_ks;
+        p.num_n_blocks = ceil_div(a.n, 64 / gemv_ks);
+        const int64_t wgs = (int64_t)p.num_n_blocks * groups_g;
+        if (wgs > 0x7ffffff0LL) return dg_set_error("dg_gemm: too many tiles");
+        p.num_tiles = (int)wgs;
+        tiles = wgs;
+        grid = align_up64(wgs, 8);
+        threads = 8 * 64;
+        lds_bytes = (unsigned)gemv_lds(gemv_mr, a.k, gemv_ks);
+    }
     if (info != nullptr) {
-        info->block_m = cfg.bm;
-        info->block_n = cfg.bn;
+        info->block_m = gemv_mr > 0 ? gemv_mr : cfg.bm;
+        info->block_n = gemv_mr > 0 ? 64 / gemv_ks : cfg.bn;
         info->grid = grid;
         info->threads = threads;
         info->tiles = tiles;
-        info->split_k = plan.split;
+        info->split_k = gemv_mr > 0 ? 1 : plan.split;
         info->persistent = persistent ? 1 : 0;
-        info->skinny = skinny ? (plan.skinny_rows ? 2 : 1) : 0;
+        info->skinny = gemv_mr > 0 ? 3 : skinny ? (plan.skinny_rows ? 2 : 1) : 0;
         return DG_OK;
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -703,7 +753,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         }
     }
     if (jit) return jit_run(a, cfg, epi_kind, plan.split, p, grid, st, compile_only);
-    const hipError_t e = launch_module_kernel(reinterpret_cast<const void*>(fn), (unsigned)grid, (unsigned)threads, p, st);
+    const hipError_t e = launch_module_kernel(reinterpret_cast<const void*>(fn), (unsigned)grid, (unsigned)threads, p, st, lds_bytes);
     if (e != hipSuccess) {
         dg_set_error(hipGetErrorString(e));
         return DG_ELAUNCH;

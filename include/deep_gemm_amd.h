@@ -264,7 +264,7 @@ typedef struct dg_launch_info {
     int64_t tiles;                /* output tiles (strips) of the problem                         */
     int32_t split_k;              /* K ranges per tile (1 = unsplit)                              */
     int32_t persistent;           /* 1: workgroups walk tiles (grid < tiles possible)             */
-    int32_t skinny;               /* 1: the decode-shape kernel, 2: its shared-ring variant        */
+    int32_t skinny;               /* 1: the decode-shape kernel, 2: its shared-ring variant, 3: the decode GEMV kernel (block_m = M rows served, block_n = rows of B per workgroup, 64 / its K split) */
 } dg_launch_info;
 int dg_launch_plan(const dg_gemm_args *args, dg_launch_info *info);
 
