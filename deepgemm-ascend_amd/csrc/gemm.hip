@@ -589,11 +589,11 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     // Decode GEMV kernel (e4m3 x e4m3, dense or batched, fp32 / bf16 D without an output
     // epilogue): workgroups of 8 waves over groups of 8 rows of B, K split ks ways between the
     // waves of a workgroup (never across workgroups); ks doubles (up to 8) while each K range keeps
-    // at least 8 steps of 128 bytes.  By default for M = 1 with K >= 4096, where it measured ahead
-    // of the MFMA decode kernel (MI355X, kernel us, cold L2: 1x2112x7168 7.3 vs 9.3, 1x4096x7168
-    // 8.9 vs 10.5, 1x7168x16384 24.4 vs 25.4); behind it at 1x7168x2048 (6.1 vs 5.8), 1x24576x1536
-    // (11.1 vs 10.4) and for M = 2 (2x2112x7168 9.5 vs 8.8), where the VALU work per byte of B
-    // doubles.  DG_GEMV forces it for M <= 4 (with ks = 1, 2, 4 or 8; "0" turns it off).  Not
+    // at least 8 steps of 128 bytes.  By default for M = 1 with 4096 <= K <= 8192, where it measured
+    // ahead of the MFMA decode kernel (MI355X, kernel us, cold L2, two boxes: 1x2112x7168 7.3 vs
+    // 9.0-9.3, 1x4096x7168 8.8-8.9 vs 10.4-10.5); level at 1x7168x16384 (24.2-24.4 vs 23.0-25.4),
+    // behind at 1x7168x2048 (6.1 vs 5.8), 1x24576x1536 (11.1 vs 10.4) and for M = 2 (2x2112x7168
+    // 9.5 vs 8.8), where the VALU work per byte of B doubles.  DG_GEMV forces it for M <= 4 (with ks = 1, 2, 4 or 8; "0" turns it off).  Not
     // under a CU cap (set_num_sms) or a forced plan (tuning overrides).
     int gemv_mr = 0, gemv_ks = 0;
     {
@@ -601,7 +601,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         const int env_ks = gemv_env != nullptr && gemv_env[0] != '\0' ? std::atoi(gemv_env) : -1;
         const int mr = a.m <= 1 ? 1 : a.m <= 2 ? 2 : 4;
         const int groups_g = a.gemm_type == kBatched ? a.num_groups : 1;
-        const bool wanted = env_ks > 0 ? a.m <= 4 : env_ks == -1 && a.m == 1 && a.k >= 4096;
+        const bool wanted = env_ks > 0 ? a.m <= 4 : env_ks == -1 && a.m == 1 && a.k >= 4096 && a.k <= 8192;
         if (wanted && a.kind == kFP8FP8 && (a.gemm_type == kNormal || a.gemm_type == kBatched) && a.m >= 1 &&
             a.k > 0 && !amn && !bmn && (epi_kind == kEpiF32 || epi_kind == kEpiBf16) && a.block_m <= 0 &&
             a.split_k <= 1 && !cus_capped(cus) && skinny_env().mode == -1) {

@@ -15,11 +15,11 @@ pytestmark = pytest.mark.gpu
 THRESH = 1e-5
 
 
-@pytest.mark.parametrize('m,n,k,ks', [(1, 2112, 7168, ''), (1, 7168, 16384, ''), (1, 4096, 7168, ''),
+@pytest.mark.parametrize('m,n,k,ks', [(1, 2112, 7168, ''), (1, 7168, 16384, '8'), (1, 4096, 7168, ''),
                                       (1, 24576, 1536, '2'), (1, 7168, 2048, '2'), (2, 4096, 7168, '4'),
                                       (4, 7168, 2048, '2')])
 def test_gemv_plan_and_parity_baseline_shapes(monkeypatch, m, n, k, ks):
-    """BASELINE config-2 decode shapes through the GEMV kernel (the default plan at M = 1, K >= 4096;
+    """BASELINE config-2 decode shapes through the GEMV kernel (the default plan at M = 1, 4096 <= K <= 8192;
     forced with DG_GEMV elsewhere), D against the oracle (N(0,1) data, 1x128 / 128x128 recipe)."""
     monkeypatch.setenv('DG_GEMV', ks)
     plan = deep_gemm.launch_plan(m, n, k)
@@ -51,7 +51,7 @@ def test_gemv_ragged_codes(monkeypatch, ks, n, k):
         # LDS of a workgroup (A as f16, its scale bytes, 64 row sums per row of A) is at most 64 KB
         mr, kp = (1 if m == 1 else 2 if m == 2 else 4), -(-k // 128) * 128
         lds = mr * kp * 2 + mr * kp // 32 + mr * 64 * 4
-        assert (plan['skinny'] == 3) == (lds <= 64 * 1024 and (ks != '' or (m == 1 and k >= 4096)))
+        assert (plan['skinny'] == 3) == (lds <= 64 * 1024 and (ks != '' or (m == 1 and 4096 <= k <= 8192)))
         a, sfa, a_deq = operand(m, k, 'e4m3', (1, 32), g)
         d = torch.empty(m, n, dtype=torch.float32, device='cuda')
         deep_gemm.fp8_gemm_nt((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d)
