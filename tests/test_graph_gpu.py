@@ -1,6 +1,7 @@
 """GEMM launches captured in a HIP graph (torch.cuda.CUDAGraph on the current stream): decode shapes on
-the skinny-M kernel (with and without a cross-workgroup K split, whose arrival counters the kernel
-itself resets: no memset node in the graph), the tile kernel and an M-grouped masked launch.  Every
+the GEMV kernel (1x2112x7168) and the skinny-M kernel (with a cross-workgroup K split, whose arrival
+counters the kernel itself resets: no memset node in the graph), the tile kernel and an M-grouped
+masked launch.  Every
 replay, with eager work between the replays, matches the eager launch bit for bit."""
 import pytest
 import torch
@@ -21,7 +22,8 @@ def _dense_case(m, n, k, seed):
     return (a, sfa), (b, sfb)
 
 
-@pytest.mark.parametrize('m,n,k', [(1, 2112, 7168), (16, 7168, 2048), (128, 4096, 7168), (4096, 2112, 1024)])
+@pytest.mark.parametrize('m,n,k', [(1, 2112, 7168), (1, 2112, 2048), (16, 7168, 2048), (128, 4096, 7168),
+                                   (4096, 2112, 1024)])
 def test_graph_replay_dense(m, n, k):
     print(f'graph dense m={m} n={n} k={k}', flush=True)
     a, b = _dense_case(m, n, k, seed=m + n)
