@@ -49,7 +49,10 @@ __device__ __forceinline__ void fp8x16_to_f16(const i32x4 x, h2* h) {
 }
 
 constexpr int kGemvWaves = 8;
-constexpr int kGemvDepth = 8;   // steps in flight per wave
+// Steps in flight per wave.  Six keep M <= 2 within 64 VGPRs (eight waves per SIMD, so that every
+// workgroup of a launch fits one round: 1x24576x1536 10.0 vs 11.0 us with eight steps at 73 VGPRs,
+// the other decode shapes level).
+constexpr int kGemvDepth = 6;
 
 // LDS bytes of one workgroup: A as f16 [MR][kp], A's scale bytes [MR][kp / 32], the K ranges'
 // row sums [MR][64 / ks][ks] (= MR x 64 floats)
@@ -57,7 +60,7 @@ __host__ __device__ constexpr int gemv_kp(int k) { return (k + 127) / 128 * 128;
 inline int gemv_lds_bytes(int mr, int k, int /*ks*/) { return mr * gemv_kp(k) * 2 + mr * gemv_kp(k) / 32 + mr * 64 * 4; }
 
 template <int MR, int EPI>
-__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(const KParams p) {
+__global__ __launch_bounds__(kGemvWaves * 64, MR <= 2 ? 8 : 4) void gemv_kernel(const KParams p) {
     constexpr int DP = kGemvDepth;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
