@@ -1,6 +1,9 @@
 """Committed fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py):
 the CPU oracle must reproduce them bit-exactly; the GPU kernels must match them
-(bit-exact for the SF layout and grouped padding rows, calc_diff < 1e-5 for GEMM values)."""
+(bit-exact for the SF layout and grouped padding rows, calc_diff < 1e-5 for GEMM values).
+tests/golden/sr_bf16_reference.npz (written by tests/golden/make_sr_golden.py) holds stochastic-rounding
+outputs that the reference's own check (tests/utils.py:70-92 of the reference) accepted: the oracle's
+rounding must reproduce them bit for bit."""
 import json
 import os
 
@@ -8,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import gemm as og, layout as ol, quant
+from oracle import epilogue as oe, gemm as og, layout as ol, quant
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden')
 
@@ -163,3 +166,15 @@ def test_bf16_output_is_fp32_output_rounded(kind):
     fn(*args, d16)
     torch.cuda.synchronize()
     assert torch.equal(d16.cpu().view(torch.int16), d32.cpu().to(torch.bfloat16).view(torch.int16))
+
+
+def test_oracle_stochastic_rounding_matches_reference_vectors():
+    """Ragged rows (zero-padded quartets), NaN / inf / signed zero / subnormal / max-finite inputs and
+    random bit patterns: the oracle's bf16 bits equal those the reference's check accepted."""
+    z = np.load(os.path.join(GOLD, 'sr_bf16_reference.npz'), allow_pickle=False)
+    n = len(z.files) // 2
+    assert n >= 8
+    for i in range(n):
+        x = torch.from_numpy(z[f'x{i}'].view(np.float32).copy())
+        got = oe.stochastic_round_bf16(x).view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(got, z[f'y{i}']), i
