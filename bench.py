@@ -44,7 +44,7 @@ def parse():
                          '(cold-L2 kernel times) instead of the north-star line')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a 256 MiB device copy (reference kernel for FETCH_SIZE / WRITE_SIZE scaling)')
-    ap.add_argument('--profile-case', choices=('north', 'north_tn', 'grouped', 'decode'), default=None,
+    ap.add_argument('--profile-case', choices=('north', 'north_tn', 'grouped', 'decode', 'gemv'), default=None,
                     help='launch one workload 20 times and exit (the command rocprofv3 wraps for the profiles/ '
                          'summaries): north = fp8_gemm_nt 4096x7168x2048, north_tn = fp8_gemm_tn at that shape (MN-major '
                          'A and B), grouped = m_grouped contiguous G=32 '
@@ -370,8 +370,8 @@ def profile_case(case):
         b, sfb = _gpu_codes((k, n), dev, gen), _gpu_sf((k // 128, -(-n // 128)), dev, gen)
         d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
         fn = lambda: deep_gemm.fp8_gemm_tn((a, sfa), (b, sfb), d, recipe_a=(1, 128), recipe_b=(128, 128))
-    elif case in ('north', 'decode'):
-        m, n, k = (4096, 7168, 2048) if case == 'north' else (128, 2112, 7168)
+    elif case in ('north', 'decode', 'gemv'):
+        m, n, k = {'north': (4096, 7168, 2048), 'decode': (128, 2112, 7168), 'gemv': (1, 2112, 7168)}[case]
         a, sfa = _gpu_codes((m, k), dev, gen), _gpu_sf((m, k // 128), dev, gen)
         b, sfb = _gpu_codes((n, k), dev, gen), _gpu_sf((-(-n // 128), k // 128), dev, gen)
         sfa = deep_gemm.transform_sf_into_required_layout(sfa, m, k, (1, 128), is_sfa=True)
