@@ -593,14 +593,17 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     // ahead of the MFMA decode kernel (MI355X, kernel us, cold L2, two boxes: 1x2112x7168 7.3 vs
     // 9.0-9.3, 1x4096x7168 8.8-8.9 vs 10.4-10.5); level at 1x7168x16384 (24.2-24.4 vs 23.0-25.4),
     // behind at 1x7168x2048 (6.1 vs 5.8), 1x24576x1536 (11.1 vs 10.4) and for M = 2 (2x2112x7168
-    // 9.5 vs 8.8), where the VALU work per byte of B doubles.  DG_GEMV forces it for M <= 4 (with ks = 1, 2, 4 or 8; "0" turns it off).  Not
+    // 9.5 vs 8.8), where the VALU work per byte of B doubles.  DG_GEMV forces it for M <= 4 (with ks = 1, 2,
+    // 4 or 8, optionally ",4" for four-wave workgroups; "0" turns it off).  Not
     // under a CU cap (set_num_sms) or a forced plan (tuning overrides).
-    int gemv_mr = 0, gemv_ks = 0;
+    int gemv_mr = 0, gemv_ks = 0, gemv_waves = 0;
     {
-        const char* gemv_env = std::getenv("DG_GEMV");   // "0" = off, "1" / "2" / "4" / "8" = forced ks (tuning)
-        const int env_ks = gemv_env != nullptr && gemv_env[0] != '\0' ? std::atoi(gemv_env) : -1;
+        // DG_GEMV (tuning): "0" = off, "ks" or "ks,waves" = forced K split (1, 2, 4, 8) and workgroup size (4, 8)
+        const char* gemv_env = std::getenv("DG_GEMV");
+        int env_ks = -1, env_waves = 0;
+        if (gemv_env != nullptr && gemv_env[0] != '\0' && std::sscanf(gemv_env, "%d,%d", &env_ks, &env_waves) < 1)
+            env_ks = -1;
         const int mr = a.m <= 1 ? 1 : a.m <= 2 ? 2 : 4;
-        const int groups_g = a.gemm_type == kBatched ? a.num_groups : 1;
         const bool wanted = env_ks > 0 ? a.m <= 4 : env_ks == -1 && a.m == 1 && a.k >= 4096 && a.k <= 8192;
         if (wanted && a.kind == kFP8FP8 && (a.gemm_type == kNormal || a.gemm_type == kBatched) && a.m >= 1 &&
             a.k > 0 && !amn && !bmn && (epi_kind == kEpiF32 || epi_kind == kEpiBf16) && a.block_m <= 0 &&
@@ -610,11 +613,17 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
             if (env_ks == 1 || env_ks == 2 || env_ks == 4 || env_ks == 8) ks = env_ks;
             else
                 while (ks < 8 && pk >= 16 * ks) ks *= 2;
+            // eight-wave workgroups (two waves per SIMD); four-wave ones (half the rows each, twice the
+            // workgroups) measured slower even where eight-wave ones leave CUs idle (1x2112x7168,
+            // ks 4: 7.8 vs 7.2 us on 264 vs 132 CUs), so they are a tuning option only
+            int waves = env_waves == 4 || env_waves == 8 ? env_waves : 8;
+            if (ks > waves) waves = 8;
             if (gemv_lds(mr, a.k, ks) <= 64 * 1024 && 64LL * ldb_b < 0x40000000LL &&
                 (int64_t)ceil_div(a.k, 64) * a.sfb_ld * 2 + 2 * (int64_t)a.n < 0x7fffffffLL &&
-                lookup_gemv(mr, epi_kind) != nullptr) {
+                lookup_gemv(mr, epi_kind, waves) != nullptr) {
                 gemv_mr = mr;
                 gemv_ks = ks;
+                gemv_waves = waves;
             }
         }
     }
@@ -703,23 +712,23 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     int threads = skinny ? plan.skinny_nw * 64 : tile_threads(cfg.bm, cfg.bn);
     unsigned lds_bytes = 0;
     if (gemv_mr > 0) {
-        // workgroups of 64 / ks rows of B, dealt over the XCDs in contiguous runs
-        fn = lookup_gemv(gemv_mr, epi_kind);
+        // workgroups of 8 waves / ks rows of B, dealt over the XCDs in contiguous runs
+        fn = lookup_gemv(gemv_mr, epi_kind, gemv_waves);
         const int groups_g = a.gemm_type == kBatched ? a.num_groups : 1;
         p.split_k = 1;
         p.split_stages = gemv_ks;
-        p.num_n_blocks = ceil_div(a.n, 64 / gemv_ks);
+        p.num_n_blocks = ceil_div(a.n, 8 * gemv_waves / gemv_ks);
         const int64_t wgs = (int64_t)p.num_n_blocks * groups_g;
         if (wgs > 0x7ffffff0LL) return dg_set_error("dg_gemm: too many tiles");
         p.num_tiles = (int)wgs;
         tiles = wgs;
         grid = align_up64(wgs, 8);
-        threads = 8 * 64;
+        threads = gemv_waves * 64;
         lds_bytes = (unsigned)gemv_lds(gemv_mr, a.k, gemv_ks);
     }
     if (info != nullptr) {
         info->block_m = gemv_mr > 0 ? gemv_mr : cfg.bm;
-        info->block_n = gemv_mr > 0 ? 64 / gemv_ks : cfg.bn;
+        info->block_n = gemv_mr > 0 ? 8 * gemv_waves / gemv_ks : cfg.bn;
         info->grid = grid;
         info->threads = threads;
         info->tiles = tiles;

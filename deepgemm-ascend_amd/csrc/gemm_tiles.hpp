@@ -123,7 +123,7 @@ KernelFn lookup_skinny_rows(int kind, int mt, int nb, int d, int epi);
 
 // Decode GEMV kernels (csrc/gemv_kernel.hip): e4m3 x e4m3, M <= mr (1, 2, 4), fp32 / bf16 D;
 // whole rows of B per wave, A staged in LDS as f16 (gemv_lds(mr, k, rows per wave) bytes).
-KernelFn lookup_gemv(int mr, int epi);
+KernelFn lookup_gemv(int mr, int epi, int waves);   // waves per workgroup: 4 or 8
 int gemv_lds(int mr, int k, int rpw);
 
 KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi, bool persistent);

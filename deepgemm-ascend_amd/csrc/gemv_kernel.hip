@@ -11,7 +11,7 @@
 //   that measured fastest from HBM on this part (a wave streaming 1 KB of one row per
 //   instruction ran at 3.8 TB/s on 7168x16384 without any arithmetic).  A lane keeps its row for
 //   the whole kernel, so its accumulator belongs to one row;
-// * a workgroup of 8 waves owns 64 / ks rows: wave w takes row group w / ks and the (w % ks)-th of
+// * a workgroup of NWV = 8 or 4 waves owns 8 NWV / ks rows: wave w takes row group w / ks and the (w % ks)-th of
 //   ks contiguous K ranges of it, DP steps (1 KB each) in flight, straight into registers; the
 //   packed scale int16 of the lane's 64-K block comes with each step;
 // * A (M rows, at most ~60 KB as f16) is converted once per workgroup into LDS as f16 (e4m3 ->
@@ -48,25 +48,24 @@ __device__ __forceinline__ void fp8x16_to_f16(const i32x4 x, h2* h) {
     }
 }
 
-constexpr int kGemvWaves = 8;
 // Steps in flight per wave.  Six keep M <= 2 within 64 VGPRs (eight waves per SIMD, so that every
 // workgroup of a launch fits one round: 1x24576x1536 10.0 vs 11.0 us with eight steps at 73 VGPRs,
 // the other decode shapes level).
 constexpr int kGemvDepth = 6;
 
 // LDS bytes of one workgroup: A as f16 [MR][kp], A's scale bytes [MR][kp / 32], the K ranges'
-// row sums [MR][64 / ks][ks] (= MR x 64 floats)
+// row sums [MR][8 NWV / ks][ks] (at most MR x 64 floats)
 __host__ __device__ constexpr int gemv_kp(int k) { return (k + 127) / 128 * 128; }
 inline int gemv_lds_bytes(int mr, int k, int /*ks*/) { return mr * gemv_kp(k) * 2 + mr * gemv_kp(k) / 32 + mr * 64 * 4; }
 
-template <int MR, int EPI>
-__global__ __launch_bounds__(kGemvWaves * 64, MR <= 2 ? 8 : 4) void gemv_kernel(const KParams p) {
+template <int MR, int EPI, int NWV>
+__global__ __launch_bounds__(NWV * 64, MR <= 2 ? 8 : 4) void gemv_kernel(const KParams p) {
     constexpr int DP = kGemvDepth;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = p.k, kp = gemv_kp(K), N = p.n;
-    const int ks = p.split_stages, rows_wg = 64 / ks;
+    const int ks = p.split_stages, rows_wg = 8 * NWV / ks;
     _Float16* const a_lds = reinterpret_cast<_Float16*>(smem);              // [MR][kp]
     uint8_t* const sa_lds = smem + MR * kp * 2;                              // [MR][kp / 32]
     float* const part_lds = reinterpret_cast<float*>(sa_lds + MR * kp / 32);  // [MR][rows_wg][ks]
@@ -158,7 +157,7 @@ __global__ __launch_bounds__(kGemvWaves * 64, MR <= 2 ? 8 : 4) void gemv_kernel(
         sa_lds[m * (kp / 32) + 2 * kb] = (uint8_t)(s & 0xff);
         sa_lds[m * (kp / 32) + 2 * kb + 1] = (uint8_t)(s >> 8);
     };
-    constexpr int T = kGemvWaves * 64;
+    constexpr int T = NWV * 64;
     const bool a0_on = tid < MR * pieces, s0_on = tid < MR * kb64;
     const i32x4 x0 = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_a, a0_on ? a_offset(tid) : kOOBOffset, 0, 0));
     const uint32_t sx0 = __builtin_amdgcn_raw_buffer_load_b16(rs_sa, s0_on ? sa_offset(tid) : kOOBOffset, 0, 0);
@@ -245,13 +244,18 @@ __global__ __launch_bounds__(kGemvWaves * 64, MR <= 2 ? 8 : 4) void gemv_kernel(
     }
 }
 
-KernelFn lookup_gemv(int mr, int epi) {
-    if (epi != kEpiF32 && epi != kEpiBf16) return nullptr;
-    const bool f = epi == kEpiF32;
+template <int MR, int NWV>
+KernelFn gemv_epi(int epi) {
+    return epi == kEpiF32 ? &gemv_kernel<MR, kEpiF32, NWV> : epi == kEpiBf16 ? &gemv_kernel<MR, kEpiBf16, NWV> : nullptr;
+}
+
+KernelFn lookup_gemv(int mr, int epi, int waves) {
+    if (waves != 4 && waves != 8) return nullptr;
+    const bool w8 = waves == 8;
     switch (mr) {
-        case 1: return f ? &gemv_kernel<1, kEpiF32> : &gemv_kernel<1, kEpiBf16>;
-        case 2: return f ? &gemv_kernel<2, kEpiF32> : &gemv_kernel<2, kEpiBf16>;
-        case 4: return f ? &gemv_kernel<4, kEpiF32> : &gemv_kernel<4, kEpiBf16>;
+        case 1: return w8 ? gemv_epi<1, 8>(epi) : gemv_epi<1, 4>(epi);
+        case 2: return w8 ? gemv_epi<2, 8>(epi) : gemv_epi<2, 4>(epi);
+        case 4: return w8 ? gemv_epi<4, 8>(epi) : gemv_epi<4, 4>(epi);
         default: return nullptr;
     }
 }

@@ -34,11 +34,12 @@ def test_gemv_plan_and_parity_baseline_shapes(monkeypatch, m, n, k, ks):
     assert calc_diff(d.cpu(), og.gemm_nt(a_deq, b_deq, torch.bfloat16)) < THRESH
 
 
-@pytest.mark.parametrize('ks', ['', '1', '2', '8'])
+@pytest.mark.parametrize('ks', ['', '1', '2', '8', '2,4', '4,4'])
 @pytest.mark.parametrize('n,k', [(500, 1040), (130, 64), (77, 3000), (1000, 9216)])
 def test_gemv_ragged_codes(monkeypatch, ks, n, k):
     """Random e4m3 codes with per-32 power-of-two scales; every M the kernel serves; the K split
-    between a workgroup's waves forced to 1, 2 and 8 (DG_GEMV) or the heuristic's."""
+    between a workgroup's waves forced to 1, 2 and 8 (DG_GEMV; "2,4" and "4,4" with four-wave workgroups) or
+    the heuristic's."""
     if ks:
         monkeypatch.setenv('DG_GEMV', ks)
     else:
