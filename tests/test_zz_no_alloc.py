@@ -71,6 +71,22 @@ def test_noalloc_matches_dg_gemm_on_two_calls():
         assert torch.equal(_run(lib, args, True), d_ws)
 
 
+def test_noalloc_gemv_plan():
+    """A decode GEMM that plans the GEMV kernel (no scratch at all): dg_gemm_noalloc matches dg_gemm bit for
+    bit on two calls in a row (the second with fewer rows of B) and the oracle."""
+    lib = _lib.load()
+    for (m, n, k), seed in (((1, 2112, 7168), 6), ((1, 1000, 4096), 7)):
+        args, keep, ref = _args(m, n, k, seed)
+        info = _lib.LaunchInfo()
+        _lib.check(lib.dg_launch_plan(ctypes.byref(args), ctypes.byref(info)), lib)
+        print(f'noalloc gemv m={m} n={n} k={k} skinny={info.skinny} split_k={info.split_k}', flush=True)
+        assert info.skinny == 3 and info.split_k == 1
+        d_noalloc = _run(lib, args, True)
+        d_ws = _run(lib, args, False)
+        assert torch.equal(d_noalloc.view(torch.int16), d_ws.view(torch.int16))
+        assert calc_diff(d_noalloc, ref) < 1e-5
+
+
 def test_noalloc_rejects_oversize_and_a_workspace():
     lib = _lib.load()
     args, keep, _ = _args(128, 8192, 16384, 3)
