@@ -63,6 +63,64 @@ def calibrate_copy():
     print(json.dumps({'calibration': 'device copy', 'bytes_read_per_launch': n, 'bytes_written_per_launch': n}))
 
 
+PEAK_CLOCK_MHZ = 2400.0      # engine clock the published peaks are quoted at
+
+
+def sustained_clock(step, seconds=0.6):
+    """Shader clock and socket power while `step` runs back to back for `seconds` (the clock the
+    chip holds under this load: MI355X is power-limited, so the published peak at 2.4 GHz is not
+    reachable).  Sampled from the SMU metrics table through amdsmi every ~5 ms; the table refreshes
+    more slowly, so distinct samples are a few per window.  None if amdsmi is unavailable."""
+    import threading
+    import torch
+    try:
+        import amdsmi
+        amdsmi.amdsmi_init()
+        h = amdsmi.amdsmi_get_processor_handles()[0]
+        amdsmi.amdsmi_get_gpu_metrics_info(h)
+    except Exception as e:   # noqa: BLE001 (no SMU access: report why)
+        return {'error': f'amdsmi unavailable: {e!r}'[:200]}
+    samples, stop = [], [False]
+
+    def sampler():
+        while not stop[0]:
+            try:
+                m = amdsmi.amdsmi_get_gpu_metrics_info(h)
+                clks = [c for c in m.get('current_gfxclks', []) if isinstance(c, int)]
+                if m.get('average_gfx_activity', 0) not in (0, 'N/A') and clks:
+                    samples.append((sum(clks) / len(clks), m.get('current_socket_power')))
+            except Exception:   # noqa: BLE001
+                pass
+            time.sleep(0.005)
+
+    for _ in range(50):
+        step()
+    torch.cuda.synchronize()
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    t_end = time.perf_counter() + seconds
+    n = 0
+    while time.perf_counter() < t_end:
+        for _ in range(100):
+            step()
+        n += 100
+        torch.cuda.synchronize()
+    stop[0] = True
+    th.join()
+    try:
+        amdsmi.amdsmi_shut_down()
+    except Exception:   # noqa: BLE001
+        pass
+    if not samples:
+        return {'error': 'no samples with the GPU active'}
+    clk = sorted(c for c, _ in samples)
+    pw = sorted(p for _, p in samples if isinstance(p, (int, float)))
+    return {'clock_mhz_median': round(clk[len(clk) // 2], 1), 'clock_mhz_min': round(clk[0], 1),
+            'clock_mhz_max': round(clk[-1], 1), 'socket_power_w_median': pw[len(pw) // 2] if pw else None,
+            'samples': len(samples), 'launches': n,
+            'source': 'amdsmi gpu_metrics current_gfxclks (mean over XCDs), sampled while the step ran back to back'}
+
+
 def make_inputs(m, n, k):
     import torch
     from oracle import quant
@@ -468,6 +526,8 @@ def main():
     # reference times its kernels): the roofline's achieved rate
     cold_us = _time_cold(step, iters=max(10, min(args.steps, 40)))
 
+    clock = sustained_clock(step)
+
     flops = 2.0 * m * n * k
     tflops = flops / (ms_per_step * 1e-3) / 1e12
     achieved = flops / (cold_us * 1e-6) / 1e12
@@ -489,6 +549,11 @@ def main():
                      'frac': round(achieved / PEAK_FP8_TFLOPS, 4), 'traffic': traffic,
                      'kernel_us_cold_median': round(cold_us, 3),
                      'kernel_avg_us_warm': round(kern_avg * 1e3, 3), 'kernel_min_us_warm': round(kern_ms[0] * 1e3, 3),
+                     'clock': clock,
+                     'peak_at_clock': (round(PEAK_FP8_TFLOPS * clock['clock_mhz_median'] / PEAK_CLOCK_MHZ, 1)
+                                       if 'clock_mhz_median' in clock else None),
+                     'frac_at_clock': (round(achieved / (PEAK_FP8_TFLOPS * clock['clock_mhz_median'] / PEAK_CLOCK_MHZ), 4)
+                                       if 'clock_mhz_median' in clock else None),
                      'timing': 'achieved = 2MNK / cold-L2 kernel time (HIP events around each launch on its stream, '
                                '1 GiB read evicts L2 and the MALL before each); value = back-to-back warm steps'},
         'calc_diff': diff,

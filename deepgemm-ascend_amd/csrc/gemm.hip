@@ -159,6 +159,26 @@ bool skinny_plan(const dg_gemm_args& a, int cus, bool allow_split, Plan& out) {
     return true;
 }
 
+// DG_GEMV (tuning override), parsed only when its text changes since the last call: "0" = off,
+// "ks" or "ks,waves" = forced K split and workgroup size of the GEMV decode kernel; ks = -1 when
+// unset.
+void gemv_env(int& ks, int& waves) {
+    static std::mutex mu;
+    static std::string last;
+    static int last_ks = -1, last_waves = 0;
+    const char* s = std::getenv("DG_GEMV");
+    const char* cur = s == nullptr ? "" : s;
+    std::lock_guard<std::mutex> lk(mu);
+    if (last != cur) {
+        last = cur;
+        last_ks = -1;
+        last_waves = 0;
+        if (cur[0] != '\0' && std::sscanf(cur, "%d,%d", &last_ks, &last_waves) < 1) last_ks = -1;
+    }
+    ks = last_ks;
+    waves = last_waves;
+}
+
 // DG_SKINNY (tuning override): "0" = never use the skinny-M kernel, "mt,nb,nw,d,ar[,split]" =
 // use that configuration wherever M fits it.
 struct SkinnyEnv {
@@ -599,10 +619,8 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     int gemv_mr = 0, gemv_ks = 0, gemv_waves = 0;
     {
         // DG_GEMV (tuning): "0" = off, "ks" or "ks,waves" = forced K split (1, 2, 4, 8) and workgroup size (4, 8)
-        const char* gemv_env = std::getenv("DG_GEMV");
         int env_ks = -1, env_waves = 0;
-        if (gemv_env != nullptr && gemv_env[0] != '\0' && std::sscanf(gemv_env, "%d,%d", &env_ks, &env_waves) < 1)
-            env_ks = -1;
+        gemv_env(env_ks, env_waves);
         const int mr = a.m <= 1 ? 1 : a.m <= 2 ? 2 : 4;
         const bool wanted = env_ks > 0 ? a.m <= 4 : env_ks == -1 && a.m == 1 && a.k >= 4096 && a.k <= 8192;
         if (wanted && a.kind == kFP8FP8 && (a.gemm_type == kNormal || a.gemm_type == kBatched) && a.m >= 1 &&
@@ -745,13 +763,15 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         int rc = check_m_indices(a.grouped_layout, a.m, a.alignment, a.num_groups, st, !noalloc);
         if (rc != DG_OK) return rc;
         if (p.anchored) {
-            // the layout's run table: in the caller's scratch for dg_gemm_noalloc (it splits no K),
-            // else in the library's per-stream buffer
+            // the layout's run table: for dg_gemm_noalloc in its scratch past the split-K tile
+            // counters (those must stay zero for the next split-K call; an anchored plan splits no
+            // K, so the partial-tile area is free), else in the library's per-stream buffer
             const int64_t need = (1 + 2 * (int64_t)ceil_div(a.m, p.alignment)) * 4;
             void* runs = nullptr;
             if (noalloc) {
-                if (need > a.workspace_bytes) return dg_set_error("dg_gemm_noalloc: m_indices run table exceeds the scratch");
-                runs = a.workspace;
+                if (kCounterBytes + need > a.workspace_bytes)
+                    return dg_set_error("dg_gemm_noalloc: m_indices run table exceeds the scratch");
+                runs = reinterpret_cast<uint8_t*>(a.workspace) + kCounterBytes;
             } else {
                 rc = stream_workspace(st, need, &runs, 1);
                 if (rc != DG_OK) return rc;

@@ -38,6 +38,7 @@ from .gemm import (  # noqa: E402
 )
 from .einsum import fp8_bmm, bf16_bmm, einsum, fp8_einsum  # noqa: E402
 from . import epilogue  # noqa: E402
+from ._lib import check_errors  # noqa: E402
 
 # FP8 aliases are the same objects as the FP8/FP4 entry points (csrc/apis/gemm.hpp:624-629)
 fp8_gemm_nt = fp8_fp4_gemm_nt

@@ -136,7 +136,7 @@ def load(path=None) -> ctypes.CDLL:
         return lib
 
 
-def error_message(bits: int) -> str:
+def error_message(bits: int, where: str = 'an earlier deep_gemm call') -> str:
     """Text of the sticky error bits (the C++ host path words it the same way, csrc/torch_ext.cpp)."""
     parts = []
     if bits & DG_ERR_SF_INVALID:
@@ -144,7 +144,7 @@ def error_message(bits: int) -> str:
     if bits & DG_ERR_M_INDICES:
         parts.append('m_indices is not padded to the M-grouped alignment (every alignment-row block must hold one '
                      'group id < num_groups followed only by -1 padding)')
-    return '; '.join(parts) + ' [reported by a kernel of an earlier deep_gemm call]'
+    return '; '.join(parts) + f' [reported by a kernel of {where}]'
 
 
 def raise_pending() -> None:
@@ -155,6 +155,21 @@ def raise_pending() -> None:
     bits = _lib.dg_take_errors()
     if bits:
         raise RuntimeError(error_message(bits))
+
+
+def check_errors(synchronize: bool = True) -> None:
+    """Raise the errors that kernels of deep_gemm calls have reported (invalid float32 scale
+    factors, unpadded m_indices), at a point the caller chooses.  With `synchronize` the current
+    device is synchronised first, so every call issued before this one is covered and the error
+    is raised for it, not by a later call; the words are cleared either way."""
+    lib = load()
+    if synchronize:
+        import torch
+        if torch.cuda.is_available():
+            torch.cuda.synchronize()
+    bits = lib.dg_take_errors()
+    if bits:
+        raise RuntimeError(error_message(bits, 'a deep_gemm call issued before check_errors()'))
 
 
 _EXT_NAME = 'deep_gemm_C'

@@ -239,7 +239,8 @@ int dg_gemm_noalloc(const dg_gemm_args *args, void *stream);
  *                      `alignment`: some alignment-row block mixed two group ids, had a group id
  *                      after a padding row, or held an id >= num_groups.
  * dg_take_errors returns the DG_ERR_* bits set by kernels that completed since the last call and
- * clears them.  dg_error_words returns the host address of the words (word i != 0: bit i). */
+ * clears them; after a hipStreamSynchronize (or event wait) it covers every call issued before
+ * it, which is how a caller checks a given call at a sync point of its choosing.  dg_error_words returns the host address of the words (word i != 0: bit i). */
 #define DG_ERR_SF_INVALID 1u
 #define DG_ERR_M_INDICES 2u
 /* The split-K workspace the library holds for (current device, stream) -- see library_workspace in

@@ -65,7 +65,7 @@ def test_config2_bias(m, n, k):
 
 @pytest.mark.parametrize('layout', ['nt', 'nn'])
 @pytest.mark.parametrize('n,k', NK)
-@pytest.mark.parametrize('m', [128, 4096])
+@pytest.mark.parametrize('m', [1, 64, 128, 4096])
 def test_config3_bf16_gemm(m, n, k, layout):
     print(f'config3 bf16_gemm_{layout} m={m} n={n} k={k}', flush=True)
     g = gen(300 + m)

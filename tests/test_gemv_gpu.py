@@ -83,6 +83,35 @@ def test_gemv_accumulate_bias(monkeypatch, m):
     assert calc_diff(d16.cpu(), ref + bias.float()) < THRESH
 
 
+def test_gemv_default_plan_bias_and_accumulate(monkeypatch):
+    """The default GEMV plan (M = 1, 4096 <= K <= 8192, no DG_GEMV): fp32 D accumulate (c is d),
+    bf16 D accumulate (the kernel reads the bf16 D back, adds, rounds once), and a bf16 bias row."""
+    monkeypatch.delenv('DG_GEMV', raising=False)
+    m, n, k = 1, 2112, 7168
+    assert deep_gemm.launch_plan(m, n, k)['skinny'] == 3
+    g = gen(45)
+    a, sfa, a_deq = operand(m, k, 'e4m3', (1, 128), g, mode='randn')
+    b, sfb, b_deq = operand(n, k, 'e4m3', (128, 128), g, mode='randn')
+    args = ((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()))
+    rec = dict(recipe_a=(1, 128), recipe_b=(128, 128))
+    ref = og.gemm_nt(a_deq, b_deq, torch.float32)
+    c = torch.randn(m, n, generator=g) * 4
+    d = c.clone().cuda()
+    deep_gemm.fp8_gemm_nt(*args, d, c=d, **rec)
+    torch.cuda.synchronize()
+    assert calc_diff(d.cpu(), ref + c) < THRESH
+    c16 = c.bfloat16()
+    d16 = c16.clone().cuda()
+    deep_gemm.fp8_gemm_nt(*args, d16, c=d16, **rec)
+    torch.cuda.synchronize()
+    assert calc_diff(d16.cpu().float(), (ref + c16.float()).bfloat16().float()) < THRESH
+    bias = torch.randn(1, n, generator=g).bfloat16()
+    d16b = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
+    deep_gemm.fp8_gemm_nt(*args, d16b, c=bias.cuda(), **rec)
+    torch.cuda.synchronize()
+    assert calc_diff(d16b.cpu().float(), ref + bias.float()) < THRESH
+
+
 def test_gemv_bmm(monkeypatch):
     monkeypatch.setenv('DG_GEMV', '2')
     bs, m, n, k = 5, 2, 300, 2000

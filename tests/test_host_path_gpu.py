@@ -58,7 +58,49 @@ def test_invalid_fp32_sf_is_reported_by_the_next_call():
         deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d, **R)
     # reported once: the next valid call runs
     deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d, **R)
-    torch.cuda.synchronize()
+
+
+def test_check_errors_raises_for_the_offending_call():
+    """deep_gemm.check_errors() synchronises and raises for the call that set the word (here the
+    last call of a sequence, which no later deep_gemm call would report), and clears it."""
+    _clear_pending()
+    (a, sfa), (b, sfb), ref = _dense(64, 256, 512, seed=3)
+    d = torch.empty(64, 256, dtype=torch.bfloat16, device='cuda')
+    deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d, **R)
+    deep_gemm.check_errors()                              # nothing reported for a valid call
+    assert calc_diff(d.cpu(), ref) < THRESH
+    bad = sfa.clone()
+    bad[5, 2] = -1.0                                      # sign bit: not a UE8M0 value
+    deep_gemm.fp8_gemm_nt((a, bad), (b, sfb), d, **R)     # no synchronisation, no error yet
+    with pytest.raises(RuntimeError, match='Invalid float32 SF.*before check_errors'):
+        deep_gemm.check_errors()
+    deep_gemm.check_errors()                              # cleared
+    deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d, **R)     # and the next call does not re-report it
+    deep_gemm.check_errors()
+
+
+def test_check_errors_unpadded_m_indices():
+    """An m_indices layout with a row of another group inside a block is reported by
+    check_errors() right after the offending call (the last call: no later call would report it)."""
+    _clear_pending()
+    alignment, g_num, n, k = 128, 3, 256, 256
+    total, ps = ol.psum_from_sizes([130, 60, 128], alignment)
+    idx = ol.m_indices_from_psum(ps, alignment, total).clone()
+    idx[200] = 2
+    g = gen(5)
+    a, sfa, _ = operand(total, k, 'e4m3', (1, 32), g)
+    b, sfb, _ = operand(n, k, 'e4m3', (1, 32), g, batch=g_num)
+    d = torch.empty(total, n, dtype=torch.bfloat16, device='cuda')
+    old = deep_gemm.get_mk_alignment_for_contiguous_layout()
+    deep_gemm.set_mk_alignment_for_contiguous_layout(alignment)
+    try:
+        deep_gemm.m_grouped_fp8_gemm_nt_contiguous((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d, idx.cuda(),
+                                                   use_psum_layout=False)
+        with pytest.raises(RuntimeError, match='m_indices is not padded'):
+            deep_gemm.check_errors()
+        deep_gemm.check_errors()
+    finally:
+        deep_gemm.set_mk_alignment_for_contiguous_layout(old)
 
 
 @pytest.mark.parametrize('case', ['mixed_block', 'group_after_padding', 'id_out_of_range'])

@@ -103,12 +103,17 @@ def test_noalloc_rejects_oversize_and_a_workspace():
 
 
 def test_noalloc_m_indices_run_table_in_scratch():
+    _check_m_indices_noalloc()
+
+
+def _check_m_indices_noalloc():
     """M-grouped m_indices GEMMs below alignment 256 take the anchored tiles, whose run table
     dg_gemm_noalloc keeps in its scratch array: bit-identical to dg_gemm (which keeps it in the
     library's per-stream buffer), on two calls in a row, the second with fewer rows."""
     from oracle import layout as ol
     lib = _lib.load()
     alignment, g_num, n, k = 128, 4, 320, 512
+    keep_alive = []
     for sizes, seed in (([257, 0, 130, 400], 3), ([5, 128], 4)):
         total, ps = ol.psum_from_sizes(sizes, alignment)
         idx = ol.m_indices_from_psum(ps, alignment, total).cuda()
@@ -127,6 +132,7 @@ def test_noalloc_m_indices_run_table_in_scratch():
         args.sfa_ld, args.sfb_ld = sfa_t.stride(-1), sfb_t.stride(-1)
         args.grouped_layout = idx.data_ptr()
         args.d_dtype, args.alpha, args.alignment = _lib.DG_DTYPE_BF16, 1.0, alignment
+        keep_alive.append((a, b, sfa_t, sfb_t, idx))
         info = _lib.LaunchInfo()
         _lib.check(lib.dg_launch_plan(ctypes.byref(args), ctypes.byref(info)), lib)
         print(f'noalloc m_indices sizes={sizes} block={info.block_m}x{info.block_n}', flush=True)
@@ -138,3 +144,23 @@ def test_noalloc_m_indices_run_table_in_scratch():
         ref = og.m_grouped_contiguous(a_deq, b_deq, idx.cpu(), False, alignment)
         assert calc_diff(d_noalloc[valid], ref[valid]) < 1e-5
         assert torch.equal(d_noalloc[~valid], torch.zeros_like(d_noalloc[~valid]))
+    return keep_alive
+
+
+def test_noalloc_split_k_after_m_indices():
+    """The run table of an m_indices call must not land on the split-K tile counters (which every
+    split-K call needs at zero): an anchored m_indices dg_gemm_noalloc call, then the 128x2112x7168
+    split-K plan twice, each bit-identical to dg_gemm with its own zeroed workspace."""
+    keep = _check_m_indices_noalloc()
+    lib = _lib.load()
+    args, keep2, ref = _args(128, 2112, 7168, 5)
+    info = _lib.LaunchInfo()
+    args.workspace, args.workspace_bytes = 1, 1 << 40
+    _lib.check(lib.dg_launch_plan(ctypes.byref(args), ctypes.byref(info)), lib)
+    args.workspace, args.workspace_bytes = None, 0
+    print(f'noalloc split-K after m_indices: split_k={info.split_k}', flush=True)
+    assert info.split_k > 1
+    d_ws = _run(lib, args, False)
+    for _ in range(2):
+        assert torch.equal(_run(lib, args, True), d_ws)
+    assert calc_diff(d_ws, ref) < 1e-5
