@@ -44,11 +44,13 @@ def parse():
                          '(cold-L2 kernel times) instead of the north-star line')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a 256 MiB device copy (reference kernel for FETCH_SIZE / WRITE_SIZE scaling)')
-    ap.add_argument('--profile-case', choices=('north', 'north_tn', 'grouped', 'decode', 'gemv'), default=None,
+    ap.add_argument('--profile-case', choices=('north', 'north_tn', 'grouped', 'decode', 'gemv', 'fp4_north', 'fp4_4096'),
+                    default=None,
                     help='launch one workload 20 times and exit (the command rocprofv3 wraps for the profiles/ '
                          'summaries): north = fp8_gemm_nt 4096x7168x2048, north_tn = fp8_gemm_tn at that shape (MN-major '
                          'A and B), grouped = m_grouped contiguous G=32 '
-                         'N=4096 K=7168, decode = fp8_gemm_nt 128x2112x7168')
+                         'N=4096 K=7168, decode = fp8_gemm_nt 128x2112x7168, fp4_north / fp4_4096 = fp8_fp4_gemm_nt '
+                         '4096x7168x2048 / 4096x4096x7168 (e2m1 B, 1x32 scales)')
     return ap.parse_args()
 
 
@@ -428,6 +430,16 @@ def profile_case(case):
         b, sfb = _gpu_codes((k, n), dev, gen), _gpu_sf((k // 128, -(-n // 128)), dev, gen)
         d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
         fn = lambda: deep_gemm.fp8_gemm_tn((a, sfa), (b, sfb), d, recipe_a=(1, 128), recipe_b=(128, 128))
+    elif case in ('fp4_north', 'fp4_4096'):
+        # e4m3 A (1x128 scales) x e2m1 B packed two per byte (1x32 scales)
+        m, n, k = (4096, 7168, 2048) if case == 'fp4_north' else (4096, 4096, 7168)
+        a, sfa = _gpu_codes((m, k), dev, gen), _gpu_sf((m, k // 128), dev, gen)
+        b = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev, generator=gen).view(torch.int8)
+        sfb = _gpu_sf((n, k // 32), dev, gen)
+        sfa = deep_gemm.transform_sf_into_required_layout(sfa, m, k, (1, 128), is_sfa=True)
+        sfb = deep_gemm.transform_sf_into_required_layout(sfb, n, k, (1, 32), is_sfa=False)
+        d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        fn = lambda: deep_gemm.fp8_fp4_gemm_nt((a, sfa), (b, sfb), d)
     elif case in ('north', 'decode', 'gemv'):
         m, n, k = {'north': (4096, 7168, 2048), 'decode': (128, 2112, 7168), 'gemv': (1, 2112, 7168)}[case]
         a, sfa = _gpu_codes((m, k), dev, gen), _gpu_sf((m, k // 128), dev, gen)

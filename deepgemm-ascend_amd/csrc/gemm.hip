@@ -299,13 +299,9 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     const double hbm_bytes = esz * ((double)a.m + a.n) * a.k * groups + 2.0 * a.m * a.n * groups;
     double best = 1e300;
     Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0, 0}, 1, 1, 0, 0, 0};
-    // Under a CU cap the 128-K-stage tiles run persistently (one workgroup per allowed CU), so only
-    // those with a persistent kernel are offered.
-    const bool capped = cus_capped(cus);
     for (int i = 0; i < kNumTiles; ++i) {
         const TileCfg& tc = kTiles[i];
         if (!tile_allowed(a, tc.bm, tc.bn)) continue;
-        if (capped && tc.km == 2 && !tile_persistable(tc)) continue;
         const int ns = ceil_div(k_tile, k_stage_elems(a.kind, tc));
         const int64_t tiles = plan_tiles(a, tc);
         const int max_split = allow_split && tile_splittable(tc) && tiles <= kMaxSplitTiles ? std::min(16, std::max(1, ns / 4)) : 1;
@@ -615,7 +611,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     // behind at 1x7168x2048 (6.1 vs 5.8), 1x24576x1536 (11.1 vs 10.4) and for M = 2 (2x2112x7168
     // 9.5 vs 8.8), where the VALU work per byte of B doubles.  DG_GEMV forces it for M <= 4 (with ks = 1, 2,
     // 4 or 8, optionally ",4" for four-wave workgroups; "0" turns it off).  Not
-    // under a CU cap (set_num_sms) or a forced plan (tuning overrides).
+    // under a forced plan (tuning overrides).
     int gemv_mr = 0, gemv_ks = 0, gemv_waves = 0;
     {
         // DG_GEMV (tuning): "0" = off, "ks" or "ks,waves" = forced K split (1, 2, 4, 8) and workgroup size (4, 8)
@@ -625,7 +621,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         const bool wanted = env_ks > 0 ? a.m <= 4 : env_ks == -1 && a.m == 1 && a.k >= 4096 && a.k <= 8192;
         if (wanted && a.kind == kFP8FP8 && (a.gemm_type == kNormal || a.gemm_type == kBatched) && a.m >= 1 &&
             a.k > 0 && !amn && !bmn && (epi_kind == kEpiF32 || epi_kind == kEpiBf16) && a.block_m <= 0 &&
-            a.split_k <= 1 && !cus_capped(cus) && skinny_env().mode == -1) {
+            a.split_k <= 1 && skinny_env().mode == -1) {
             const int pk = ceil_div(a.k, 128);
             int ks = 1;
             if (env_ks == 1 || env_ks == 2 || env_ks == 4 || env_ks == 8) ks = env_ks;
@@ -744,10 +740,21 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         threads = gemv_waves * 64;
         lds_bytes = (unsigned)gemv_lds(gemv_mr, a.k, gemv_ks);
     }
+    // Under a CU cap (set_num_sms below the device's CUs) at most `cus` workgroups run at a time:
+    // one per allowed CU (the reference launches num_cores blocks, csrc/jit_kernels/heuristics.hpp:98).
+    // The persistent kernel walks its tiles with that many; the other kernels get the plan's
+    // workgroups in stream-ordered launches of at most `cus` each (KParams::vbase; rounded down to
+    // whole groups of 8, one per XCD, so the XCD-aware workgroup orders keep their placement), which
+    // leaves the kernels' code as it is for uncapped launches.
+    p.vgrid = (int)grid;
+    p.vbase = 0;
+    int64_t launched = grid;
+    if (cus_capped(cus) && !persistent) launched = std::min<int64_t>(grid, cus >= 8 ? cus / 8 * 8 : cus);
     if (info != nullptr) {
+        info->plan_workgroups = grid;
         info->block_m = gemv_mr > 0 ? gemv_mr : cfg.bm;
         info->block_n = gemv_mr > 0 ? 8 * gemv_waves / gemv_ks : cfg.bn;
-        info->grid = grid;
+        info->grid = launched;
         info->threads = threads;
         info->tiles = tiles;
         info->split_k = gemv_mr > 0 ? 1 : plan.split;
@@ -781,11 +788,16 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
             if (rc != DG_OK) return rc;
         }
     }
-    if (jit) return jit_run(a, cfg, epi_kind, plan.split, p, grid, st, compile_only);
-    const hipError_t e = launch_module_kernel(reinterpret_cast<const void*>(fn), (unsigned)grid, (unsigned)threads, p, st, lds_bytes);
-    if (e != hipSuccess) {
-        dg_set_error(hipGetErrorString(e));
-        return DG_ELAUNCH;
+    if (jit) return jit_run(a, cfg, epi_kind, plan.split, p, launched, st, compile_only);
+    for (int64_t base = 0; base < grid; base += launched) {
+        p.vbase = (int)base;
+        const unsigned n = (unsigned)std::min<int64_t>(launched, grid - base);
+        const hipError_t e = launch_module_kernel(reinterpret_cast<const void*>(fn), n, (unsigned)threads, p, st, lds_bytes);
+        if (e != hipSuccess) {
+            dg_set_error(hipGetErrorString(e));
+            return DG_ELAUNCH;
+        }
+        if (persistent) break;   // (one launch walks every tile)
     }
     return DG_OK;
 }

@@ -69,6 +69,10 @@ struct KParams {
     // Persistent launches: bytes of each operand / SF tensor over all its batches or groups (every
     // span below 2^31, so a tile's base fits a buffer instruction's scalar offset).
     int64_t a_span, b_span, sfa_span, sfb_span;
+    // Workgroups of the launch plan (vgrid) and the first one this launch serves (vbase): under a
+    // CU cap (set_num_sms) the plan's workgroups go out in launches of at most that many, and
+    // workgroup b of a launch serves plan workgroup vbase + b.
+    int vgrid, vbase;
 };
 
 // Epilogue variants.
@@ -503,7 +507,7 @@ __device__ __forceinline__ void epilogue_block(const KParams& p, const f32x16& a
 // arguments, the JIT compiles one body per problem (csrc/jit.hip).
 template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI, int CT = -1,
           int CS = 0, int CM = 0, int CN = 0, int CK = 0, bool AMN = false, bool BMN = false, int NSB_ = 0>
-__device__ __forceinline__ void gemm_body(const KParams& p) {
+__device__ __forceinline__ void gemm_body(const KParams& p, const int vb) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
     constexpr bool kBf16 = KIND == kBF16;
@@ -603,7 +607,7 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         // Split-K launch: grid = 8 * ceil(tiles / 8) * split_k, and workgroup b serves tile
         // (b / 8 / split_k) * 8 + b % 8, split (b / 8) % split_k, so all splits of a tile share
         // b % 8 -- the XCD (and L2) the dispatcher places them on.
-        const int b = blockIdx.x, r = b >> 3;
+        const int b = vb, r = b >> 3;
         t = (r / split_k) * 8 + (b & 7);
         split = r % split_k;
         if (p.split_spread) {
@@ -613,7 +617,7 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         }
         if (t >= p.num_tiles) return;
     } else {
-        t = xcd_remap(blockIdx.x, gridDim.x);
+        t = xcd_remap(vb, p.vgrid);
     }
     const int tile_id = t;
     int batch = 0;
@@ -629,8 +633,8 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
         // the launch's real tiles spread over the XCDs as xcd_remap spreads a full grid
         const int total =
             __builtin_amdgcn_readfirstlane(anchored_total(p.layout, p.num_groups, runs, p.alignment, BM, M, nn));
-        if ((int)blockIdx.x >= total) return;
-        t = xcd_remap(blockIdx.x, total);
+        if (vb >= total) return;
+        t = xcd_remap(vb, total);
         anchored_tile(p.layout, p.num_groups, runs, p.alignment, t, BM, M, nn, anchor_group, m0, nb, tile_end,
                       anchor_valid);
         anchor_group = __builtin_amdgcn_readfirstlane(anchor_group);
@@ -1244,7 +1248,7 @@ __device__ __forceinline__ void gemm_body(const KParams& p) {
 template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI, bool AMN = false,
           bool BMN = false, int NSB = 0>
 __global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_kernel(const KParams p) {
-    gemm_body<BM, BN, WGM, NW, LW, NSTAGE, KM, OCC, KIND, EPI, -1, 0, 0, 0, 0, AMN, BMN, NSB>(p);
+    gemm_body<BM, BN, WGM, NW, LW, NSTAGE, KM, OCC, KIND, EPI, -1, 0, 0, 0, 0, AMN, BMN, NSB>(p, blockIdx.x + p.vbase);
 }
 
 }  // namespace dg

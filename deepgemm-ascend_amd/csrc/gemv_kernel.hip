@@ -59,7 +59,7 @@ __host__ __device__ constexpr int gemv_kp(int k) { return (k + 127) / 128 * 128;
 inline int gemv_lds_bytes(int mr, int k, int /*ks*/) { return mr * gemv_kp(k) * 2 + mr * gemv_kp(k) / 32 + mr * 64 * 4; }
 
 template <int MR, int EPI, int NWV>
-__global__ __launch_bounds__(NWV * 64, MR <= 2 ? 8 : 4) void gemv_kernel(const KParams p) {
+__device__ __forceinline__ void gemv_body(const KParams& p, const int vb) {
     constexpr int DP = kGemvDepth;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(NWV * 64, MR <= 2 ? 8 : 4) void gemv_kernel(const K
 
     // workgroup of this block: contiguous runs of workgroups per XCD (block b runs on XCD b % 8)
     const int wgs = p.num_tiles, per_xcd = ceil_div(wgs, 8);
-    const int c = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+    const int c = (vb % 8) * per_xcd + vb / 8;
     if (c >= wgs) return;
     const int batch = c / p.num_n_blocks;
     const int n0 = (c - batch * p.num_n_blocks) * rows_wg;
@@ -242,6 +242,11 @@ __global__ __launch_bounds__(NWV * 64, MR <= 2 ? 8 : 4) void gemv_kernel(const K
         if (p.accumulate) v += to_f(*dp);
         if constexpr (kF32) *dp = v; else *dp = f32_to_bf16_rne(v);
     }
+}
+
+template <int MR, int EPI, int NWV>
+__global__ __launch_bounds__(NWV * 64, MR <= 2 ? 8 : 4) void gemv_kernel(const KParams p) {
+    gemv_body<MR, EPI, NWV>(p, blockIdx.x + p.vbase);
 }
 
 template <int MR, int NWV>

@@ -121,11 +121,11 @@ struct Spec {
 };
 
 std::string source_of(const Spec& s) {
-    char buf[640];
+    char buf[768];
     snprintf(buf, sizeof(buf),
              "#include \"gemm_kernel.hpp\"\n"
              "extern \"C\" __global__ __launch_bounds__(%d, %d) void dg_jit_kernel(const dg::KParams p) {\n"
-             "    dg::gemm_body<%d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, false, false, %d>(p);\n"
+             "    dg::gemm_body<%d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, %d, false, false, %d>(p, blockIdx.x + p.vbase);\n"
              "}\n",
              s.t.nw * 64, s.t.occ * s.t.nw / 4, s.t.bm, s.t.bn, s.t.wgm, s.t.nw, s.t.lw, s.t.stages, s.t.km, s.t.occ,
              s.kind, s.epi, s.ct, s.cs, s.cm, s.cn, s.ck, s.t.nsb);
@@ -240,14 +240,18 @@ int jit_run(const dg_gemm_args& a, const TileCfg& cfg, int epi, int split, const
             g_fn.emplace(fkey, fn);   // modules stay loaded for the life of the process
         }
     }
-    KParams kp = p;
-    size_t kp_size = sizeof(kp);
-    void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &kp, HIP_LAUNCH_PARAM_BUFFER_SIZE, &kp_size, HIP_LAUNCH_PARAM_END};
-    const hipError_t e = hipModuleLaunchKernel(fn, (unsigned)grid, 1, 1, (unsigned)(cfg.nw * 64), 1, 1, 0, st, nullptr,
-                                               config);
-    if (e != hipSuccess) {
-        dg_set_error(hipGetErrorString(e));
-        return DG_ELAUNCH;
+    // (launches of at most `grid` workgroups over the plan's p.vgrid, as for the ahead-of-time kernels)
+    for (int base = 0; base < p.vgrid; base += (int)grid) {
+        KParams kp = p;
+        kp.vbase = base;
+        size_t kp_size = sizeof(kp);
+        void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &kp, HIP_LAUNCH_PARAM_BUFFER_SIZE, &kp_size, HIP_LAUNCH_PARAM_END};
+        const unsigned n = (unsigned)std::min<int64_t>(grid, (int64_t)p.vgrid - base);
+        const hipError_t e = hipModuleLaunchKernel(fn, n, 1, 1, (unsigned)(cfg.nw * 64), 1, 1, 0, st, nullptr, config);
+        if (e != hipSuccess) {
+            dg_set_error(hipGetErrorString(e));
+            return DG_ELAUNCH;
+        }
     }
     return DG_OK;
 }

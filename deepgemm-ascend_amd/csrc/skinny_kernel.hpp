@@ -51,7 +51,7 @@ __device__ __forceinline__ int shift_at_use(int x, int sh) {
 }
 
 template <int KIND, int MT, int NB, int NW, int D, int AR, int EPI>
-__global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const KParams p) {
+__device__ __forceinline__ void skinny_body(const KParams& p, const int vb) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
     constexpr bool kBf16 = KIND == kBF16;
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
     int t, split = 0;
     if (split_k > 1) {
         // grid = 8 * ceil(strips / 8) * split_k; all splits of a strip share blockIdx % 8 (XCD)
-        const int b = blockIdx.x, rr = b >> 3;
+        const int b = vb, rr = b >> 3;
         t = (rr / split_k) * 8 + (b & 7);
         split = rr % split_k;
         if (p.split_spread) {
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const 
         }
         if (t >= p.num_tiles) return;
     } else {
-        t = blockIdx.x;
+        t = vb;
     }
     const int tile_id = t;
     const int nn = p.num_n_blocks;
@@ -441,7 +441,7 @@ namespace dg {
 // loop goes global -> LDS, so no vector-memory result lands in a register and the only waits are
 // the explicit per-group ones.
 template <int KIND, int MT, int NB, int D, int EPI>
-__device__ __forceinline__ void skinny_rows_body(const KParams& p) {
+__device__ __forceinline__ void skinny_rows_body(const KParams& p, const int vb) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
     constexpr bool kBf16 = KIND == kBF16;
@@ -483,7 +483,7 @@ __device__ __forceinline__ void skinny_rows_body(const KParams& p) {
     int t, split = 0;
     if (split_k > 1) {
         // grid = 8 * ceil(strips / 8) * split_k; all splits of a strip share blockIdx % 8 (XCD)
-        const int b = blockIdx.x, rr = b >> 3;
+        const int b = vb, rr = b >> 3;
         t = (rr / split_k) * 8 + (b & 7);
         split = rr % split_k;
         if (p.split_spread) {
@@ -492,7 +492,7 @@ __device__ __forceinline__ void skinny_rows_body(const KParams& p) {
         }
         if (t >= p.num_tiles) return;
     } else {
-        t = blockIdx.x;
+        t = vb;
     }
     const int tile_id = t;
     const int nn = p.num_n_blocks;
@@ -709,7 +709,12 @@ __device__ __forceinline__ void skinny_rows_body(const KParams& p) {
 // and above emitted no launch stub for it)
 template <int KIND, int MT, int NB, int D, int EPI>
 __global__ __launch_bounds__(MT * NB * 64, 1) void skinny_rows_kernel(const KParams p) {
-    skinny_rows_body<KIND, MT, NB, D, EPI>(p);
+    skinny_rows_body<KIND, MT, NB, D, EPI>(p, blockIdx.x + p.vbase);
+}
+
+template <int KIND, int MT, int NB, int NW, int D, int AR, int EPI>
+__global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const KParams p) {
+    skinny_body<KIND, MT, NB, NW, D, AR, EPI>(p, blockIdx.x + p.vbase);
 }
 
 }  // namespace dg

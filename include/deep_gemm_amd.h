@@ -266,6 +266,10 @@ typedef struct dg_launch_info {
     int32_t split_k;              /* K ranges per tile (1 = unsplit)                              */
     int32_t persistent;           /* 1: workgroups walk tiles (grid < tiles possible)             */
     int32_t skinny;               /* 1: the decode-shape kernel, 2: its shared-ring variant, 3: the decode GEMV kernel (block_m = M rows served, block_n = rows of B per workgroup, 64 / its K split) */
+    int64_t plan_workgroups;      /* workgroups of the plan; under a CU cap (num_cus below the
+                                     device's CUs) they go out in stream-ordered launches of at
+                                     most `grid` <= num_cus workgroups each (the persistent kernel:
+                                     one launch of `grid` workgroups walking every tile)          */
 } dg_launch_info;
 int dg_launch_plan(const dg_gemm_args *args, dg_launch_info *info);
 

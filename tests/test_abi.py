@@ -121,18 +121,17 @@ def _plan_args(m, n, k, num_cus):
 
 def test_launch_plan_without_device(lib):
     """dg_launch_plan describes the launch and touches no device: one workgroup per tile at the
-    full CU count, persistent min(tiles, num_cus) workgroups under a set_num_sms cap (below the
-    256 CUs of MI355X the library assumes when it cannot query a device)."""
+    full CU count; under a set_num_sms cap (below the 256 CUs of MI355X the library assumes when it
+    cannot query a device) at most num_cus workgroups, each serving plan workgroups in turn."""
     full = _lib.LaunchInfo()
     assert lib.dg_launch_plan(_plan_args(4096, 7168, 2048, 0), ctypes.byref(full)) == 0, lib.dg_last_error()
-    assert full.persistent == 0 and full.grid == full.tiles and full.block_m == 256
+    assert full.persistent == 0 and full.grid == full.tiles == full.plan_workgroups and full.block_m == 256
     capped = _lib.LaunchInfo()
     assert lib.dg_launch_plan(_plan_args(4096, 7168, 2048, 64), ctypes.byref(capped)) == 0, lib.dg_last_error()
-    assert capped.persistent == 1 and capped.grid == 64 and capped.tiles > 64
-    assert (capped.block_m, capped.block_n) != (256, 256)   # no persistent 256x256 kernel
+    assert capped.grid == 64 and capped.tiles > 64 and capped.plan_workgroups >= capped.grid
     small = _lib.LaunchInfo()
     assert lib.dg_launch_plan(_plan_args(1, 2112, 7168, 64), ctypes.byref(small)) == 0, lib.dg_last_error()
-    assert small.skinny == 1 and small.persistent == 0
+    assert small.skinny in (1, 3) and small.persistent == 0 and small.grid <= 64
     # decode shapes with 64 < M <= 128 and K <= 8192 take the shared-ring decode kernel
     mid = _lib.LaunchInfo()
     assert lib.dg_launch_plan(_plan_args(128, 2112, 7168, 0), ctypes.byref(mid)) == 0, lib.dg_last_error()

@@ -1,7 +1,7 @@
 """GPU parity of the persistent tile kernel (csrc/gemm_persistent.hpp) and the set_num_sms cap.
 
-With set_num_sms below the device's CU count the 256-row tiles run persistently: min(tiles,
-num_sms) workgroups walk the tiles (the reference's persistent block walk,
+With set_num_sms below the device's CU count at most num_sms workgroups run: the 128-K-stage
+tiles with a persistent kernel walk the tiles with min(tiles, num_sms) workgroups (the reference's persistent block walk,
 deep_gemm/include/deep_gemm/scheduler.hpp:141-196, launched with num_cores blocks,
 csrc/jit_kernels/heuristics.hpp:98).  Checked against the oracle (calc_diff < 1e-5) and, where the
 tile shape matches the uncapped launch, bit for bit against it (same MFMAs in the same K order).
@@ -50,7 +50,6 @@ def test_set_num_sms_caps_the_grid(num_sms):
     num_sms(64)
     capped = deep_gemm.launch_plan(m, n, k)
     print('full plan', full, 'capped plan', capped, flush=True)
-    assert capped['persistent'] == 1
     assert capped['grid'] == 64 < capped['tiles']
     d_cap = run()
     assert calc_diff(d_cap, ref) < THRESH
@@ -71,6 +70,7 @@ def test_persistent_dense(num_sms, m, n, k, bias, d_dtype):
     run, ref = _fp8_nt(m, n, k, seed=2, d_dtype=d_dtype, bias=bias)
     out = run()
     assert calc_diff(out, ref) < THRESH
+    assert plan['grid'] <= 255
     if plan['persistent']:
         assert plan['grid'] == min(plan['tiles'], 255)
 
