@@ -68,7 +68,7 @@ def calibrate_copy():
 PEAK_CLOCK_MHZ = 2400.0      # engine clock the published peaks are quoted at
 
 
-def sustained_clock(step, seconds=0.6):
+def sustained_clock(step, seconds=1.0):
     """Shader clock and socket power while `step` runs back to back for `seconds` (the clock the
     chip holds under this load: MI355X is power-limited, so the published peak at 2.4 GHz is not
     reachable).  Sampled from the SMU metrics table through amdsmi every ~5 ms; the table refreshes
@@ -89,7 +89,12 @@ def sustained_clock(step, seconds=0.6):
             try:
                 m = amdsmi.amdsmi_get_gpu_metrics_info(h)
                 clks = [c for c in m.get('current_gfxclks', []) if isinstance(c, int)]
-                if m.get('average_gfx_activity', 0) not in (0, 'N/A') and clks:
+                if not clks:
+                    c = m.get('current_gfxclk')
+                    clks = [c] if isinstance(c, int) else []
+                # (idle XCDs sit near 100 MHz; a sample taken before the clock ramps is not the
+                # sustained clock)
+                if clks and min(clks) >= 1000:
                     samples.append((sum(clks) / len(clks), m.get('current_socket_power')))
             except Exception:   # noqa: BLE001
                 pass
@@ -114,7 +119,7 @@ def sustained_clock(step, seconds=0.6):
     except Exception:   # noqa: BLE001
         pass
     if not samples:
-        return {'error': 'no samples with the GPU active'}
+        return {'error': 'no samples at a loaded clock (>= 1000 MHz on every XCD)'}
     clk = sorted(c for c, _ in samples)
     pw = sorted(p for _, p in samples if isinstance(p, (int, float)))
     return {'clock_mhz_median': round(clk[len(clk) // 2], 1), 'clock_mhz_min': round(clk[0], 1),
