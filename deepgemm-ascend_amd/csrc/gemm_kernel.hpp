@@ -363,13 +363,45 @@ __device__ __forceinline__ void anchored_tile(const int* psum, int num_groups, c
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Old D values of a full 32-column block (accumulate), read ahead of its epilogue_block so that a
+// wave issues the reads of several blocks before waiting for any (the lane's 16 values, in the
+// accumulator's element order); zeros where epilogue_block reads D itself (ragged blocks).
+template <int EPI>
+__device__ __forceinline__ void load_old_block(const KParams& p, const uint8_t* d_base, int m, bool row_ok, int nblk,
+                                               int N, int q, float (&old)[16]) {
+    constexpr bool kF32 = EPI == kEpiF32;
+    using OutT = typename Cond<kF32, float, uint16_t>::type;
+    const OutT* drow = reinterpret_cast<const OutT*>(d_base) + (int64_t)m * p.ldd;
+    const bool full = p.vec_store && nblk + 32 <= N;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) old[i] = 0.f;
+    if (full && row_ok) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            if constexpr (kF32) {
+                const f32x4 o = *reinterpret_cast<const f32x4*>(drow + nblk + 8 * g + 4 * q);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) old[4 * g + i] = o[i];
+            } else {
+                const i32x2 o = *reinterpret_cast<const i32x2*>(drow + nblk + 8 * g + 4 * q);
+                old[4 * g + 0] = bf16_to_f32((uint16_t)(o[0] & 0xffff));
+                old[4 * g + 1] = bf16_to_f32((uint16_t)((uint32_t)o[0] >> 16));
+                old[4 * g + 2] = bf16_to_f32((uint16_t)(o[1] & 0xffff));
+                old[4 * g + 3] = bf16_to_f32((uint16_t)((uint32_t)o[1] >> 16));
+            }
+        }
+    }
+}
+
 // Epilogue of one 32x32 accumulator block: lane (r, q) holds output row m (the caller's
 // row_ok / pad_row flags describe it) and columns nblk + 8 g + 4 q + {0..3} in elements
 // 4 g + {0..3}; alpha, bias, accumulate, the D dtype (EPI) and stochastic rounding / FP8
 // quantisation are applied here and the block is stored to D (d_base already offset by batch).
+// old_pre: the block's old D values read ahead (load_old_block), or nullptr to read them here.
 template <int EPI>
 __device__ __forceinline__ void epilogue_block(const KParams& p, const f32x16& acc, uint8_t* d_base, int m,
-                                               bool row_ok, bool pad_row, int nblk, int N, int batch, int q) {
+                                               bool row_ok, bool pad_row, int nblk, int N, int batch, int q,
+                                               const float* old_pre = nullptr) {
     const float alpha = p.alpha;
     constexpr bool kF32 = EPI == kEpiF32;
     constexpr bool kSR = EPI == kEpiBf16SR;
@@ -421,10 +453,15 @@ __device__ __forceinline__ void epilogue_block(const KParams& p, const f32x16& a
                 for (int i = 0; i < 4; ++i) v[4 * g + i] += to_f(bp[nblk + 8 * g + 4 * q + i]);
         }
         if (acc_old && row_ok) {
+            if (old_pre != nullptr) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
+                for (int i = 0; i < 16; ++i) v[i] += old_pre[i];
+            } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[4 * g + i] += to_f(drow[nblk + 8 * g + 4 * q + i]);
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[4 * g + i] += to_f(drow[nblk + 8 * g + 4 * q + i]);
+            }
         }
         if constexpr (kF32) {
             if (row_ok) {
@@ -616,6 +653,14 @@ __device__ __forceinline__ void gemm_body(const KParams& p, const int vb) {
             split = b % split_k;
         }
         if (t >= p.num_tiles) return;
+    } else if (gemm_type == kKGrouped) {
+        // K-grouped: each group's tiles are spread over the XCDs on their own, so at any time all
+        // XCDs work on one group and its A / B K-slices (Kg x (M + N) bytes) are streamed once,
+        // instead of every XCD pair streaming another group's and the groups together overflowing
+        // the last-level cache.  (groups in order; a group's tiles are consecutive workgroups)
+        const int per_group = nm * nn;
+        const int g = vb / per_group;
+        t = g * per_group + xcd_remap(vb - g * per_group, per_group);
     } else {
         t = xcd_remap(vb, p.vgrid);
     }
@@ -1236,6 +1281,24 @@ __device__ __forceinline__ void gemm_body(const KParams& p, const int vb) {
         bool pad_row = false;
         if (gemm_type == kMGroupedPsum) pad_row = m >= valid_end;
         else if (gemm_type == kMGroupedIdx) pad_row = row_ok && p.layout[m] != group;
+        if constexpr (EPI == kEpiF32 || EPI == kEpiBf16) {
+            if (p.accumulate) {
+                // the old D of this row of blocks in one burst, then the blocks
+                float old[TN][16];
+                static_for<TN>([&](auto jn_c) {
+                    constexpr int jn = decltype(jn_c)::value;
+                    if (!(kRagged && jn >= TN_LAST && wn == WGN - 1))
+                        load_old_block<EPI>(p, d_base, m, row_ok, n0 + wn * WN + jn * 32, N, q, old[jn]);
+                });
+                static_for<TN>([&](auto jn_c) {
+                    constexpr int jn = decltype(jn_c)::value;
+                    if (kRagged && jn >= TN_LAST && wn == WGN - 1) return;
+                    epilogue_block<EPI>(p, acc[jn][jm], d_base, m, row_ok, pad_row, n0 + wn * WN + jn * 32, N, batch, q,
+                                        old[jn]);
+                });
+                return;
+            }
+        }
         static_for<TN>([&](auto jn_c) {
             constexpr int jn = decltype(jn_c)::value;
             if (kRagged && jn >= TN_LAST && wn == WGN - 1) return;   // no such block in this wave
