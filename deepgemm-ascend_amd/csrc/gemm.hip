@@ -63,6 +63,14 @@ KernelFn lookup_kernel(int kind, int bm, int bn, int epi, bool persistent) {
     }
 }
 
+KernelFn lookup_walk(int kind, int bm, int bn, int epi) {
+    switch (kind) {
+        case kFP8FP8: return lookup_walk_fp8fp8(bm, bn, epi);
+        case kBF16: return lookup_walk_bf16(bm, bn, epi);
+        default: return nullptr;
+    }
+}
+
 int device_cus() {
     static int cached[64] = {0};
     int dev = 0;
@@ -711,6 +719,20 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     // one workgroup per CU (set_num_sms caps them)
     int64_t grid = persistent ? std::min<int64_t>(tiles, (int64_t)cus * cfg.occ)
                        : plan.split > 1 ? align_up64(tiles, 8) * plan.split : tiles;
+    // Anchored M-grouped tiles under a CU cap: one workgroup per allowed CU walks the layout's real
+    // tiles (gemm_walk_kernel).  Uncapped, the upper-bound grid is faster: the dispatcher hands each
+    // CU that frees the next real tile and the spare workgroups exit after one scan, where a fixed
+    // round-robin walk loses that balance (G=32 routed, alignment 128, cold us: N=4096 K=7168 366
+    // vs 346, N=7168 K=2048 217 vs 199; m_indices 407 vs 391, 249 vs 229).  DG_ANCHORED_WALK=1 forces
+    // the walk (tuning).
+    static const char* walk_env = std::getenv("DG_ANCHORED_WALK");
+    const bool walk = p.anchored && !jit && plan.split == 1 &&
+                      (cus_capped(cus) || (walk_env != nullptr && walk_env[0] == '1')) &&
+                      lookup_walk(a.kind, cfg.bm, cfg.bn, epi_kind) != nullptr;
+    if (walk) {
+        fn = lookup_walk(a.kind, cfg.bm, cfg.bn, epi_kind);
+        grid = std::min<int64_t>(tiles, cus);
+    }
     p.a_span = a_span; p.b_span = b_span; p.sfa_span = sfa_span; p.sfb_span = sfb_span;
     if (grid > 0x7fffffffLL) return dg_set_error("dg_gemm: too many tiles");
     p.split_k = plan.split;
@@ -749,7 +771,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     p.vgrid = (int)grid;
     p.vbase = 0;
     int64_t launched = grid;
-    if (cus_capped(cus) && !persistent) launched = std::min<int64_t>(grid, cus >= 8 ? cus / 8 * 8 : cus);
+    if (cus_capped(cus) && !persistent && !walk) launched = std::min<int64_t>(grid, cus >= 8 ? cus / 8 * 8 : cus);
     if (info != nullptr) {
         info->plan_workgroups = grid;
         info->block_m = gemv_mr > 0 ? gemv_mr : cfg.bm;
@@ -758,7 +780,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         info->threads = threads;
         info->tiles = tiles;
         info->split_k = gemv_mr > 0 ? 1 : plan.split;
-        info->persistent = persistent ? 1 : 0;
+        info->persistent = persistent || walk ? 1 : 0;
         info->skinny = gemv_mr > 0 ? 3 : skinny ? (plan.skinny_rows ? 2 : 1) : 0;
         return DG_OK;
     }
@@ -797,7 +819,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
             dg_set_error(hipGetErrorString(e));
             return DG_ELAUNCH;
         }
-        if (persistent) break;   // (one launch walks every tile)
+        if (persistent || walk) break;   // (one launch walks every tile)
     }
     return DG_OK;
 }

@@ -544,7 +544,7 @@ __device__ __forceinline__ void epilogue_block(const KParams& p, const f32x16& a
 // arguments, the JIT compiles one body per problem (csrc/jit.hip).
 template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI, int CT = -1,
           int CS = 0, int CM = 0, int CN = 0, int CK = 0, bool AMN = false, bool BMN = false, int NSB_ = 0>
-__device__ __forceinline__ void gemm_body(const KParams& p, const int vb) {
+__device__ __forceinline__ void gemm_body(const KParams& p, const int vb, const int known_total = -1) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
     constexpr bool kBf16 = KIND == kBF16;
@@ -676,8 +676,8 @@ __device__ __forceinline__ void gemm_body(const KParams& p, const int vb) {
     if (anchored) {
         const int* runs = gemm_type == kMGroupedIdx ? p.runs : nullptr;
         // the launch's real tiles spread over the XCDs as xcd_remap spreads a full grid
-        const int total =
-            __builtin_amdgcn_readfirstlane(anchored_total(p.layout, p.num_groups, runs, p.alignment, BM, M, nn));
+        const int total = known_total >= 0 ? known_total
+            : __builtin_amdgcn_readfirstlane(anchored_total(p.layout, p.num_groups, runs, p.alignment, BM, M, nn));
         if (vb >= total) return;
         t = xcd_remap(vb, total);
         anchored_tile(p.layout, p.num_groups, runs, p.alignment, t, BM, M, nn, anchor_group, m0, nb, tile_end,
@@ -1305,6 +1305,24 @@ __device__ __forceinline__ void gemm_body(const KParams& p, const int vb) {
             epilogue_block<EPI>(p, acc[jn][jm], d_base, m, row_ok, pad_row, n0 + wn * WN + jn * 32, N, batch, q);
         });
     });
+}
+
+// Persistent walk over the real tiles of an anchored M-grouped launch (the reference's psum
+// scheduler, deep_gemm/include/deep_gemm/scheduler.hpp:144-162, on CDNA4 terms): one workgroup
+// per CU counts the layout's tiles once and serves tiles b, b + gridDim.x, ... below that count,
+// instead of a grid sized for the worst case whose spare workgroups exit.
+template <int BM, int BN, int WGM, int NW, int LW, int NSTAGE, int KM, int OCC, int KIND, int EPI, int NSB = 0>
+__global__ __launch_bounds__(NW * 64, OCC * NW / 4) void gemm_walk_kernel(const KParams p) {
+    const int gemm_type = p.gemm_type;
+    const int* runs = gemm_type == kMGroupedIdx ? p.runs : nullptr;
+    const int total = __builtin_amdgcn_readfirstlane(
+        anchored_total(p.layout, p.num_groups, runs, p.alignment, BM, p.m, p.num_n_blocks));
+    for (int vb = blockIdx.x; vb < total; vb += gridDim.x) {
+        gemm_body<BM, BN, WGM, NW, LW, NSTAGE, KM, OCC, KIND, EPI, -1, 0, 0, 0, 0, false, false, NSB>(p, vb, total);
+        // (every load of the tile, including the ring's dead ones, lands before the next tile's)
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
 }
 
 // The ahead-of-time kernel of one tile shape: everything from the arguments.

@@ -3,4 +3,5 @@
 
 namespace dg {
 KernelFn lookup_kernel_bf16(int bm, int bn, int epi, bool persistent) { return lookup_tile<kBF16>(bm, bn, epi, persistent); }
+KernelFn lookup_walk_bf16(int bm, int bn, int epi) { return lookup_walk<kBF16>(bm, bn, epi); }
 }  // namespace dg

@@ -78,6 +78,31 @@ KernelFn pick_persistent_epi(int epi) {
     }
 }
 
+// Persistent walk kernels exist for the anchored (M-grouped, more than 256 rows) tiles.
+template <int I, int KIND>
+KernelFn pick_walk_epi(int epi) {
+    constexpr TileCfg t = kTiles[I];
+    if constexpr (t.bm <= 256) {
+        return nullptr;
+    } else {
+        switch (epi) {
+            case kEpiF32: return &gemm_walk_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiF32, t.nsb>;
+            case kEpiBf16: return &gemm_walk_kernel<t.bm, t.bn, t.wgm, t.nw, t.lw, t.stages, t.km, t.occ, KIND, kEpiBf16, t.nsb>;
+            default: return nullptr;
+        }
+    }
+}
+
+template <int KIND, int I = 0>
+KernelFn lookup_walk(int bm, int bn, int epi) {
+    if constexpr (I == kNumTiles) {
+        return nullptr;
+    } else {
+        if (bm == kTiles[I].bm && bn == kTiles[I].bn) return pick_walk_epi<I, KIND>(epi);
+        return lookup_walk<KIND, I + 1>(bm, bn, epi);
+    }
+}
+
 template <int KIND, int I = 0>
 KernelFn lookup_tile(int bm, int bn, int epi, bool persistent) {
     if constexpr (I == kNumTiles) {
@@ -127,6 +152,9 @@ KernelFn lookup_gemv(int mr, int epi, int waves);   // waves per workgroup: 4 or
 int gemv_lds(int mr, int k, int rpw);
 
 KernelFn lookup_kernel_fp8fp8(int bm, int bn, int epi, bool persistent);
+// anchored M-grouped tiles walked persistently (gemm_walk_kernel), e4m3 x e4m3 / bf16
+KernelFn lookup_walk_fp8fp8(int bm, int bn, int epi);
+KernelFn lookup_walk_bf16(int bm, int bn, int epi);
 KernelFn lookup_kernel_fp8fp4(int bm, int bn, int epi, bool persistent);
 KernelFn lookup_kernel_fp4fp4(int bm, int bn, int epi, bool persistent);
 KernelFn lookup_kernel_bf16(int bm, int bn, int epi, bool persistent);

@@ -128,6 +128,7 @@ def test_cap_anchored_m_grouped(cap, psum):
         plan = deep_gemm.launch_plan(total, n, k, gemm_type=2 if psum else 3, num_groups=len(sizes))
         print(f'cu cap 36 anchored psum={psum} plan={plan}', flush=True)
         assert (plan['block_m'], plan['block_n']) == (384, 192) and plan['grid'] <= 36
+        assert plan['persistent'] == 1   # the anchored tiles' walk kernel
         deep_gemm.m_grouped_fp8_gemm_nt_contiguous((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d, layout_t.cuda(),
                                                    use_psum_layout=psum)
         torch.cuda.synchronize()
@@ -139,6 +140,39 @@ def test_cap_anchored_m_grouped(cap, psum):
         valid[sl] = True
     assert torch.equal(out[~valid], torch.zeros_like(out[~valid]))
     ref = og.m_grouped_contiguous(a_deq, b_deq, layout_t, psum, alignment)
+    assert calc_diff(out[valid], ref[valid]) < THRESH
+
+
+@pytest.mark.parametrize('psum', [True, False])
+def test_cap_anchored_m_grouped_bf16(cap, psum):
+    """The bf16 anchored tiles' walk kernel under a cap (psum and m_indices, an empty group)."""
+    cap(44)
+    alignment, n, k = 128, 768, 1024
+    sizes = [300, 0, 129, 77, 512, 1]
+    total, ps = ol.psum_from_sizes(sizes, alignment)
+    g = gen(17)
+    a = (torch.randn(total, k, generator=g) * 0.1).to(torch.bfloat16)
+    for sl in ol.psum_pad_slices(ps, alignment):
+        a[sl] = 0
+    b = (torch.randn(len(sizes), n, k, generator=g) * 0.1).to(torch.bfloat16)
+    layout_t = torch.tensor(ps, dtype=torch.int32) if psum else ol.m_indices_from_psum(ps, alignment, total)
+    d = torch.full((total, n), float('nan'), dtype=torch.bfloat16, device='cuda')
+    old = deep_gemm.get_mk_alignment_for_contiguous_layout()
+    deep_gemm.set_mk_alignment_for_contiguous_layout(alignment)
+    try:
+        plan = deep_gemm.launch_plan(total, n, k, kind=3, gemm_type=2 if psum else 3, num_groups=len(sizes))
+        print(f'cu cap 44 anchored bf16 psum={psum} plan={plan}', flush=True)
+        assert plan['grid'] <= 44
+        deep_gemm.m_grouped_bf16_gemm_nt_contiguous(a.cuda(), b.cuda(), d, layout_t.cuda(), use_psum_layout=psum)
+        torch.cuda.synchronize()
+    finally:
+        deep_gemm.set_mk_alignment_for_contiguous_layout(old)
+    out = d.cpu()
+    valid = torch.zeros(total, dtype=torch.bool)
+    for sl in ol.psum_slices(ps, alignment):
+        valid[sl] = True
+    assert torch.equal(out[~valid], torch.zeros_like(out[~valid]))
+    ref = og.m_grouped_contiguous(a.float(), b.float(), layout_t, psum, alignment)
     assert calc_diff(out[valid], ref[valid]) < THRESH
 
 
