@@ -107,6 +107,7 @@ struct Plan {
     int skinny_ar;      // and rows of A it stages
     int skinny_rows;    // 1: the shared-ring decode kernel (skinny_rows_kernel, skinny_nw = mt x nb waves, ring skinny_d)
     int gemv_mr;        // > 0: the decode GEMV kernel for M <= gemv_mr (split_stages = rows of B per wave)
+    int split_reduce;   // 1: split-K partials summed by a second launch (shared-ring kernel only)
 };
 
 // K elements of one kernel stage of tile t
@@ -192,14 +193,15 @@ void gemv_env(int& ks, int& waves) {
 struct SkinnyEnv {
     int mode;   // -1 default, 0 off, 1 forced configuration
     int mt, nb, nw, d, ar, split;
-    int rows, rmt, rnb, rd, rsplit;   // DG_SKINNY_ROWS: -1 default, 0 off, 1 forced "mt,nb,d[,split]"
+    int rows, rmt, rnb, rd, rsplit;   // DG_SKINNY_ROWS: -1 default, 0 off, 1 forced "mt,nb,d[,split[,reduce]]"
+    int rreduce;                      // (-1: the plan's choice, 0: last-arriving workgroup, 1: second launch)
 };
 SkinnyEnv skinny_env() {
-    SkinnyEnv e = {-1, 0, 0, 0, 0, 0, 0, -1, 0, 0, 0, 0};
+    SkinnyEnv e = {-1, 0, 0, 0, 0, 0, 0, -1, 0, 0, 0, 0, -1};
     const char* rs = std::getenv("DG_SKINNY_ROWS");
     if (rs != nullptr && *rs != '\0') {
         if (std::strcmp(rs, "0") == 0) e.rows = 0;
-        else if (std::sscanf(rs, "%d,%d,%d,%d", &e.rmt, &e.rnb, &e.rd, &e.rsplit) >= 3) e.rows = 1;
+        else if (std::sscanf(rs, "%d,%d,%d,%d,%d", &e.rmt, &e.rnb, &e.rd, &e.rsplit, &e.rreduce) >= 3) e.rows = 1;
     }
     const char* s = std::getenv("DG_SKINNY");
     if (s == nullptr || *s == '\0') return e;
@@ -231,6 +233,19 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
         (a.gemm_type == kNormal || a.gemm_type == kBatched) && (int64_t)ceil_div(a.n, 32) * groups0 <= 2 * (int64_t)cus) {
         rows_env.rows = 1;
         rows_env.rmt = 4; rows_env.rnb = 1; rows_env.rd = 4; rows_env.rsplit = 0;
+        // Long K over many columns: 64-column strips (half the A bytes per column of D), split 2-4 ways
+        // to fill the CUs, the partials summed by a second launch (split_reduce_kernel) instead of
+        // each strip's last workgroup.  Measured on MI355X (event us, warm, 32-column plan in
+        // brackets): 128x4096x7168 20.5 (23.0), 128x3072x7168 19.3 (21.8), 96x4096x7168 19.3 (21.6),
+        // 128x6144x7168 26.2 (29.4), 128x7168x7168 27.4 (30.0); level at 128x2112x7168 (18.6 vs
+        // 18.7) and behind for K <= 4096 (128x4096x4096 18.9 vs 18.0, 128x7168x4096 21.3 vs 19.7),
+        // where the second launch's fixed cost outweighs the saved A traffic.
+        const int64_t strips2 = (int64_t)ceil_div(a.n, 64) * groups0;
+        if (allow_split && a.k > 4096 && a.n >= 3072 && 2 * strips2 <= cus) {
+            rows_env.rnb = 2;
+            rows_env.rsplit = (int)std::max<int64_t>(2, std::min<int64_t>(4, cus / strips2));
+            rows_env.rreduce = 1;
+        }
     }
     if (rows_env.rows == 1 && a.m <= 32 * rows_env.rmt &&
         lookup_skinny_rows(a.kind, rows_env.rmt, rows_env.rnb, rows_env.rd, kEpiBf16) != nullptr) {
@@ -246,7 +261,8 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
         }
         const int ss = ceil_div(nk64, sp);
         out = {{32 * env.rmt, 32 * env.rnb, 0, env.rmt * env.rnb, 0, 0, 0, 0, 0}, ceil_div(nk64, ss), ss,
-               env.rmt * env.rnb, env.rd, 32 * env.rmt, 1};
+               env.rmt * env.rnb, env.rd, 32 * env.rmt, 1, 0, 0};
+        out.split_reduce = out.split > 1 && env.rreduce == 1 ? 1 : 0;
         return true;
     }
     int mt = a.m <= 32 ? 1 : (a.m <= 64 ? 2 : 4), nb = 1, nw = 4, d = 2, ar = a.m <= 16 ? 16 : 32 * mt;
@@ -744,6 +760,15 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         p.split_spread = spread != nullptr && spread[0] == '1';
         p.counters = reinterpret_cast<int*>(workspace);
         p.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + kCounterBytes);
+        p.split_reduce = plan.split_reduce;
+    }
+    KernelFn reduce_fn = nullptr;
+    if (p.split_reduce) {
+        reduce_fn = lookup_split_reduce(cfg.bm / 32, cfg.bn / 32, epi_kind);
+        if (reduce_fn == nullptr) {
+            dg_set_error("dg_gemm: no compiled split-K reduction kernel for this plan");
+            return DG_ENOKERNEL;
+        }
     }
     int threads = skinny ? plan.skinny_nw * 64 : tile_threads(cfg.bm, cfg.bn);
     unsigned lds_bytes = 0;
@@ -782,6 +807,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
         info->split_k = gemv_mr > 0 ? 1 : plan.split;
         info->persistent = persistent || walk ? 1 : 0;
         info->skinny = gemv_mr > 0 ? 3 : skinny ? (plan.skinny_rows ? 2 : 1) : 0;
+        info->split_reduce = p.split_reduce;
         return DG_OK;
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -820,6 +846,23 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
             return DG_ELAUNCH;
         }
         if (persistent || walk) break;   // (one launch walks every tile)
+    }
+    if (reduce_fn != nullptr) {
+        // second launch: one wave per 32x32 block of the tiles, DG_REDUCE_WAVES (tuning, default 1) per workgroup
+        static const int rw_env = std::getenv("DG_REDUCE_WAVES") ? std::atoi(std::getenv("DG_REDUCE_WAVES")) : 1;
+        const int rw = rw_env == 2 || rw_env == 4 ? rw_env : 1;
+        const int64_t rgrid = ceil_div(tiles * (cfg.bm / 32) * (cfg.bn / 32), rw);
+        const int64_t rlaunched = cus_capped(cus) ? std::min<int64_t>(rgrid, cus >= 8 ? cus / 8 * 8 : cus) : rgrid;
+        p.vgrid = (int)rgrid;
+        for (int64_t base = 0; base < rgrid; base += rlaunched) {
+            p.vbase = (int)base;
+            const unsigned n = (unsigned)std::min<int64_t>(rlaunched, rgrid - base);
+            const hipError_t e = launch_module_kernel(reinterpret_cast<const void*>(reduce_fn), n, 64u * rw, p, st, 0);
+            if (e != hipSuccess) {
+                dg_set_error(hipGetErrorString(e));
+                return DG_ELAUNCH;
+            }
+        }
     }
     return DG_OK;
 }

@@ -58,6 +58,7 @@ struct KParams {
     float* ws;
     int* counters;
     int split_spread;          // test knob: the splits of a tile go to consecutive workgroups (other XCDs)
+    int split_reduce;          // split-K partials summed by a second launch (split_reduce_kernel)
     // M-grouped psum GEMMs with tiles anchored at each group's first row (BM need not divide the
     // alignment): an upper bound of the tile count is launched; the grid's extra workgroups exit.
     int anchored;

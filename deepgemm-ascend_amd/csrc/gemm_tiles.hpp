@@ -142,9 +142,11 @@ KernelFn lookup_skinny(int kind, int mt, int nb, int nw, int d, int ar, int epi)
 struct SkinnyRowsCfg {
     int mt, nb, d;
 };
-constexpr SkinnyRowsCfg kSkinnyRows[] = {{4, 1, 3}, {4, 1, 4}, {4, 1, 5}, {4, 2, 4}, {2, 1, 4}, {2, 2, 4}};
+constexpr SkinnyRowsCfg kSkinnyRows[] = {{4, 1, 3}, {4, 1, 4}, {4, 1, 5}, {4, 2, 4}, {4, 4, 4}, {2, 1, 4}, {2, 2, 4}, {2, 4, 4}};
 constexpr int kNumSkinnyRows = sizeof(kSkinnyRows) / sizeof(kSkinnyRows[0]);
 KernelFn lookup_skinny_rows(int kind, int mt, int nb, int d, int epi);
+// second launch of a split-K shared-ring plan: sums the partials of each 32x32 block, then its epilogue
+KernelFn lookup_split_reduce(int mt, int nb, int epi);
 
 // Decode GEMV kernels (csrc/gemv_kernel.hip): e4m3 x e4m3, M <= mr (1, 2, 4), fp32 / bf16 D;
 // whole rows of B per wave, A staged in LDS as f16 (gemv_lds(mr, k, rows per wave) bytes).

@@ -670,6 +670,17 @@ __device__ __forceinline__ void skinny_rows_body(const KParams& p, const int vb)
         auto part_off = [&](int sp) -> uint32_t {
             return m < M ? (uint32_t)((sp * NBLK + blk) * 1024 + lane * 16) * 4u : kOOBOffset;
         };
+        if (p.split_reduce) {
+            // the second launch (split_reduce_kernel) sums the partials: plain stores, made visible
+            // to it by the kernel boundary, and no arrival count
+            const uint32_t off = part_off(split);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(u32x4, f32x4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]}), rs_ws,
+                    off + 16 * g, 0, 0);
+            return;
+        }
         {
             const uint32_t off = part_off(split);
 #pragma unroll
@@ -710,6 +721,68 @@ __device__ __forceinline__ void skinny_rows_body(const KParams& p, const int vb)
 template <int KIND, int MT, int NB, int D, int EPI>
 __global__ __launch_bounds__(MT * NB * 64, 1) void skinny_rows_kernel(const KParams p) {
     skinny_rows_body<KIND, MT, NB, D, EPI>(p, blockIdx.x + p.vbase);
+}
+
+// Second launch of a split-K shared-ring plan (KParams::split_reduce): one wave per 32x32 output
+// block (block b = waves per workgroup x workgroup + wave, over the tiles' MT x NB blocks in the
+// first launch's order) sums the block's split_k fp32 partials in split order -- the same sums, in
+// the same order, as the first launch's own last-arriving workgroup would form, so D is the same bit
+// for bit -- and runs the block's epilogue.  The loads of up to eight splits are issued before any
+// is added.  Spreading the reduction over one wave per block keeps it off the critical path of a
+// single CU, whose load rate bounds how many partials one workgroup can sum quickly.
+template <int MT, int NB, int EPI>
+__device__ __forceinline__ void split_reduce_body(const KParams& p, const int vb) {
+    constexpr int NBLK = MT * NB, BN = 32 * NB;
+    constexpr int CH = 8;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int gb = vb * (int)(blockDim.x >> 6) + w;
+    const int tile_id = gb / NBLK, blk = gb - tile_id * NBLK;
+    if (tile_id >= p.num_tiles) return;
+    const int wjm = blk % MT, wjn = blk / MT;
+    const int r = lane & 31, q = lane >> 5;
+    int t = tile_id, batch = 0;
+    if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
+        batch = t / p.num_n_blocks;
+        t -= batch * p.num_n_blocks;
+    }
+    const int M = __builtin_amdgcn_readfirstlane(p.gemm_type == kMasked ? min(p.m, p.layout[batch]) : p.m);
+    if (M <= 0) return;
+    uint8_t* d_base = p.d;
+    if (p.gemm_type == kBatched || p.gemm_type == kMasked) d_base += (int64_t)batch * p.bsd * p.out_esize;
+    const int m = wjm * 32 + r;
+    const int split_k = p.split_k;
+    const float* const tile_ws = p.ws + (int64_t)tile_id * split_k * (NBLK * 1024);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(tile_ws, (int64_t)split_k * NBLK * 1024 * 4);
+    const uint32_t off0 = m < M ? (uint32_t)(blk * 1024 + lane * 16) * 4u : kOOBOffset;
+    f32x16 acc = f32x16{};
+    for (int sp0 = 0; sp0 < split_k; sp0 += CH) {
+        f32x4 v[CH][4];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const uint32_t off = sp0 + j < split_k && off0 != kOOBOffset ? off0 + (uint32_t)(sp0 + j) * (NBLK * 4096u) : kOOBOffset;
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                v[j][g] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * g, 0, 0));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // (a split past the last adds -0.0, the exact identity of IEEE addition, so no add is
+        // conditional and every load of the chunk is issued before the first add)
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const bool on = sp0 + j < split_k;
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[4 * g + i] += on ? v[j][g][i] : -0.0f;
+        }
+    }
+    epilogue_block<EPI>(p, acc, d_base, m, m < M, false, t * BN + wjn * 32, p.n, batch, q);
+}
+
+template <int MT, int NB, int EPI>
+__global__ __launch_bounds__(256) void split_reduce_kernel(const KParams p) {
+    split_reduce_body<MT, NB, EPI>(p, blockIdx.x + p.vbase);
 }
 
 template <int KIND, int MT, int NB, int NW, int D, int AR, int EPI>

@@ -55,7 +55,31 @@ KernelFn rows_find(int mt, int nb, int d, int epi) {
     }
 }
 
+template <int I>
+KernelFn reduce_epi(int epi) {
+    constexpr SkinnyRowsCfg c = kSkinnyRows[I];
+    switch (epi) {
+        case kEpiF32: return &split_reduce_kernel<c.mt, c.nb, kEpiF32>;
+        case kEpiBf16: return &split_reduce_kernel<c.mt, c.nb, kEpiBf16>;
+        case kEpiBf16SR: return &split_reduce_kernel<c.mt, c.nb, kEpiBf16SR>;
+        case kEpiFp8: return &split_reduce_kernel<c.mt, c.nb, kEpiFp8>;
+        default: return nullptr;
+    }
+}
+
+template <int I = 0>
+KernelFn reduce_find(int mt, int nb, int epi) {
+    if constexpr (I == kNumSkinnyRows) {
+        return nullptr;
+    } else {
+        if (mt == kSkinnyRows[I].mt && nb == kSkinnyRows[I].nb) return reduce_epi<I>(epi);
+        return reduce_find<I + 1>(mt, nb, epi);
+    }
+}
+
 }  // namespace
+
+KernelFn lookup_split_reduce(int mt, int nb, int epi) { return reduce_find(mt, nb, epi); }
 
 KernelFn lookup_skinny_rows(int kind, int mt, int nb, int d, int epi) {
     switch (kind) {

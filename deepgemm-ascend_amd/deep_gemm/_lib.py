@@ -59,6 +59,7 @@ class LaunchInfo(ctypes.Structure):
         ('block_m', ctypes.c_int32), ('block_n', ctypes.c_int32), ('grid', ctypes.c_int64),
         ('threads', ctypes.c_int32), ('tiles', ctypes.c_int64), ('split_k', ctypes.c_int32),
         ('persistent', ctypes.c_int32), ('skinny', ctypes.c_int32), ('plan_workgroups', ctypes.c_int64),
+        ('split_reduce', ctypes.c_int32),
     ]
 
 

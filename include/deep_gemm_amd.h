@@ -270,6 +270,8 @@ typedef struct dg_launch_info {
                                      device's CUs) they go out in stream-ordered launches of at
                                      most `grid` <= num_cus workgroups each (the persistent kernel:
                                      one launch of `grid` workgroups walking every tile)          */
+    int32_t split_reduce;         /* 1: a second launch sums the split-K partials (one wave per
+                                     32x32 block of D) instead of each tile's last workgroup      */
 } dg_launch_info;
 int dg_launch_plan(const dg_gemm_args *args, dg_launch_info *info);
 

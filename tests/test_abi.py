@@ -136,6 +136,15 @@ def test_launch_plan_without_device(lib):
     mid = _lib.LaunchInfo()
     assert lib.dg_launch_plan(_plan_args(128, 2112, 7168, 0), ctypes.byref(mid)) == 0, lib.dg_last_error()
     assert mid.skinny == 2 and mid.threads == 256 and mid.block_m == 128 and mid.block_n == 32
+    assert mid.split_reduce == 0
+    # long K over many columns: 64-column strips, the split-K partials summed by a second launch
+    # (only where the call can split K: here with the library's per-stream workspace)
+    wide = _lib.LaunchInfo()
+    wide_args = _plan_args(128, 4096, 7168, 0)
+    wide_args.library_workspace = 1
+    assert lib.dg_launch_plan(wide_args, ctypes.byref(wide)) == 0, lib.dg_last_error()
+    assert wide.skinny == 2 and wide.threads == 512 and wide.block_n == 64 and wide.split_reduce == 1
+    assert 2 <= wide.split_k <= 4
     long_k = _lib.LaunchInfo()
     assert lib.dg_launch_plan(_plan_args(128, 7168, 16384, 0), ctypes.byref(long_k)) == 0, lib.dg_last_error()
     assert long_k.skinny == 1

@@ -1,5 +1,6 @@
 """The shared-ring decode kernel (csrc/skinny_kernel.hpp, skinny_rows_kernel) on every configuration
-of its menu, forced through the DG_SKINNY_ROWS tuning override ("mt,nb,d[,split]"), against the CPU
+of its menu, forced through the DG_SKINNY_ROWS tuning override ("mt,nb,d[,split[,reduce]]"; reduce = 1:
+the split-K partials are summed by the second launch, split_reduce_kernel), against the CPU
 oracle (calc_diff < 1e-5): ragged N (a partial last strip), K ending inside a 64-K block and inside
 a group, K split across workgroups, every operand kind, fp32 accumulate and bias, batched and
 masked launches, odd M / N (the scale rows are fetched as row-pair dwords), and the bit-exact
@@ -16,7 +17,8 @@ from helpers import gen, operand, calc_diff
 pytestmark = pytest.mark.gpu
 THRESH = 1e-5
 # the kSkinnyRows menu of csrc/gemm_tiles.hpp, plus forced K splits
-CONFIGS = ['4,1,3', '4,1,4', '4,1,5', '4,2,4', '2,1,4', '2,2,4', '4,1,4,3', '2,2,4,5']
+CONFIGS = ['4,1,3', '4,1,4', '4,1,5', '4,2,4', '4,4,4', '2,1,4', '2,2,4', '2,4,4', '4,1,4,3', '2,2,4,5',
+           '4,1,4,3,1', '4,2,4,6,1', '4,4,4,9,1', '2,4,4,4,1']
 
 
 def _ms(cfg):
@@ -89,7 +91,7 @@ def test_rows_bf16(rows, cfg):
         assert calc_diff(d.cpu(), og.gemm_nt(a.float(), b.float())) < THRESH
 
 
-@pytest.mark.parametrize('cfg', ['4,1,4', '2,2,4,2'])
+@pytest.mark.parametrize('cfg', ['4,1,4', '2,2,4,2', '4,4,4,3,1'])
 def test_rows_bmm(rows, cfg):
     bs, m, n, k = 3, 57, 192, 640
     print(f'rows {cfg} bmm bs={bs} m={m} n={n} k={k}', flush=True)
@@ -104,7 +106,7 @@ def test_rows_bmm(rows, cfg):
         assert calc_diff(d[i].cpu(), og.gemm_nt(a_deq[i], b_deq[i])) < THRESH
 
 
-@pytest.mark.parametrize('cfg', ['4,1,4', '4,2,4,2'])
+@pytest.mark.parametrize('cfg', ['4,1,4', '4,2,4,2', '4,4,4,5,1'])
 def test_rows_epilogues_bit_exact(rows, cfg):
     """Stochastic rounding: bit-exact against the hash of the same plan's fp32 output; FP8 output:
     bit-exact against quantising its bf16 output per (row, 32 columns)."""
@@ -137,7 +139,7 @@ def test_rows_epilogues_bit_exact(rows, cfg):
 
 
 @pytest.mark.parametrize('m,n,k', [(128, 2112, 7168), (128, 4096, 7168), (128, 7168, 2048), (65, 4096, 1024),
-                                   (100, 300, 7168), (128, 24576, 1536)])
+                                   (100, 300, 7168), (128, 24576, 1536), (96, 3072, 7168), (128, 7168, 7168)])
 def test_rows_default_plan_vs_tile_kernel(monkeypatch, m, n, k):
     """The heuristic's decode plans for 64 < M <= 128 agree with the tile kernel (DG_SKINNY=0) and
     with the oracle; the BASELINE decode shapes take the shared-ring kernel."""
@@ -148,7 +150,9 @@ def test_rows_default_plan_vs_tile_kernel(monkeypatch, m, n, k):
     args = ((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()))
     if n <= 8192:
         info = deep_gemm.launch_plan(m, n, k)
-        assert info['skinny'] == 2 and info['threads'] == 256 and info['block_n'] == 32, info
+        wide = k > 4096 and n >= 3072   # 64-column strips, partials summed by the second launch
+        assert info['skinny'] == 2 and info['block_n'] == (64 if wide else 32), info
+        assert info['split_reduce'] == int(wide) and (info['split_k'] > 1 or not wide), info
     d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
     deep_gemm.fp8_gemm_nt(*args, d, recipe_a=(1, 128), recipe_b=(128, 128))
     monkeypatch.setenv('DG_SKINNY', '0')
@@ -159,7 +163,7 @@ def test_rows_default_plan_vs_tile_kernel(monkeypatch, m, n, k):
     assert calc_diff(d.cpu(), d0.cpu()) < 1e-6
 
 
-@pytest.mark.parametrize('cfg', ['4,1,4', '2,1,4', '4,2,4,2'])
+@pytest.mark.parametrize('cfg', ['4,1,4', '2,1,4', '4,2,4,2', '4,4,4,3,1'])
 @pytest.mark.parametrize('max_m,n,k', [(128, 384, 1024), (64, 300, 1040)])
 def test_rows_masked(monkeypatch, cfg, max_m, n, k):
     """M-grouped masked launches on forced configurations: valid rows match the oracle, rows past
@@ -221,3 +225,30 @@ def test_rows_split_back_to_back_bit_exact(monkeypatch):
     torch.cuda.synchronize()
     for o in outs:
         assert torch.equal(o.view(torch.int16), d0.view(torch.int16))
+
+
+@pytest.mark.parametrize('cfg', ['4,1,4,3', '4,2,4,6', '4,4,4,9', '2,4,4,4'])
+@pytest.mark.parametrize('out', [torch.float32, torch.bfloat16])
+def test_rows_split_reduce_launch_bit_exact(monkeypatch, cfg, out):
+    """The second-launch reduction (split_reduce_kernel) sums the same partials in the same split
+    order as the first launch's last-arriving workgroup: bit-identical D, fp32 and bf16, on a
+    ragged N and a K that ends inside a 64-K block; launch_plan reports which path runs."""
+    mt = int(cfg.split(',')[0])
+    m, n, k = 32 * mt - 5, 1000, 7000
+    print(f'rows split reduce {cfg} m={m} n={n} k={k} {out}', flush=True)
+    g = gen(70)
+    a, sfa, a_deq = operand(m, k, 'e4m3', (1, 128), g, 'randn')
+    b, sfb, b_deq = operand(n, k, 'e4m3', (128, 128), g, 'randn')
+    args = ((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()))
+    res = {}
+    for reduce in (0, 1):
+        monkeypatch.setenv('DG_SKINNY_ROWS', f'{cfg},{reduce}')
+        info = deep_gemm.launch_plan(m, n, k)
+        assert info['split_k'] == int(cfg.split(',')[3]) and info['split_reduce'] == reduce, info
+        d = torch.empty(m, n, dtype=out, device='cuda')
+        deep_gemm.fp8_gemm_nt(*args, d, recipe_a=(1, 128), recipe_b=(128, 128))
+        torch.cuda.synchronize()
+        res[reduce] = d.cpu()
+    bits = torch.int32 if out == torch.float32 else torch.int16
+    assert torch.equal(res[0].view(bits), res[1].view(bits))
+    assert calc_diff(res[1], og.gemm_nt(a_deq, b_deq, out)) < THRESH
