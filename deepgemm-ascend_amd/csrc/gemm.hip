@@ -194,7 +194,8 @@ struct SkinnyEnv {
     int mode;   // -1 default, 0 off, 1 forced configuration
     int mt, nb, nw, d, ar, split;
     int rows, rmt, rnb, rd, rsplit;   // DG_SKINNY_ROWS: -1 default, 0 off, 1 forced "mt,nb,d[,split[,reduce]]"
-    int rreduce;                      // (-1: the plan's choice, 0: last-arriving workgroup, 1: second launch)
+    int rreduce;                      // (-1: the plan's choice, 0: last-arriving workgroup, 1: second launch,
+                                      //  2: second launch from three K ranges on)
 };
 SkinnyEnv skinny_env() {
     SkinnyEnv e = {-1, 0, 0, 0, 0, 0, 0, -1, 0, 0, 0, 0, -1};
@@ -222,12 +223,13 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
     if (env.mode == 0 || !(a.gemm_type == kNormal || a.gemm_type == kBatched || a.gemm_type == kMasked)) return false;
     const int groups0 = a.gemm_type == kNormal ? 1 : a.num_groups;
     // FP8 decode shapes with 64 < M <= 128 and K <= 8192 (dense or batched) take the shared-ring kernel:
-    // its waves own the tile's four 32-row blocks and fetch each group of B and A once per
-    // workgroup, four groups deep.  Measured on MI355X (fp8, cold L2, event us, skinny kernel in
+    // its waves own the tile's 32x32 blocks and fetch each group of B and A once per workgroup, four
+    // groups deep.  Measured on MI355X with 128 x 32 strips (fp8, cold L2, event us, skinny kernel in
     // brackets): 128x2112x7168 21.9 (24.8), 128x4096x7168 26.8 (30.0), 128x7168x2048 15.0 (17.0),
     // 96x4096x7168 24.5 (27.6); slower at K = 16384 (87.5 vs 74.5) and for M <= 64 (64x2112x7168
     // 18.6 vs 17.4), which keep the skinny kernel, as do bf16 and FP4-B operands (no gain measured:
-    // bf16 128x4096x7168 29.9 vs 29.0 kernel us).
+    // bf16 128x4096x7168 29.9 vs 29.0 kernel us).  The tile shapes below (128 x 64, 64 x 64) replaced
+    // the 128 x 32 strips.
     SkinnyEnv rows_env = env;
     if (env.rows == -1 && env.mode == -1 && a.kind == kFP8FP8 && a.m > 64 && a.m <= 128 && a.k <= 8192 &&
         (a.gemm_type == kNormal || a.gemm_type == kBatched) && (int64_t)ceil_div(a.n, 32) * groups0 <= 2 * (int64_t)cus) {
@@ -245,14 +247,25 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
             rows_env.rnb = 2;
             rows_env.rsplit = (int)std::max<int64_t>(2, std::min<int64_t>(4, cus / strips2));
             rows_env.rreduce = 1;
+        } else if (a.m > 80) {
+            // Otherwise 64 x 64 tiles (M in two 64-row blocks): at the same number of workgroups each moves
+            // ~20 % fewer bytes of A and B than a 128 x 32 strip.  K split as below, the partials summed by
+            // the second launch from three ranges on.  Measured on MI355X (event us, cold L2, 128 x 32
+            // strips in brackets): 128x2112x7168 19.3 (20.7, split 3), 128x7168x2048 13.4 (14.3),
+            // 128x7168x4096 20.0 (21.3), 128x4096x4096 19.2 (20.0), 96x2112x7168 19.1 (20.0); behind
+            // where the second block holds few rows (65x4096x1024 13.3 vs 12.5: B read twice for one row).
+            rows_env.rmt = 2; rows_env.rnb = 2;
+            rows_env.rreduce = 2;   // (second launch when the plan splits K three ways or more)
         }
     }
-    if (rows_env.rows == 1 && a.m <= 32 * rows_env.rmt &&
+    // (dense and batched launches may hold M in several tiles of 32 mt rows, M <= 128)
+    const bool rows_mblocks = (a.gemm_type == kNormal || a.gemm_type == kBatched) && a.m <= 128;
+    if (rows_env.rows == 1 && (a.m <= 32 * rows_env.rmt || rows_mblocks) &&
         lookup_skinny_rows(a.kind, rows_env.rmt, rows_env.rnb, rows_env.rd, kEpiBf16) != nullptr) {
         const SkinnyEnv& env = rows_env;
-        // shared-ring decode kernel: K split across workgroups while the strips leave CUs idle,
+        // shared-ring decode kernel: K split across workgroups while the tiles leave CUs idle,
         // each range keeping at least eight 64-K blocks
-        const int64_t strips = (int64_t)ceil_div(a.n, 32 * env.rnb) * groups0;
+        const int64_t strips = (int64_t)ceil_div(a.n, 32 * env.rnb) * ceil_div(a.m, 32 * env.rmt) * groups0;
         const int nk64 = std::max(1, ceil_div(a.k, 64));
         int sp = 1;
         if (allow_split && strips <= kMaxSplitTiles) {
@@ -262,7 +275,7 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
         const int ss = ceil_div(nk64, sp);
         out = {{32 * env.rmt, 32 * env.rnb, 0, env.rmt * env.rnb, 0, 0, 0, 0, 0}, ceil_div(nk64, ss), ss,
                env.rmt * env.rnb, env.rd, 32 * env.rmt, 1, 0, 0};
-        out.split_reduce = out.split > 1 && env.rreduce == 1 ? 1 : 0;
+        out.split_reduce = (out.split > 1 && env.rreduce == 1) || (out.split > 2 && env.rreduce == 2) ? 1 : 0;
         return true;
     }
     int mt = a.m <= 32 ? 1 : (a.m <= 64 ? 2 : 4), nb = 1, nw = 4, d = 2, ar = a.m <= 16 ? 16 : 32 * mt;

@@ -430,8 +430,9 @@ __device__ __forceinline__ void skinny_body(const KParams& p, const int vb) {
 
 namespace dg {
 
-// Decode kernel with one shared ring (M <= 32 MT).  The tile is 32 MT x 32 NB like skinny_kernel's,
-// but its NW = MT x NB waves split the tile instead of K: wave w owns the 32x32 output block
+// Decode kernel with one shared ring.  The tile is 32 MT x 32 NB like skinny_kernel's (a dense or
+// batched M above 32 MT takes several tiles per strip), but its NW = MT x NB waves split the tile
+// instead of K: wave w owns the 32x32 output block
 // (w % MT, w / MT) over the workgroup's whole K range.  All waves walk the same groups of G 64-K
 // blocks through one ring of D group slots (B rows of the strip, all 32 MT rows of A, and the
 // packed scale rows of both) that they fill together, so every byte is fetched once per
@@ -495,19 +496,23 @@ __device__ __forceinline__ void skinny_rows_body(const KParams& p, const int vb)
         t = vb;
     }
     const int tile_id = t;
-    const int nn = p.num_n_blocks;
+    // tile = (batch, strip, M block): the M blocks of a strip are consecutive tiles (dense and
+    // batched launches whose M exceeds the BM rows of one tile; masked launches have one)
+    const int nn = p.num_n_blocks, nmb = p.num_m_blocks;
     int batch = 0;
     if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
-        batch = t / nn;
-        t -= batch * nn;
+        batch = t / (nn * nmb);
+        t -= batch * (nn * nmb);
     }
+    const int m0 = (t % nmb) * BM;
+    t /= nmb;
     const int n0 = t * BN;
     const int N = p.n;
     const int M = __builtin_amdgcn_readfirstlane(p.gemm_type == kMasked ? min(p.m, p.layout[batch]) : p.m);
-    if (M <= 0) return;
-    const uint8_t* a_base = p.a;
+    if (M <= m0) return;
+    const uint8_t* a_base = p.a + (int64_t)m0 * p.lda;
     const uint8_t* b_base = p.b + (int64_t)n0 * p.ldb;
-    const uint16_t* sfa = p.sfa;
+    const uint16_t* sfa = p.sfa + m0;
     const uint16_t* sfb = p.sfb;
     uint8_t* d_base = p.d;
     if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
@@ -519,7 +524,7 @@ __device__ __forceinline__ void skinny_rows_body(const KParams& p, const int vb)
             sfb += (int64_t)batch * p.sfb_bs;
         }
     }
-    const int rows_a = min(BM, M), rows_b = min(BN, N - n0);
+    const int rows_a = min(BM, M - m0), rows_b = min(BN, N - n0);
     const int nk64 = ceil_div(p.k, 64);
     const int kb0 = split * p.split_stages;
     const int kb1 = split_k > 1 ? min(nk64, kb0 + p.split_stages) : nk64;
@@ -564,7 +569,7 @@ __device__ __forceinline__ void skinny_rows_body(const KParams& p, const int vb)
             const int s = w + j * NW;
             const bool is_a = s < G;
             sc_base[j] = is_a ? sfa : sfb + n0;
-            sc_size[j] = is_a ? (int64_t)nk64 * p.sfa_ld * 2 : ((int64_t)nk64 * p.sfb_ld - n0) * 2;
+            sc_size[j] = is_a ? ((int64_t)nk64 * p.sfa_ld - m0) * 2 : ((int64_t)nk64 * p.sfb_ld - n0) * 2;
             sc_step[j] = (int)(is_a ? p.sfa_ld : p.sfb_ld) * 2;
             sc_blk[j] = is_a ? s : s - G;
             sc_v[j] = s < NSF && 2 * lane < (is_a ? rows_a : rows_b) ? (uint32_t)(lane * 4) : kOOBOffset;
@@ -660,7 +665,7 @@ __device__ __forceinline__ void skinny_rows_body(const KParams& p, const int vb)
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    const int m = wjm * 32 + r;
+    const int m = m0 + wjm * 32 + r;
     // ------------------------------------------------------------------ split-K across workgroups
     if (split_k > 1) {
         constexpr int NBLK = NW;
@@ -741,16 +746,19 @@ __device__ __forceinline__ void split_reduce_body(const KParams& p, const int vb
     if (tile_id >= p.num_tiles) return;
     const int wjm = blk % MT, wjn = blk / MT;
     const int r = lane & 31, q = lane >> 5;
+    const int nn = p.num_n_blocks, nmb = p.num_m_blocks;
     int t = tile_id, batch = 0;
     if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
-        batch = t / p.num_n_blocks;
-        t -= batch * p.num_n_blocks;
+        batch = t / (nn * nmb);
+        t -= batch * (nn * nmb);
     }
+    const int m0 = (t % nmb) * MT * 32;
+    t /= nmb;
     const int M = __builtin_amdgcn_readfirstlane(p.gemm_type == kMasked ? min(p.m, p.layout[batch]) : p.m);
-    if (M <= 0) return;
+    if (M <= m0) return;
     uint8_t* d_base = p.d;
     if (p.gemm_type == kBatched || p.gemm_type == kMasked) d_base += (int64_t)batch * p.bsd * p.out_esize;
-    const int m = wjm * 32 + r;
+    const int m = m0 + wjm * 32 + r;
     const int split_k = p.split_k;
     const float* const tile_ws = p.ws + (int64_t)tile_id * split_k * (NBLK * 1024);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(tile_ws, (int64_t)split_k * NBLK * 1024 * 4);

@@ -135,7 +135,7 @@ def test_launch_plan_without_device(lib):
     # decode shapes with 64 < M <= 128 and K <= 8192 take the shared-ring decode kernel
     mid = _lib.LaunchInfo()
     assert lib.dg_launch_plan(_plan_args(128, 2112, 7168, 0), ctypes.byref(mid)) == 0, lib.dg_last_error()
-    assert mid.skinny == 2 and mid.threads == 256 and mid.block_m == 128 and mid.block_n == 32
+    assert mid.skinny == 2 and mid.threads == 256 and mid.block_m == 64 and mid.block_n == 64
     assert mid.split_reduce == 0
     # long K over many columns: 64-column strips, the split-K partials summed by a second launch
     # (only where the call can split K: here with the library's per-stream workspace)

@@ -18,12 +18,14 @@ pytestmark = pytest.mark.gpu
 THRESH = 1e-5
 # the kSkinnyRows menu of csrc/gemm_tiles.hpp, plus forced K splits
 CONFIGS = ['4,1,3', '4,1,4', '4,1,5', '4,2,4', '4,4,4', '2,1,4', '2,2,4', '2,4,4', '4,1,4,3', '2,2,4,5',
-           '4,1,4,3,1', '4,2,4,6,1', '4,4,4,9,1', '2,4,4,4,1']
+           '4,1,4,3,1', '4,2,4,6,1', '4,4,4,9,1', '2,4,4,4,1', '2,2,4,3,1']
 
 
 def _ms(cfg):
+    """M values for a configuration: one tile's rows and, below 128 rows a tile, M held in several
+    tiles per strip (a ragged last one included)."""
     rows = 32 * int(cfg.split(',')[0])
-    return sorted({1, rows - 3, rows})
+    return sorted({1, rows - 3, rows} | ({rows + 37, 128} if rows < 128 else set()))
 
 
 @pytest.fixture
@@ -151,8 +153,11 @@ def test_rows_default_plan_vs_tile_kernel(monkeypatch, m, n, k):
     if n <= 8192:
         info = deep_gemm.launch_plan(m, n, k)
         wide = k > 4096 and n >= 3072   # 64-column strips, partials summed by the second launch
-        assert info['skinny'] == 2 and info['block_n'] == (64 if wide else 32), info
-        assert info['split_reduce'] == int(wide) and (info['split_k'] > 1 or not wide), info
+        # (64 x 64 tiles from M = 81 on, else 128-row strips: 128 x 64 where wide, 128 x 32 otherwise)
+        bm, bn = (128, 64) if wide else (64, 64) if m > 80 else (128, 32)
+        assert info['skinny'] == 2 and (info['block_m'], info['block_n']) == (bm, bn), info
+        assert info['split_reduce'] == int(wide or (m > 80 and info['split_k'] > 2)), info
+        assert info['split_k'] > 1 or not wide, info
     d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
     deep_gemm.fp8_gemm_nt(*args, d, recipe_a=(1, 128), recipe_b=(128, 128))
     monkeypatch.setenv('DG_SKINNY', '0')
