@@ -227,11 +227,14 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
     // groups deep.  Measured on MI355X with 128 x 32 strips (fp8, cold L2, event us, skinny kernel in
     // brackets): 128x2112x7168 21.9 (24.8), 128x4096x7168 26.8 (30.0), 128x7168x2048 15.0 (17.0),
     // 96x4096x7168 24.5 (27.6); slower at K = 16384 (87.5 vs 74.5) and for M <= 64 (64x2112x7168
-    // 18.6 vs 17.4), which keep the skinny kernel, as do bf16 and FP4-B operands (no gain measured:
-    // bf16 128x4096x7168 29.9 vs 29.0 kernel us).  The tile shapes below (128 x 64, 64 x 64) replaced
-    // the 128 x 32 strips.
+    // 18.6 vs 17.4), which keep the skinny kernel.  The tile shapes below (128 x 64, 64 x 64) replaced
+    // the 128 x 32 strips; with them bf16 and FP8 x FP4 (e2m1 B) decode shapes gain too (cold event us,
+    // skinny kernel in brackets): FP8 x FP4 128x7168x2048 12.5 (14.0), 128x4096x7168 21.8 (24.4),
+    // 128x2112x7168 18.3 (21.4); bf16 128x7168x2048 17.5 (18.5), 128x4096x7168 28.2 (32.6),
+    // 128x2112x7168 24.0 (26.2).  (With 128 x 32 strips they had not: bf16 128x4096x7168 29.9 vs 29.0.)
     SkinnyEnv rows_env = env;
-    if (env.rows == -1 && env.mode == -1 && a.kind == kFP8FP8 && a.m > 64 && a.m <= 128 && a.k <= 8192 &&
+    const bool rows_kind = a.kind == kFP8FP8 || a.kind == kFP8FP4 || a.kind == kBF16;
+    if (env.rows == -1 && env.mode == -1 && rows_kind && a.m > 64 && a.m <= 128 && a.k <= 8192 &&
         (a.gemm_type == kNormal || a.gemm_type == kBatched) && (int64_t)ceil_div(a.n, 32) * groups0 <= 2 * (int64_t)cus) {
         rows_env.rows = 1;
         rows_env.rmt = 4; rows_env.rnb = 1; rows_env.rd = 4; rows_env.rsplit = 0;
@@ -256,6 +259,14 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
             // where the second block holds few rows (65x4096x1024 13.3 vs 12.5: B read twice for one row).
             rows_env.rmt = 2; rows_env.rnb = 2;
             rows_env.rreduce = 2;   // (second launch when the plan splits K three ways or more)
+            // bf16 rows of 8 KB and more in an unsplit plan stay on the skinny kernel (128x7168x4096
+            // 37.1 vs 29.1 us; split or shorter rows gain: 128x4096x4096 23.2 vs 24.2, 128x7168x3072
+            // 23.0 vs 24.9, 128x2112x7168 24.0 vs 26.2)
+            const int64_t tiles64 = (int64_t)ceil_div(a.n, 64) * 2 * groups0;
+            const bool unsplit = !allow_split || cus / tiles64 <= 1 || ceil_div(a.k, 64) < 16;
+            if (a.kind == kBF16 && unsplit && a.k >= 4096) rows_env.rows = -1;
+        } else if (a.kind != kFP8FP8) {
+            rows_env.rows = -1;   // (128 x 32 strips measured no gain over the skinny kernel for these kinds)
         }
     }
     // (dense and batched launches may hold M in several tiles of 32 mt rows, M <= 128)

@@ -257,3 +257,32 @@ def test_rows_split_reduce_launch_bit_exact(monkeypatch, cfg, out):
     bits = torch.int32 if out == torch.float32 else torch.int16
     assert torch.equal(res[0].view(bits), res[1].view(bits))
     assert calc_diff(res[1], og.gemm_nt(a_deq, b_deq, out)) < THRESH
+
+
+@pytest.mark.parametrize('kind', ['bf16', 'fp4'])
+@pytest.mark.parametrize('m,n,k', [(128, 2112, 7168), (128, 4096, 7168), (128, 7168, 2048), (96, 7168, 4096), (72, 1000, 2048)])
+def test_rows_default_plan_bf16_fp4(monkeypatch, kind, m, n, k):
+    """bf16 and FP8 x FP4 decode shapes on their default plans (the shared-ring kernel where it measured
+    ahead, the skinny kernel elsewhere) agree with the oracle and with the tile kernel."""
+    g = gen(73)
+    if kind == 'bf16':
+        a = (torch.randn(m, k, generator=g) * 0.1).bfloat16()
+        b = (torch.randn(n, k, generator=g) * 0.1).bfloat16()
+        ref = og.gemm_nt(a.float(), b.float())
+        call = lambda d: deep_gemm.bf16_gemm_nt(a.cuda(), b.cuda(), d)
+        info = deep_gemm.launch_plan(m, n, k, kind=deep_gemm._lib.DG_KIND_BF16)
+    else:
+        a, sfa, a_deq = operand(m, k, 'e4m3', (1, 32), g, 'randn')
+        b, sfb, b_deq = operand(n, k, 'e2m1', (1, 32), g)
+        ref = og.gemm_nt(a_deq, b_deq)
+        call = lambda d: deep_gemm.fp8_fp4_gemm_nt((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d)
+        info = deep_gemm.launch_plan(m, n, k, kind=deep_gemm._lib.DG_KIND_FP8_FP4)
+    print(f'rows default {kind} m={m} n={n} k={k} plan={info}', flush=True)
+    d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
+    call(d)
+    monkeypatch.setenv('DG_SKINNY', '0')
+    d0 = torch.empty_like(d)
+    call(d0)
+    torch.cuda.synchronize()
+    assert calc_diff(d.cpu(), ref) < THRESH
+    assert calc_diff(d.cpu(), d0.cpu()) < 1e-6
