@@ -40,7 +40,7 @@ def parse():
     ap.add_argument('--n', type=int, default=N)
     ap.add_argument('--k', type=int, default=K)
     ap.add_argument('--suite', default=None,
-                    help='comma list of dense,decode,bf16,fp4,grouped,kgrouped,einsum,host: one JSON line per shape '
+                    help='comma list of dense,decode,bf16,fp4,grouped,kgrouped,einsum,host,ref: one JSON line per shape '
                          '(cold-L2 kernel times) instead of the north-star line')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a 256 MiB device copy (reference kernel for FETCH_SIZE / WRITE_SIZE scaling)')
@@ -313,6 +313,37 @@ def run_suite(groups):
                 us = _time_cold(lambda: deep_gemm.fp8_fp4_gemm_nt((a, sfa), (b, sfb), d))
                 _line('fp4', f'fp8_fp4_gemm_nt {m}x{n}x{k}', us, 2.0 * m * n * k,
                       m * k + n * k // 2 + 2 * m * n + (m + n) * (k // 64) * 2)
+    if 'ref' in groups:
+        # the reference's other published FP8 x FP4 shapes (its MX recipe: 1x32 UE8M0 scales on both
+        # operands, e2m1 B packed two per byte): dense 4096x7168x16384, and M-grouped contiguous with 8
+        # groups of 4096 rows at N=4096 K=2048 and N=7168 K=3072
+        def fp4_b(rows, k, batch=None):
+            shape = ((batch,) if batch else ()) + (rows, k // 2)
+            sf = _gpu_sf(((batch,) if batch else ()) + (rows, k // 32), dev, gen, 125, 128)
+            return torch.randint(-128, 128, shape, dtype=torch.int8, device=dev, generator=gen), sf
+        m, n, k = 4096, 7168, 16384
+        a = _gpu_codes((m, k), dev, gen)
+        sfa = deep_gemm.transform_sf_into_required_layout(_gpu_sf((m, k // 32), dev, gen), m, k, (1, 32), is_sfa=True)
+        b, sfb = fp4_b(n, k)
+        sfb = deep_gemm.transform_sf_into_required_layout(sfb, n, k, (1, 32), is_sfa=False)
+        d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        us = _time_cold(lambda: deep_gemm.fp8_fp4_gemm_nt((a, sfa), (b, sfb), d))
+        _line('ref', f'fp8_fp4_gemm_nt {m}x{n}x{k} (1x32 / 1x32)', us, 2.0 * m * n * k,
+              m * k + n * k // 2 + 2 * m * n + (m + n) * (k // 32))
+        g_, rows = 8, 4096
+        deep_gemm.set_mk_alignment_for_contiguous_layout(256)
+        layout = torch.tensor([rows * (i + 1) for i in range(g_)], dtype=torch.int32, device=dev)
+        for n, k in ((4096, 2048), (7168, 3072)):
+            total = g_ * rows
+            a = _gpu_codes((total, k), dev, gen)
+            sfa = deep_gemm.transform_sf_into_required_layout(_gpu_sf((total, k // 32), dev, gen), total, k, (1, 32),
+                                                               is_sfa=True, psum_layout=layout)
+            b, sfb = fp4_b(n, k, batch=g_)
+            sfb = deep_gemm.transform_sf_into_required_layout(sfb, n, k, (1, 32), num_groups=g_, is_sfa=False)
+            d = torch.empty(total, n, dtype=torch.bfloat16, device=dev)
+            us = _time_cold(lambda: deep_gemm.m_grouped_fp8_fp4_gemm_nt_contiguous((a, sfa), (b, sfb), d, layout))
+            _line('ref', f'm_grouped_fp8_fp4_gemm_nt_contiguous G=8 x {rows} rows N={n} K={k} (1x32 / 1x32)', us,
+                  2.0 * total * n * k, total * k + g_ * n * k // 2 + 2 * total * n + (total + g_ * n) * (k // 32))
     if 'grouped' in groups:
         counts = _routed_counts()
         align = 128

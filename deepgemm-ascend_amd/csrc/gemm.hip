@@ -332,7 +332,10 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     // cold us): N=4096 K=7168 345.6 vs 458.7 (128x256), N=7168 K=2048 200.3 vs 237.9; bf16
     // 635.6 vs 839.9 and 330.2 vs 408.5.  With alignment 256 the 256-row tiles are faster (443 vs
     // 526 at N=4096 K=7168).
-    if ((a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) && a.alignment % 256 != 0) {
+    // (e2m1 B: the 384x192 kernel spills 148-192 bytes per lane and ran 2.5x behind the scored plan,
+    // G=32 routed, alignment 128, cold us: N=4096 K=7168 1011 vs 408 on 128x256, N=7168 K=2048 532 vs 216)
+    const bool fp4_b = a.kind == kFP8FP4 || a.kind == kFP4FP4;
+    if ((a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) && a.alignment % 256 != 0 && !fp4_b) {
         for (const TileCfg& tc : kTiles)
             if (tc.bm == 384 && tc.bn == 192) return {tc, 1, ceil_div(a.k, k_stage_elems(a.kind, tc)), 0, 0, 0};
     }
@@ -349,7 +352,10 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     Plan pick = {{0, 0, 0, 0, 0, 0, 0, 0, 0}, 1, 1, 0, 0, 0};
     for (int i = 0; i < kNumTiles; ++i) {
         const TileCfg& tc = kTiles[i];
-        if (!tile_allowed(a, tc.bm, tc.bn)) continue;
+        // (anchored tiles only where the alignment rules out 256-row tiles, above: at alignment 256 they
+        // measured behind, 526 vs 443 us for 256x224 at G=32 N=4096 K=7168, and FP8 x FP4 G=8 x 4096
+        // rows N=7168 K=3072 took 2546 us on 384x192)
+        if (!tile_allowed(a, tc.bm, tc.bn) || tile_anchored(tc.bm)) continue;
         const int ns = ceil_div(k_tile, k_stage_elems(a.kind, tc));
         const int64_t tiles = plan_tiles(a, tc);
         const int max_split = allow_split && tile_splittable(tc) && tiles <= kMaxSplitTiles ? std::min(16, std::max(1, ns / 4)) : 1;

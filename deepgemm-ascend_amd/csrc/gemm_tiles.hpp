@@ -59,11 +59,12 @@ KernelFn pick_epi(int epi) {
     }
 }
 
-// Persistent kernels exist for the 128-K-stage (km = 2, two-slot ring) tiles of up to 256 rows.
+// Persistent kernels exist for the 128-K-stage (km = 2, two-slot ring) tiles of up to 256 rows, except
+// 256x256, whose persistent body does not fit the register file (the planner never takes it).
 template <int I, int KIND>
 KernelFn pick_persistent_epi(int epi) {
     constexpr TileCfg t = kTiles[I];
-    if constexpr (t.km != 2 || t.stages != 2 || t.bm > 256) {
+    if constexpr (t.km != 2 || t.stages != 2 || t.bm > 256 || (t.bm == 256 && t.bn == 256)) {
         return nullptr;
     } else {
         switch (epi) {

@@ -96,6 +96,25 @@ def test_select_config_respects_grouped_alignment(lib):
                 assert align % bm.value == 0 and bn.value > 0
 
 
+def test_fp4_grouped_plans_skip_anchored_tiles(lib):
+    """M-grouped FP8 x FP4 / FP4 x FP4 layouts take scored tiles whose block_m divides the alignment (the
+    384-row anchored kernel spills for e2m1 B), and no layout scores an anchored tile at alignment 256."""
+    for kind in (1, 2):
+        for align in (128, 256):
+            args = _lib.GemmArgs()
+            args.kind, args.gemm_type, args.m, args.n, args.k, args.num_groups = kind, 2, 8192, 4096, 7168, 32
+            args.alignment, args.num_cus = align, 256
+            bm, bn = ctypes.c_int32(), ctypes.c_int32()
+            assert lib.dg_select_config(ctypes.byref(args), ctypes.byref(bm), ctypes.byref(bn)) == 0
+            assert bm.value <= 256 and align % bm.value == 0, (kind, align, bm.value, bn.value)
+    args = _lib.GemmArgs()
+    args.kind, args.gemm_type, args.m, args.n, args.k, args.num_groups = 0, 2, 32768, 7168, 3072, 8
+    args.alignment, args.num_cus = 256, 256
+    bm, bn = ctypes.c_int32(), ctypes.c_int32()
+    assert lib.dg_select_config(ctypes.byref(args), ctypes.byref(bm), ctypes.byref(bn)) == 0
+    assert bm.value <= 256, (bm.value, bn.value)
+
+
 def test_transform_sf_argument_checks(lib):
     f = lib.dg_transform_sf
     # gran_mn not a power of two
