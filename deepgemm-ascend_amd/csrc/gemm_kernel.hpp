@@ -628,7 +628,12 @@ __device__ __forceinline__ void gemm_body(const KParams& p, const int vb, const 
     auto a_slot = [&](int s) -> uint8_t* { return smem + s * STAGE_A; };
     auto b_slot = [&](int sb) -> uint8_t* { return kSplitRing ? smem + RING_A + sb * B_BYTES : smem + sb * STAGE + A_BYTES; };
 
-    const int tid = threadIdx.x;
+    int tid = threadIdx.x;
+    // In the persistent walk (known_total >= 0) the thread index is made opaque on every tile, so the
+    // per-lane load and fragment offsets derived from it are recomputed per tile instead of being hoisted
+    // out of the walk and held live across the main loop (they spilled the 384-row walk, ~290 bytes per
+    // lane).  A one-tile launch passes -1 and keeps its code as it was.
+    if (known_total >= 0) asm volatile("" : "+v"(tid));
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lwave = wave - FW, ltid = tid - FW * 64;   // loader wave / thread index
