@@ -23,7 +23,7 @@ def _dense_case(m, n, k, seed):
 
 
 @pytest.mark.parametrize('m,n,k', [(1, 2112, 7168), (1, 2112, 2048), (16, 7168, 2048), (128, 4096, 7168),
-                                   (4096, 2112, 1024)])
+                                   (128, 2112, 7168), (4096, 2112, 1024)])
 def test_graph_replay_dense(m, n, k):
     print(f'graph dense m={m} n={n} k={k}', flush=True)
     a, b = _dense_case(m, n, k, seed=m + n)
