@@ -851,7 +851,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
             // the layout's run table: for dg_gemm_noalloc in its scratch past the split-K tile
             // counters (those must stay zero for the next split-K call; an anchored plan splits no
             // K, so the partial-tile area is free), else in the library's per-stream buffer
-            const int64_t need = (1 + 2 * (int64_t)ceil_div(a.m, p.alignment)) * 4;
+            const int64_t need = (1 + 3 * (int64_t)ceil_div(a.m, p.alignment)) * 4;
             void* runs = nullptr;
             if (noalloc) {
                 if (kCounterBytes + need > a.workspace_bytes)

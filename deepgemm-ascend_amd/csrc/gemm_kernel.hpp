@@ -275,10 +275,10 @@ __device__ __forceinline__ Segment segment_at(const int* psum, int alignment, co
                                               int m_total) {
     Segment sg;
     if (runs != nullptr) {
-        sg.start = runs[1 + 2 * e];
-        sg.end = e + 1 < count ? runs[3 + 2 * e] : m_total;
-        sg.valid = sg.end;
-        sg.group = runs[2 + 2 * e];
+        sg.start = runs[1 + 3 * e];
+        sg.end = e + 1 < count ? runs[4 + 3 * e] : m_total;
+        sg.valid = runs[3 + 3 * e];
+        sg.group = runs[2 + 3 * e];
     } else {
         sg.start = e == 0 ? 0 : align_up(psum[e - 1], alignment);
         sg.end = align_up(psum[e], alignment);

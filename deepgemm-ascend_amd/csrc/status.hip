@@ -83,10 +83,12 @@ int check_m_indices(const int32_t* idx, int m, int alignment, int num_groups, hi
 }
 
 // Runs of an m_indices layout: maximal sequences of `alignment`-row blocks whose first rows carry
-// the same group id (-1: padding).  Output: runs[0] = the number of runs, then (first row, group)
-// per run; a run ends where the next begins (the last at m).  One workgroup: each thread takes a
-// contiguous span of blocks, counts the runs starting there, and a workgroup prefix sum places
-// them.
+// the same group id (-1: padding).  Output: runs[0] = the number of runs, then (first row, group,
+// valid end) per run; a run ends where the next begins (the last at m), and its valid end is one past
+// the last row of its final block that carries the run's group (the padding rows after it are neither
+// loaded nor multiplied by the anchored tiles; rows before it keep their per-row id check).  One
+// workgroup: each thread takes a contiguous span of blocks, counts the runs starting there, and a
+// workgroup prefix sum places them.
 constexpr int kRunThreads = 1024;
 __global__ __launch_bounds__(kRunThreads) void m_indices_runs_kernel(const int32_t* idx, int m, int alignment,
                                                                     int32_t* runs) {
@@ -110,9 +112,15 @@ __global__ __launch_bounds__(kRunThreads) void m_indices_runs_kernel(const int32
     for (int b = b0; b < b1; ++b) {
         const int g = idx[(int64_t)b * alignment];
         if (b == 0 || g != idx[(int64_t)(b - 1) * alignment]) {
-            runs[1 + 2 * r] = b * alignment;
-            runs[2 + 2 * r] = g;
+            runs[1 + 3 * r] = b * alignment;
+            runs[2 + 3 * r] = g;
             ++r;
+        }
+        // the run's final block (the next block starts another run, or there is none): its valid end
+        if (b + 1 == nblk || idx[(int64_t)(b + 1) * alignment] != g) {
+            int e = min(m, (b + 1) * alignment);
+            while (e > b * alignment + 1 && idx[e - 1] != g) --e;
+            runs[3 * r] = e;   // (run r - 1, the one this block belongs to)
         }
     }
     if (tid == kRunThreads - 1) runs[0] = counts[tid];
