@@ -1286,7 +1286,9 @@ __device__ __forceinline__ void gemm_body(const KParams& p, const int vb, const 
         const bool row_ok = m < tile_end && !(gemm_type == kMasked && m >= valid_end);
         bool pad_row = false;
         if (gemm_type == kMGroupedPsum) pad_row = m >= valid_end;
-        else if (gemm_type == kMGroupedIdx) pad_row = row_ok && p.layout[m] != group;
+        // (an anchored m_indices tile knows its run's valid end: the checked layout holds one group on a
+        // prefix of each alignment block, so no row id needs reading)
+        else if (gemm_type == kMGroupedIdx) pad_row = anchored ? m >= valid_end : row_ok && p.layout[m] != group;
         if constexpr (EPI == kEpiF32 || EPI == kEpiBf16) {
             if (p.accumulate) {
                 // the old D of this row of blocks in one burst, then the blocks
