@@ -286,3 +286,19 @@ def test_rows_default_plan_bf16_fp4(monkeypatch, kind, m, n, k):
     torch.cuda.synchronize()
     assert calc_diff(d.cpu(), ref) < THRESH
     assert calc_diff(d.cpu(), d0.cpu()) < 1e-6
+
+
+@pytest.mark.parametrize('m,n,k', [(100, 2112, 2048), (128, 4096, 7168), (97, 3000, 5000)])
+def test_rows_default_plan_bmm(m, n, k):
+    """Batched launches on the default decode plans (64 x 64 tiles with M in two row blocks, or the 128 x 64
+    two-launch plan): every batch against the oracle."""
+    bs = 3
+    print(f'rows default bmm bs={bs} m={m} n={n} k={k}', flush=True)
+    g = gen(74)
+    a, sfa, a_deq = operand(m, k, 'e4m3', (1, 32), g, 'randn', batch=bs)
+    b, sfb, b_deq = operand(n, k, 'e4m3', (1, 32), g, 'randn', batch=bs)
+    d = torch.empty(bs, m, n, dtype=torch.bfloat16, device='cuda')
+    deep_gemm.fp8_bmm((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d)
+    torch.cuda.synchronize()
+    for i in range(bs):
+        assert calc_diff(d[i].cpu(), og.gemm_nt(a_deq[i], b_deq[i])) < THRESH, i
