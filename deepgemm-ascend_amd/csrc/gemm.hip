@@ -132,9 +132,18 @@ constexpr int64_t kCounterBytes = 64 * 1024;
 constexpr int kXcds = 8;   // MI355X: 8 XCDs, workgroup b dispatched to XCD b % 8
 constexpr int64_t kMaxSplitTiles = kCounterBytes / 4;
 
+// Tiles of a shared-ring decode plan as its kernels number them: with M in several row blocks the strips
+// are padded to whole groups of eight, so that the row blocks of a strip (tile ids eight apart) share an
+// XCD and its L2 holds the strip's B rows once.
+int64_t rows_tiles(const dg_gemm_args& a, const TileCfg& t) {
+    const int groups = a.gemm_type == kBatched || a.gemm_type == kMasked ? a.num_groups : 1;
+    const int64_t nmb = ceil_div(a.m, t.bm), nn = ceil_div(a.n, t.bn);
+    return (nmb > 1 ? nmb * align_up64(nn, 8) : nn) * groups;
+}
+
 int64_t plan_workspace(const dg_gemm_args& a, const Plan& pl) {
     if (pl.split <= 1) return 0;
-    const int64_t tiles = plan_tiles(a, pl.tile);
+    const int64_t tiles = pl.skinny_rows ? rows_tiles(a, pl.tile) : plan_tiles(a, pl.tile);
     return kCounterBytes + tiles * pl.split * (int64_t)pl.tile.bm * pl.tile.bn * 4;
 }
 
@@ -759,7 +768,7 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     static const int group_m_env = std::getenv("DG_GROUP_M") ? std::atoi(std::getenv("DG_GROUP_M")) : 0;   // tuning
     p.group_m = group_m_env > 0 ? group_m_env : 4;
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;
-    int64_t tiles = (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
+    int64_t tiles = plan.skinny_rows ? rows_tiles(a, cfg) : (int64_t)p.num_m_blocks * p.num_n_blocks * groups;
     if (tiles <= 0) return DG_OK;
     // split-K grids are padded to whole groups of 8 tiles (one per XCD); persistent grids hold
     // one workgroup per CU (set_num_sms caps them)

@@ -496,16 +496,20 @@ __device__ __forceinline__ void skinny_rows_body(const KParams& p, const int vb)
         t = vb;
     }
     const int tile_id = t;
-    // tile = (batch, strip, M block): the M blocks of a strip are consecutive tiles (dense and
-    // batched launches whose M exceeds the BM rows of one tile; masked launches have one)
+    // tile = (batch, strip, M block).  With M in several row blocks (dense and batched launches whose M
+    // exceeds the BM rows of one tile; masked launches have one) the strips are padded to whole groups of
+    // eight and a strip's row blocks are tile ids eight apart, on one XCD, so its L2 fetches the strip's B
+    // rows once; tiles of padding strips exit.
     const int nn = p.num_n_blocks, nmb = p.num_m_blocks;
+    const int nnp = nmb > 1 ? (nn + 7) / 8 * 8 : nn;
     int batch = 0;
     if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
-        batch = t / (nn * nmb);
-        t -= batch * (nn * nmb);
+        batch = t / (nnp * nmb);
+        t -= batch * (nnp * nmb);
     }
-    const int m0 = (t % nmb) * BM;
-    t /= nmb;
+    const int m0 = nmb > 1 ? ((t >> 3) % nmb) * BM : 0;
+    if (nmb > 1) t = (t >> 3) / nmb * 8 + (t & 7);
+    if (t >= nn) return;
     const int n0 = t * BN;
     const int N = p.n;
     const int M = __builtin_amdgcn_readfirstlane(p.gemm_type == kMasked ? min(p.m, p.layout[batch]) : p.m);
@@ -746,14 +750,17 @@ __device__ __forceinline__ void split_reduce_body(const KParams& p, const int vb
     if (tile_id >= p.num_tiles) return;
     const int wjm = blk % MT, wjn = blk / MT;
     const int r = lane & 31, q = lane >> 5;
+    // (the first launch's tile numbering: strips padded to groups of eight when M takes several row blocks)
     const int nn = p.num_n_blocks, nmb = p.num_m_blocks;
+    const int nnp = nmb > 1 ? (nn + 7) / 8 * 8 : nn;
     int t = tile_id, batch = 0;
     if (p.gemm_type == kBatched || p.gemm_type == kMasked) {
-        batch = t / (nn * nmb);
-        t -= batch * (nn * nmb);
+        batch = t / (nnp * nmb);
+        t -= batch * (nnp * nmb);
     }
-    const int m0 = (t % nmb) * MT * 32;
-    t /= nmb;
+    const int m0 = nmb > 1 ? ((t >> 3) % nmb) * MT * 32 : 0;
+    if (nmb > 1) t = (t >> 3) / nmb * 8 + (t & 7);
+    if (t >= nn) return;
     const int M = __builtin_amdgcn_readfirstlane(p.gemm_type == kMasked ? min(p.m, p.layout[batch]) : p.m);
     if (M <= m0) return;
     uint8_t* d_base = p.d;
