@@ -243,7 +243,7 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
     // 128x2112x7168 24.0 (26.2).  (With 128 x 32 strips they had not: bf16 128x4096x7168 29.9 vs 29.0.)
     SkinnyEnv rows_env = env;
     const bool rows_kind = a.kind == kFP8FP8 || a.kind == kFP8FP4 || a.kind == kBF16;
-    if (env.rows == -1 && env.mode == -1 && rows_kind && a.m > 64 && a.m <= 128 && a.k <= 8192 &&
+    if (env.rows == -1 && env.mode == -1 && rows_kind && a.m > 64 && a.m <= 128 && a.k <= 16384 &&
         (a.gemm_type == kNormal || a.gemm_type == kBatched) && (int64_t)ceil_div(a.n, 32) * groups0 <= 2 * (int64_t)cus) {
         rows_env.rows = 1;
         rows_env.rmt = 4; rows_env.rnb = 1; rows_env.rd = 4; rows_env.rsplit = 0;
@@ -255,10 +255,15 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
         // 18.7) and behind for K <= 4096 (128x4096x4096 18.9 vs 18.0, 128x7168x4096 21.3 vs 19.7),
         // where the second launch's fixed cost outweighs the saved A traffic.
         const int64_t strips2 = (int64_t)ceil_div(a.n, 64) * groups0;
+        // (up to K = 16384, cold event us, skinny kernel in brackets: 128x7168x16384 48.5 (55.8), 128x4096x16384
+        // 32.0 (37.4), 128x3072x16384 29.8 (35.7), 128x6144x12288 39.1 (45.8); bf16 128x7168x16384 72.0 (88.8),
+        // 128x4096x16384 47.8 (56.4); FP8 x FP4 43.8 (46.7), 29.5 (33.9))
         if (allow_split && a.k > 4096 && a.n >= 3072 && 2 * strips2 <= cus) {
             rows_env.rnb = 2;
             rows_env.rsplit = (int)std::max<int64_t>(2, std::min<int64_t>(4, cus / strips2));
             rows_env.rreduce = 1;
+        } else if (a.k > 8192) {
+            rows_env.rows = -1;   // (longer K otherwise stays on the skinny kernel)
         } else if (a.m > 80) {
             // Otherwise 64 x 64 tiles (M in two 64-row blocks): at the same number of workgroups each moves
             // ~20 % fewer bytes of A and B than a 128 x 32 strip.  K split as below, the partials summed by

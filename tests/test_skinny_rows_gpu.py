@@ -141,7 +141,8 @@ def test_rows_epilogues_bit_exact(rows, cfg):
 
 
 @pytest.mark.parametrize('m,n,k', [(128, 2112, 7168), (128, 4096, 7168), (128, 7168, 2048), (65, 4096, 1024),
-                                   (100, 300, 7168), (128, 24576, 1536), (96, 3072, 7168), (128, 7168, 7168)])
+                                   (100, 300, 7168), (128, 24576, 1536), (96, 3072, 7168), (128, 7168, 7168),
+                                   (128, 7168, 16384), (96, 3072, 12288)])
 def test_rows_default_plan_vs_tile_kernel(monkeypatch, m, n, k):
     """The heuristic's decode plans for 64 < M <= 128 agree with the tile kernel (DG_SKINNY=0) and
     with the oracle; the BASELINE decode shapes take the shared-ring kernel."""
