@@ -60,6 +60,8 @@ def _dense(m, n, k, seed, b_kind='e4m3'):
     (24, 256, 1024, 4096, '64x128', 4, 'tile 64x128 split 4'),
     (16, 16, 7168, 2048, None, None, 'skinny'),
     (40, 128, 2112, 7168, None, None, 'shared-ring decode'),
+    (100, 128, 1024, 7168, None, None, 'shared-ring two-launch 64x64'),
+    (160, 128, 3072, 7168, None, None, 'shared-ring two-launch 128x64'),
     (20, 1, 2112, 7168, None, None, 'decode GEMV'),
     (12, 1, 4096, 4096, None, 3, 'skinny split 3'),
 ])
@@ -73,6 +75,9 @@ def test_cap_dense_families(cap, n_cus, m, n, k, block, split, kind):
         assert plan['skinny'] == 3
     elif kind == 'shared-ring decode':
         assert plan['skinny'] == 2
+    elif kind.startswith('shared-ring two-launch'):
+        # (the second launch's workgroups go out in chunks of at most n_cus as well)
+        assert plan['skinny'] == 2 and plan['split_reduce'] == 1 and plan['split_k'] >= 3, plan
     elif kind.startswith('skinny'):
         assert plan['skinny'] == 1
     elif block is not None:
