@@ -175,6 +175,27 @@ def test_launch_plan_without_device(lib):
     assert lib.dg_launch_plan(None, None) == -1
 
 
+def test_workspace_size_of_decode_plans(lib):
+    """dg_gemm_workspace_size covers the shared-ring plans' partial tiles as their kernels number them: with M
+    in two 64-row blocks the strips are padded to whole groups of eight (128x2112x7168: 33 strips -> 40, two
+    row blocks, split 3, 64x64 fp32 partials), plus the 64 KiB counter area; the wide 128x64 plan has no row
+    blocks (128x4096x7168: 64 strips, split 4)."""
+    def size(m, n, k):
+        args = _plan_args(m, n, k, 256)
+        nbytes = ctypes.c_int64(0)
+        assert lib.dg_gemm_workspace_size(ctypes.byref(args), ctypes.byref(nbytes)) == 0, lib.dg_last_error()
+        info = _lib.LaunchInfo()
+        args.library_workspace = 1
+        assert lib.dg_launch_plan(args, ctypes.byref(info)) == 0, lib.dg_last_error()
+        return nbytes.value, info
+    ws, info = size(128, 2112, 7168)
+    assert (info.block_m, info.block_n, info.split_k, info.tiles) == (64, 64, 3, 80), (info.block_m, info.block_n, info.split_k, info.tiles)
+    assert ws == 64 * 1024 + 80 * 3 * 64 * 64 * 4
+    ws, info = size(128, 4096, 7168)
+    assert (info.block_m, info.block_n, info.split_k, info.tiles) == (128, 64, 4, 64)
+    assert ws == 64 * 1024 + 64 * 4 * 128 * 64 * 4
+
+
 def test_error_words_and_stream_workspace_without_device(lib):
     # no kernel has run: nothing pending; the workspace query rejects null outputs
     assert lib.dg_take_errors() == 0
