@@ -346,12 +346,13 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
     // cold us): N=4096 K=7168 345.6 vs 458.7 (128x256), N=7168 K=2048 200.3 vs 237.9; bf16
     // 635.6 vs 839.9 and 330.2 vs 408.5.  With alignment 256 the 256-row tiles are faster (443 vs
     // 526 at N=4096 K=7168).
-    // (e2m1 B: the 384x192 kernel spills 148-192 bytes per lane and ran 2.5x behind the scored plan,
-    // G=32 routed, alignment 128, cold us: N=4096 K=7168 1011 vs 408 on 128x256, N=7168 K=2048 532 vs 216)
+    // (e2m1 B takes 384x128: its 384x192 build spills 148-192 bytes per lane and ran 2.5x behind, G=32 routed,
+    // alignment 128, cold us: N=4096 K=7168 1011 vs 370 on 384x128 and 410 on the scored 128x256, N=7168
+    // K=2048 532 vs 217 / 219)
     const bool fp4_b = a.kind == kFP8FP4 || a.kind == kFP4FP4;
-    if ((a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) && a.alignment % 256 != 0 && !fp4_b) {
+    if ((a.gemm_type == kMGroupedPsum || a.gemm_type == kMGroupedIdx) && a.alignment % 256 != 0) {
         for (const TileCfg& tc : kTiles)
-            if (tc.bm == 384 && tc.bn == 192) return {tc, 1, ceil_div(a.k, k_stage_elems(a.kind, tc)), 0, 0, 0};
+            if (tc.bm == 384 && tc.bn == (fp4_b ? 128 : 192)) return {tc, 1, ceil_div(a.k, k_stage_elems(a.kind, tc)), 0, 0, 0};
     }
     allow_split = false;   // wide problems fill the CUs with tiles
     const int groups = (a.gemm_type == kBatched || a.gemm_type == kMasked || a.gemm_type == kKGrouped) ? a.num_groups : 1;

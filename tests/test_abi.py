@@ -97,8 +97,9 @@ def test_select_config_respects_grouped_alignment(lib):
 
 
 def test_fp4_grouped_plans_skip_anchored_tiles(lib):
-    """M-grouped FP8 x FP4 / FP4 x FP4 layouts take scored tiles whose block_m divides the alignment (the
-    384-row anchored kernel spills for e2m1 B), and no layout scores an anchored tile at alignment 256."""
+    """M-grouped FP8 x FP4 / FP4 x FP4 layouts below alignment 256 take the 384x128 anchored tiles (the 384x192
+    build spills for e2m1 B), at alignment 256 scored tiles whose block_m divides it; no layout scores an
+    anchored tile at alignment 256."""
     for kind in (1, 2):
         for align in (128, 256):
             args = _lib.GemmArgs()
@@ -106,7 +107,10 @@ def test_fp4_grouped_plans_skip_anchored_tiles(lib):
             args.alignment, args.num_cus = align, 256
             bm, bn = ctypes.c_int32(), ctypes.c_int32()
             assert lib.dg_select_config(ctypes.byref(args), ctypes.byref(bm), ctypes.byref(bn)) == 0
-            assert bm.value <= 256 and align % bm.value == 0, (kind, align, bm.value, bn.value)
+            if align == 128:
+                assert (bm.value, bn.value) == (384, 128), (kind, align, bm.value, bn.value)
+            else:
+                assert bm.value <= 256 and align % bm.value == 0, (kind, align, bm.value, bn.value)
     args = _lib.GemmArgs()
     args.kind, args.gemm_type, args.m, args.n, args.k, args.num_groups = 0, 2, 32768, 7168, 3072, 8
     args.alignment, args.num_cus = 256, 256

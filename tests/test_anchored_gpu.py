@@ -143,3 +143,42 @@ def test_anchored_m_indices(case):
     ref = og.m_grouped_contiguous(a_deq, b_deq, idx, False, alignment)
     assert calc_diff(out[~pad], ref[~pad]) < THRESH
 
+
+
+@pytest.mark.parametrize('psum', [True, False])
+def test_anchored_m_grouped_fp8_fp4(psum):
+    """FP8 x FP4 (e2m1 B, 1x32 scales) M-grouped layouts below alignment 256 take the 384x128 anchored tiles on
+    their default plan: valid rows match the oracle, padding rows are exact zeros, nothing is written past D."""
+    sizes, alignment = [257, 240, 0, 272, 1, 384, 385, 900], 128
+    total, ps = ol.psum_from_sizes(sizes, alignment)
+    n, k = 448, 1024
+    g = gen(81 + psum)
+    a, sfa, a_deq = operand(total, k, 'e4m3', (1, 32), g)
+    for sl in ol.psum_pad_slices(ps, alignment):
+        a.view(torch.uint8)[sl] = 0
+        a_deq[sl] = 0
+    b, sfb, b_deq = operand(n, k, 'e2m1', (1, 32), g, batch=len(sizes))
+    layout_t = torch.tensor(ps, dtype=torch.int32)
+    idx = ol.m_indices_from_psum(ps, alignment, total)
+    out_full = torch.full((total + 1, n), float('nan'), dtype=torch.bfloat16, device='cuda')
+    d = out_full[:total]
+    old = deep_gemm.get_mk_alignment_for_contiguous_layout()
+    deep_gemm.set_mk_alignment_for_contiguous_layout(alignment)
+    try:
+        plan = deep_gemm.launch_plan(total, n, k, kind=1, gemm_type=2 if psum else 3, num_groups=len(sizes))
+        print(f'anchored fp8xfp4 psum={psum} plan={plan}', flush=True)
+        assert (plan['block_m'], plan['block_n']) == (384, 128), plan
+        deep_gemm.m_grouped_fp8_fp4_gemm_nt_contiguous((a.cuda(), sfa.cuda()), (b.cuda(), sfb.cuda()), d,
+                                                       (layout_t if psum else idx).cuda(), use_psum_layout=psum)
+    finally:
+        deep_gemm.set_mk_alignment_for_contiguous_layout(old)
+    torch.cuda.synchronize()
+    res = out_full.cpu()
+    assert torch.isnan(res[total].float()).all(), 'wrote past D'
+    out = res[:total]
+    valid = torch.zeros(total, dtype=torch.bool)
+    for sl in ol.psum_slices(ps, alignment):
+        valid[sl] = True
+    assert torch.equal(out[~valid], torch.zeros_like(out[~valid])), 'padding rows must be exact zeros'
+    ref = og.m_grouped_contiguous(a_deq, b_deq, layout_t, True, alignment)
+    assert calc_diff(out[valid], ref[valid]) < THRESH
