@@ -694,8 +694,12 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
             const int pk = ceil_div(a.k, 128);
             int ks = 1;
             if (env_ks == 1 || env_ks == 2 || env_ks == 4 || env_ks == 8) ks = env_ks;
-            else
-                while (ks < 8 && pk >= 16 * ks) ks *= 2;
+            else {
+                // (and while the workgroups of 8 waves still fit one round on the CUs: 1x7168x4096 11.7 vs
+                // 13.4 us at ks 2 / 4, 1x7168x7168 16.1 vs 16.9; cold event us)
+                const int64_t gb = a.gemm_type == kBatched ? a.num_groups : 1;
+                while (ks < 8 && pk >= 16 * ks && (int64_t)ceil_div(a.n, 32 / ks) * gb <= cus) ks *= 2;
+            }
             // eight-wave workgroups (two waves per SIMD); four-wave ones (half the rows each, twice the
             // workgroups) measured slower even where eight-wave ones leave CUs idle (1x2112x7168,
             // ks 4: 7.8 vs 7.2 us on 264 vs 132 CUs), so they are a tuning option only

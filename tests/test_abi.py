@@ -179,6 +179,17 @@ def test_launch_plan_without_device(lib):
     assert lib.dg_launch_plan(None, None) == -1
 
 
+def test_gemv_plan_splits_k_within_one_round(lib):
+    """M = 1 decode GEMV: the K split between a workgroup's waves doubles while each range keeps 16 steps
+    of 128 bytes and the workgroups (64 / ks rows of B each) still fit one round on the 256 CUs."""
+    for (n, k), rows in (((2112, 7168), 16), ((4096, 7168), 16), ((7168, 7168), 32), ((7168, 4096), 32),
+                         ((3072, 7168), 16)):
+        info = _lib.LaunchInfo()
+        assert lib.dg_launch_plan(_plan_args(1, n, k, 0), ctypes.byref(info)) == 0, lib.dg_last_error()
+        assert info.skinny == 3 and info.block_n == rows, (n, k, info.skinny, info.block_n)
+        assert info.grid <= 256
+
+
 def test_workspace_size_of_decode_plans(lib):
     """dg_gemm_workspace_size covers the shared-ring plans' partial tiles as their kernels number them: with M
     in two 64-row blocks the strips are padded to whole groups of eight (128x2112x7168: 33 strips -> 40, two
