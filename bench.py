@@ -40,7 +40,7 @@ def parse():
     ap.add_argument('--n', type=int, default=N)
     ap.add_argument('--k', type=int, default=K)
     ap.add_argument('--suite', default=None,
-                    help='comma list of dense,decode,bf16,fp4,grouped,kgrouped,einsum,host,ref: one JSON line per shape '
+                    help='comma list of dense,decode,bf16,bf16nn,fp4,grouped,kgrouped,einsum,host,ref: one JSON line per shape '
                          '(cold-L2 kernel times) instead of the north-star line')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a 256 MiB device copy (reference kernel for FETCH_SIZE / WRITE_SIZE scaling)')
@@ -292,15 +292,22 @@ def run_suite(groups):
                 us = _time_cold(lambda: deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d))
                 _line('dense', f'fp8_gemm_nt {m}x{n}x{k}', us, 2.0 * m * n * k,
                       m * k + n * k + 2 * m * n + (m + n) * (k // 64) * 2)
-    if 'bf16' in groups:
-        for m in (128, 4096):
-            for n, k in NK:
-                a = (torch.randn(m, k, device=dev, generator=gen) * 0.1).bfloat16()
-                b = (torch.randn(n, k, device=dev, generator=gen) * 0.1).bfloat16()
-                d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-                us = _time_cold(lambda: deep_gemm.bf16_gemm_nt(a, b, d))
-                _line('bf16', f'bf16_gemm_nt {m}x{n}x{k}', us, 2.0 * m * n * k, 2 * (m * k + n * k + m * n),
-                      peak_tflops=2500.0)
+    if 'bf16' in groups or 'bf16nn' in groups:
+        # config 3: bf16_gemm_nt and bf16_gemm_nn (B stored [K, N]) over config 2's grid
+        for lay in [x for x in ('nt', 'nn') if ('bf16' if x == 'nt' else 'bf16nn') in groups]:
+            for m in (1, 64, 128, 4096):
+                for n, k in NK:
+                    a = (torch.randn(m, k, device=dev, generator=gen) * 0.1).bfloat16()
+                    b = (torch.randn(n, k, device=dev, generator=gen) * 0.1).bfloat16()
+                    d = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+                    if lay == 'nt':
+                        fn = lambda: deep_gemm.bf16_gemm_nt(a, b, d)
+                    else:
+                        b_kn = b.t().contiguous()
+                        fn = lambda: deep_gemm.bf16_gemm_nn(a, b_kn, d)
+                    us = _time_cold(fn)
+                    _line('bf16' if lay == 'nt' else 'bf16nn', f'bf16_gemm_{lay} {m}x{n}x{k}', us, 2.0 * m * n * k,
+                          2 * (m * k + n * k + m * n), peak_tflops=2500.0)
     if 'fp4' in groups:
         for m in (128, 4096):
             for n, k in ((7168, 2048), (4096, 7168)):

@@ -305,8 +305,9 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
     }
     int mt = a.m <= 32 ? 1 : (a.m <= 64 ? 2 : 4), nb = 1, nw = 4, d = 2, ar = a.m <= 16 ? 16 : 32 * mt;
     // long K over at most one strip per CU: eight waves per strip keep more of it in flight
-    // (M = 1, 7168x16384: 24.4 vs 26.9 us)
-    if (a.m <= 16 && a.k >= 8192 && (int64_t)ceil_div(a.n, 32) * groups0 <= cus)
+    // (M = 1, 7168x16384: 24.4 vs 26.9 us; bf16 rows, twice the bytes per K, keep four waves:
+    // 46.6 vs 50.3 us cold)
+    if (a.m <= 16 && a.k >= 8192 && a.kind != kBF16 && (int64_t)ceil_div(a.n, 32) * groups0 <= cus)
         nw = 8;
     if (env.mode == 1) {
         mt = env.mt; nb = env.nb; nw = env.nw; d = env.d; ar = env.ar;
