@@ -230,6 +230,9 @@ SkinnyEnv skinny_env() {
 // of A, more than two strips per CU (N = 24576) favour the tile kernel (M = 64: 20.1 vs 15.4).
 bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const SkinnyEnv& env, Plan& out) {
     if (env.mode == 0 || !(a.gemm_type == kNormal || a.gemm_type == kBatched || a.gemm_type == kMasked)) return false;
+    // (MN-major B is read in place by the skinny kernel's 32-column configurations; MN-major A is not)
+    const bool bmn = a.b_mn_major != 0;
+    if (a.a_mn_major) return false;
     const int groups0 = a.gemm_type == kNormal ? 1 : a.num_groups;
     // FP8 decode shapes with 64 < M <= 128 and K <= 8192 (dense or batched) take the shared-ring kernel:
     // its waves own the tile's 32x32 blocks and fetch each group of B and A once per workgroup, four
@@ -243,7 +246,7 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
     // 128x2112x7168 24.0 (26.2).  (With 128 x 32 strips they had not: bf16 128x4096x7168 29.9 vs 29.0.)
     SkinnyEnv rows_env = env;
     const bool rows_kind = a.kind == kFP8FP8 || a.kind == kFP8FP4 || a.kind == kBF16;
-    if (env.rows == -1 && env.mode == -1 && rows_kind && a.m > 64 && a.m <= 128 && a.k <= 16384 &&
+    if (env.rows == -1 && env.mode == -1 && rows_kind && !bmn && a.m > 64 && a.m <= 128 && a.k <= 16384 &&
         (a.gemm_type == kNormal || a.gemm_type == kBatched) && (int64_t)ceil_div(a.n, 32) * groups0 <= 2 * (int64_t)cus) {
         rows_env.rows = 1;
         rows_env.rmt = 4; rows_env.rnb = 1; rows_env.rd = 4; rows_env.rsplit = 0;
@@ -285,7 +288,7 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
     }
     // (dense and batched launches may hold M in several tiles of 32 mt rows, M <= 128)
     const bool rows_mblocks = (a.gemm_type == kNormal || a.gemm_type == kBatched) && a.m <= 128;
-    if (rows_env.rows == 1 && (a.m <= 32 * rows_env.rmt || rows_mblocks) &&
+    if (rows_env.rows == 1 && !bmn && (a.m <= 32 * rows_env.rmt || rows_mblocks) &&
         lookup_skinny_rows(a.kind, rows_env.rmt, rows_env.rnb, rows_env.rd, kEpiBf16) != nullptr) {
         const SkinnyEnv& env = rows_env;
         // shared-ring decode kernel: K split across workgroups while the tiles leave CUs idle,
@@ -314,7 +317,9 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
     } else if (a.m > 128 || (a.m > 16 && (int64_t)ceil_div(a.n, 32) * groups0 > 2 * (int64_t)cus)) {
         return false;
     }
-    if (a.m > ar || lookup_skinny(a.kind, mt, nb, nw, d, ar, kEpiBf16) == nullptr) return false;
+    if (a.m > ar || (bmn ? lookup_skinny_mn(a.kind, mt, nb, nw, d, ar, kEpiBf16)
+                         : lookup_skinny(a.kind, mt, nb, nw, d, ar, kEpiBf16)) == nullptr)
+        return false;
     const int64_t strips = (int64_t)ceil_div(a.n, 32 * nb) * groups0;
     const int nk64 = std::max(1, ceil_div(a.k, 64));
     int sp = 1;
@@ -404,7 +409,7 @@ Plan select_plan(const dg_gemm_args& a, int cus, bool allow_split) {
 }
 
 struct MemoKey {
-    int kind, type, m, n, k, g, cus, align, allow_split;
+    int kind, type, m, n, k, g, cus, align, allow_split, mn;
     SkinnyEnv skinny;
     bool operator==(const MemoKey& o) const { return memcmp(this, &o, sizeof(*this)) == 0; }
 };
@@ -436,6 +441,7 @@ Plan choose(const dg_gemm_args& a, int cus, bool allow_split) {
     key.kind = a.kind; key.type = a.gemm_type; key.m = a.m; key.n = a.n; key.k = a.k;
     key.g = a.num_groups; key.cus = cus; key.align = a.alignment;
     key.allow_split = allow_split && a.split_k != 1;
+    key.mn = (a.a_mn_major ? 1 : 0) | (a.b_mn_major ? 2 : 0);
     key.skinny = skinny_env();
     Plan pl;
     {
@@ -661,8 +667,10 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     }
     const TileCfg cfg = plan.tile;
     if (cfg.bm == 0) return dg_set_error("dg_gemm: no tile shape fits this problem");
-    if ((amn || bmn) && (plan.skinny_nw > 0 || plan.split != 1 || cfg.km != 2 || cfg.stages != 2 ||
-                         cfg.bm > 256 || cfg.bn > 256)) {
+    // (MN-major B also in the skinny kernel's 32-column plans)
+    const bool skinny_mn = bmn && !amn && plan.skinny_nw > 0 && !plan.skinny_rows && cfg.bn == 32;
+    if ((amn || bmn) && !skinny_mn && (plan.skinny_nw > 0 || plan.split != 1 || cfg.km != 2 || cfg.stages != 2 ||
+                                       cfg.bm > 256 || cfg.bn > 256)) {
         dg_set_error("dg_gemm: MN-major operands need a 128-byte-stage tile plan (large M and N); this problem "
                      "plans another kernel");
         return DG_ENOKERNEL;
@@ -738,7 +746,8 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
                             b_span <= 0x7fffffffLL && sfa_span <= 0x7fffffffLL && sfb_span <= 0x7fffffffLL;
     KernelFn fn = jit ? nullptr
                 : skinny ? (plan.skinny_rows ? lookup_skinny_rows(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_d, epi_kind)
-                                             : lookup_skinny(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_nw, plan.skinny_d, plan.skinny_ar, epi_kind))
+                          : skinny_mn ? lookup_skinny_mn(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_nw, plan.skinny_d, plan.skinny_ar, epi_kind)
+                                      : lookup_skinny(a.kind, cfg.bm / 32, cfg.bn / 32, plan.skinny_nw, plan.skinny_d, plan.skinny_ar, epi_kind))
                 : (amn || bmn) ? lookup_kernel_mn(a.kind, cfg.bm, cfg.bn, epi_kind, amn, bmn)
                          : lookup_kernel(a.kind, cfg.bm, cfg.bn, epi_kind, persistent);
     if (fn == nullptr && !jit) {
@@ -783,8 +792,10 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     if (tiles <= 0) return DG_OK;
     // split-K grids are padded to whole groups of 8 tiles (one per XCD); persistent grids hold
     // one workgroup per CU (set_num_sms caps them)
+    // (MN-major skinny launches: padded to whole blocks of 8 x the strips that share a 128-byte line of B)
+    const int64_t tiles_pad = skinny_mn ? align_up64(tiles, 8 * (a.kind == kBF16 ? 2 : 4)) : tiles;
     int64_t grid = persistent ? std::min<int64_t>(tiles, (int64_t)cus * cfg.occ)
-                       : plan.split > 1 ? align_up64(tiles, 8) * plan.split : tiles;
+                       : plan.split > 1 ? align_up64(tiles_pad, 8) * plan.split : tiles_pad;
     // Anchored M-grouped tiles under a CU cap: one workgroup per allowed CU walks the layout's real
     // tiles (gemm_walk_kernel).  Uncapped, the upper-bound grid is faster: the dispatcher hands each
     // CU that frees the next real tile and the spare workgroups exit after one scan, where a fixed

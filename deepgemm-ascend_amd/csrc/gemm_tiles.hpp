@@ -137,6 +137,8 @@ constexpr SkinnyCfg kSkinny[] = {{1, 1, 4, 2, 16}, {1, 1, 4, 3, 16}, {1, 1, 4, 2
                                  {4, 1, 4, 2, 128}};
 constexpr int kNumSkinny = sizeof(kSkinny) / sizeof(kSkinny[0]);
 KernelFn lookup_skinny(int kind, int mt, int nb, int nw, int d, int ar, int epi);
+// the same with MN-major B (stored [K][N], read in place): e4m3 / bf16, 32-column strips (nb = 1)
+KernelFn lookup_skinny_mn(int kind, int mt, int nb, int nw, int d, int ar, int epi);
 
 // Shared-ring decode kernels (skinny_rows_kernel): MT x NB waves, one 32x32 block each, a ring
 // of d group slots shared by the workgroup.

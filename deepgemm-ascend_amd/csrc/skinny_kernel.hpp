@@ -50,7 +50,7 @@ __device__ __forceinline__ int shift_at_use(int x, int sh) {
     return y;
 }
 
-template <int KIND, int MT, int NB, int NW, int D, int AR, int EPI>
+template <int KIND, int MT, int NB, int NW, int D, int AR, int EPI, bool BMN = false>
 __device__ __forceinline__ void skinny_body(const KParams& p, const int vb) {
     constexpr bool kAFp4 = KIND == kFP4FP4;
     constexpr bool kBFp4 = KIND == kFP8FP4 || KIND == kFP4FP4;
@@ -67,6 +67,13 @@ __device__ __forceinline__ void skinny_body(const KParams& p, const int vb) {
     constexpr int RPI = 64 / SPR, RPIA = 64 / SPRA;         // rows per load instruction
     constexpr int NDMA = BN / RPI, NDMAA = AR / RPIA;       // load instructions per group slot
     static_assert(AR % RPIA == 0 && AR <= BM, "staged A rows");
+    // MN-major B (BMN: B stored [K][N], N contiguous; e4m3 or bf16, one 32-column block per strip): a
+    // group slot holds the group's K rows of the strip's 32 columns (32 e4m3 / 64 bf16 bytes each, the
+    // same bytes as the K-major slot), and fragments are read with ds_read_b64_tr_b8 / _b16, which hand
+    // each lane consecutive K of one column.  A half-wave's transposing read covers 8 (e4m3) / 4 (bf16)
+    // consecutive K rows in one contiguous 256-byte span, so the rows need no swizzle.
+    static_assert(!BMN || (NB == 1 && (KIND == kFP8FP8 || KIND == kBF16)), "MN-major B: e4m3 / bf16, 32-column strips");
+    constexpr int MN_E = kBf16 ? 2 : 1, MN_PITCH = 32 * MN_E;
     constexpr int SLOTB = BN * RG;                          // B part of a group slot
     constexpr int SLOT = SLOTB + AR * RGA;                  // bytes of one group slot
     constexpr int NBLK = NB * MT;                           // 32x32 output blocks
@@ -97,9 +104,17 @@ __device__ __forceinline__ void skinny_body(const KParams& p, const int vb) {
             t = b / split_k;
             split = b % split_k;
         }
-        if (t >= p.num_tiles) return;
+        if (!BMN && t >= p.num_tiles) return;
     } else {
         t = vb;
+    }
+    if constexpr (BMN) {
+        // The L = 128 / MN_PITCH strips whose K rows share 128-byte lines run on one XCD (workgroup t
+        // runs on XCD t % 8; the host pads the grid to whole blocks of 8 L), so each line reaches one L2.
+        constexpr int L = 128 / MN_PITCH;
+        const int i = t % (8 * L);
+        t = t - i + (i % 8) * L + i / 8;
+        if (t >= p.num_tiles) return;
     }
     const int tile_id = t;
     const int nn = p.num_n_blocks;
@@ -116,7 +131,7 @@ __device__ __forceinline__ void skinny_body(const KParams& p, const int vb) {
     const int M = __builtin_amdgcn_readfirstlane(p.gemm_type == kMasked ? min(p.m, p.layout[batch]) : p.m);
     if (M <= 0) return;
     const uint8_t* a_base = p.a;
-    const uint8_t* b_base = p.b + (int64_t)n0 * p.ldb;
+    const uint8_t* b_base = p.b + (BMN ? (int64_t)n0 * MN_E : (int64_t)n0 * p.ldb);
     const uint16_t* sfa = p.sfa;
     const uint16_t* sfb = p.sfb;
     uint8_t* d_base = p.d;
@@ -141,7 +156,8 @@ __device__ __forceinline__ void skinny_body(const KParams& p, const int vb) {
     const int ngw = max(0, min(ng, gw0 + gpw) - gw0);               // groups of this wave
 
     const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(a_base, (int64_t)rows_a * p.lda);
-    const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(b_base, (int64_t)rows_b * p.ldb);
+    const __amdgpu_buffer_rsrc_t rs_b =
+        make_rsrc(b_base, BMN ? (int64_t)p.k * p.ldb - (int64_t)n0 * MN_E : (int64_t)rows_b * p.ldb);
     __amdgpu_buffer_rsrc_t rs_sa, rs_sb;
     if constexpr (!kBf16) {
         rs_sa = make_rsrc(sfa, (int64_t)nk64 * p.sfa_ld * 2);
@@ -179,6 +195,17 @@ __device__ __forceinline__ void skinny_body(const KParams& p, const int vb) {
         const int row = i * RPI + lane / SPR;
         vrow[i] = row < rows_b ? (uint32_t)(row * p.ldb + lk[i]) : kOOBOffset;
     }
+    // MN-major B: load instruction i fills LDS bytes [1024 i, +1024) of the slot's B part, i.e. K row
+    // kr = (1024 i + 16 lane) / MN_PITCH of the group, column bytes (16 lane) % MN_PITCH (past the
+    // strip's columns: out of range); lk[i] holds kr
+    if constexpr (BMN) {
+#pragma unroll
+        for (int i = 0; i < NDMA; ++i) {
+            const int o = i * 1024 + lane * 16;
+            lk[i] = o / MN_PITCH;
+            vrow[i] = (o % MN_PITCH) < rows_b * MN_E ? (uint32_t)(lk[i] * p.ldb + o % MN_PITCH) : kOOBOffset;
+        }
+    }
     int lka[NDMAA];
     uint32_t vrowa[NDMAA];
 #pragma unroll
@@ -199,7 +226,16 @@ __device__ __forceinline__ void skinny_body(const KParams& p, const int vb) {
         constexpr int S = decltype(slot_tag)::value;
         const bool live = gi < ngw;
         const int kbg = kb0 + (gw0 + gi) * G;
-        {
+        if constexpr (BMN) {
+            // K rows of the group (rows past K or past the split's range read zeros)
+            const int krows = live && kbg < kb1 ? min(p.k, kb1 * 64) - kbg * 64 : 0;
+            const uint32_t kofs = (uint32_t)(kbg * 64) * (uint32_t)p.ldb;
+#pragma unroll
+            for (int i = 0; i < NDMA; ++i) {
+                const uint32_t v = lk[i] < krows && vrow[i] != kOOBOffset ? vrow[i] + kofs : kOOBOffset;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, (lds_void*)(ring + S * SLOT + i * 1024), 16, v, 0, 0, 0);
+            }
+        } else {
             // B rows of the group: whole lines into the wave's ring slot S (a piece past K or past
             // the strip's rows reads zeros)
             const int left = live && kbg < kb1 ? kbytes_b - kbg * RBB : 0;
@@ -210,6 +246,8 @@ __device__ __forceinline__ void skinny_body(const KParams& p, const int vb) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, (lds_void*)(ring + S * SLOT + i * 1024), 16, v,
                                                          __builtin_amdgcn_readfirstlane(kbg * RBB), 0, 0);
             }
+        }
+        {
             // A rows likewise, behind the B rows of the slot
             const int left_a = live && kbg < kb1 ? kbytes_a - kbg * RBA : 0;
             const int kend_a = (kb1 - kbg) * RBA;
@@ -243,6 +281,30 @@ __device__ __forceinline__ void skinny_body(const KParams& p, const int vb) {
 
     // B fragment piece P of block j, strip block jn, from ring slot S
     auto b_piece = [&](int S, int j, int jn, int P) -> i32x4 {
+        if constexpr (BMN) {
+            // two transposing reads: lane (r, q) gets K [32 P + 16 q, +16) (e4m3) / [16 P + 8 q, +8) (bf16)
+            // of column r of block j (the K-major piece's bytes).  e4m3: in each 16-lane group lane s
+            // supplies the 8 bytes of K row k0 + s / 2 at column bytes 16 h + 8 (s % 2), and lane i
+            // receives K k0 .. k0 + 7 of column 16 h + i; bf16: lane s supplies K row k0 + s / 4 at
+            // columns 16 h + 4 (s % 4), and lane i receives K k0 .. k0 + 3 of column 16 h + i.
+            typedef int v2i __attribute__((ext_vector_type(2)));
+            const int s16 = lane & 15, h = (lane >> 4) & 1;
+            const uint8_t* slot0 = ring + S * SLOT;
+            if constexpr (!kBf16) {
+                typedef __attribute__((address_space(3))) v2i lds_v2i;
+                const uint8_t* b0 = slot0 + (j * 64 + 32 * P + 16 * q + (s16 >> 1)) * MN_PITCH + 16 * h + (s16 & 1) * 8;
+                const v2i e0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0));
+                const v2i e1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(b0 + 8 * MN_PITCH));
+                return i32x4{e0[0], e0[1], e1[0], e1[1]};
+            } else {
+                typedef short v4s __attribute__((ext_vector_type(4)));
+                typedef __attribute__((address_space(3))) v4s lds_v4s;
+                const uint8_t* b0 = slot0 + (j * 64 + 16 * P + 8 * q + (s16 >> 2)) * MN_PITCH + 32 * h + (s16 & 3) * 8;
+                const v2i e0 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(b0)));
+                const v2i e1 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(b0 + 4 * MN_PITCH)));
+                return i32x4{e0[0], e0[1], e1[0], e1[1]};
+            }
+        }
         const int R = jn * 32 + r;
         const int slot = (j * RBB + 32 * P) / 16 + q;
         return *reinterpret_cast<const i32x4*>(ring + S * SLOT + R * RG + ((slot ^ slot_swizzle<SPR>(R)) << 4));
@@ -800,9 +862,9 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const KParams p) {
     split_reduce_body<MT, NB, EPI>(p, blockIdx.x + p.vbase);
 }
 
-template <int KIND, int MT, int NB, int NW, int D, int AR, int EPI>
+template <int KIND, int MT, int NB, int NW, int D, int AR, int EPI, bool BMN = false>
 __global__ __launch_bounds__(NW * 64, NW <= 4 ? 2 : 1) void skinny_kernel(const KParams p) {
-    skinny_body<KIND, MT, NB, NW, D, AR, EPI>(p, blockIdx.x + p.vbase);
+    skinny_body<KIND, MT, NB, NW, D, AR, EPI, BMN>(p, blockIdx.x + p.vbase);
 }
 
 }  // namespace dg

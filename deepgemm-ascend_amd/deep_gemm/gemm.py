@@ -140,10 +140,11 @@ def _launch_operands(args: _lib.GemmArgs, d: torch.Tensor, a: torch.Tensor, b: t
     every other operand get a K-major copy."""
     if args.kind in (_lib.DG_KIND_FP8_FP8, _lib.DG_KIND_BF16) and not get_dry_run() and not args.jit:
         a_mn, b_mn = _mn_in_place(a, k), _mn_in_place(b, k)
-        if args.kind == _lib.DG_KIND_BF16 and not a_mn and args.gemm_type == _lib.DG_GEMM_NORMAL:
+        if args.kind == _lib.DG_KIND_BF16 and not a_mn and args.gemm_type == _lib.DG_GEMM_NORMAL and args.m > 128:
             # dense bf16 with only B MN-major (nn) measured faster with B copied (4096x2112x7168: 176.0
             # vs 199.5 us; tn / tt gain in place: 183.9 vs 207.3, 172.1 vs 190.5).  M-grouped B is the
-            # whole expert-weight tensor, read in place.
+            # whole expert-weight tensor, read in place; decode shapes (M <= 128) read B in place with the
+            # skinny-M kernel where their plan takes it.
             b_mn = False
         if a_mn or b_mn:
             a_k = a if a_mn else _to_kernel_operand(a, k)

@@ -82,7 +82,8 @@ def test_mn_major_north_star_default_plan(monkeypatch, no_copy, layout):
 
 
 def test_mn_major_small_plan_falls_back_to_copy(monkeypatch):
-    """A plan without a 128-K-stage tile (here a decode shape) copies the MN-major operand."""
+    """A plan that cannot read an MN-major operand in place (here MN-major A at a decode shape: the
+    decode kernels read A K-major) copies it."""
     m, n, k = 64, 512, 256
     calls = []
     orig = dg_gemm_mod._transpose_to_k_major
@@ -91,10 +92,10 @@ def test_mn_major_small_plan_falls_back_to_copy(monkeypatch):
     a, sfa, a_deq = operand(m, k, 'e4m3', (1, 128), g, 'randn')
     b, sfb, b_deq = operand(n, k, 'e4m3', (128, 128), g, 'randn')
     d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
-    deep_gemm.fp8_gemm_nn((a.cuda(), sfa.cuda()), (b.cuda().t().contiguous(), sfb.cuda().t()), d,
-                          recipe_a=(1, 128), recipe_b=(128, 128))
+    a_km = a.cuda().view(torch.uint8).t().contiguous().view(torch.float8_e4m3fn)   # [K, M]
+    deep_gemm.fp8_gemm_tt((a_km, sfa.cuda().t()), (b.cuda(), sfb.cuda()), d, recipe_a=(1, 128), recipe_b=(128, 128))
     torch.cuda.synchronize()
-    assert calls, 'the decode plan was expected to copy B'
+    assert calls, 'the decode plan was expected to copy A'
     assert calc_diff(d.cpu(), og.gemm_nt(a_deq, b_deq)) < THRESH
 
 
@@ -156,7 +157,7 @@ def _bf16_layout_call(layout, m, n, k, seed, block, monkeypatch, no_copy):
         monkeypatch.setenv('DG_FORCE_BLOCK', block)
     fn = getattr(deep_gemm, f'bf16_gemm_{layout}')
     d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
-    # (bf16 nn copies B by design: only A MN-major operands are read in place for bf16)
+    # (bf16 nn at M > 128 copies B by design: only A MN-major operands are read in place there)
     no_copy(layout in ('tn', 'tt'))
     fn(a, b, d)
     torch.cuda.synchronize()
