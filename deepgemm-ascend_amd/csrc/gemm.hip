@@ -314,7 +314,8 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
         nw = 8;
     if (env.mode == 1) {
         mt = env.mt; nb = env.nb; nw = env.nw; d = env.d; ar = env.ar;
-    } else if (a.m > 128 || (a.m > 16 && (int64_t)ceil_div(a.n, 32) * groups0 > 2 * (int64_t)cus)) {
+    } else if (a.m > 128 || (a.m > 16 && !bmn && (int64_t)ceil_div(a.n, 32) * groups0 > 2 * (int64_t)cus)) {
+        // (MN-major B keeps the skinny kernel over many strips: the tile plans would copy B first)
         return false;
     }
     if (a.m > ar || (bmn ? lookup_skinny_mn(a.kind, mt, nb, nw, d, ar, kEpiBf16)
