@@ -164,3 +164,26 @@ def test_noalloc_split_k_after_m_indices():
     for _ in range(2):
         assert torch.equal(_run(lib, args, True), d_ws)
     assert calc_diff(d_ws, ref) < 1e-5
+
+
+def test_noalloc_mn_major_b_decode():
+    """A split-K decode plan with MN-major B ([K][N], read in place by the skinny kernel): dg_gemm_noalloc
+    matches dg_gemm bit for bit on two calls in a row (the second smaller) and the oracle."""
+    lib = _lib.load()
+    for (m, n, k), seed in (((64, 2112, 7168), 8), ((16, 1000, 4096), 9)):
+        args, keep, ref = _args(m, n, k, seed)
+        ldb = -(-n // 16) * 16   # (K rows of B 16-byte aligned)
+        b_kn = torch.zeros(k, ldb, dtype=torch.uint8, device='cuda')   # [K, N] in a wider buffer
+        b_kn[:, :n] = keep[1].view(torch.uint8).t()
+        args.b, args.ldb, args.b_mn_major = b_kn.data_ptr(), ldb, 1
+        info = _lib.LaunchInfo()
+        args.workspace, args.workspace_bytes = 1, 1 << 40
+        _lib.check(lib.dg_launch_plan(ctypes.byref(args), ctypes.byref(info)), lib)
+        args.workspace, args.workspace_bytes = None, 0
+        print(f'noalloc mn-major B m={m} n={n} k={k} split_k={info.split_k} skinny={info.skinny}', flush=True)
+        assert info.skinny == 1 and info.split_k > 1
+        d_noalloc = _run(lib, args, True)
+        d_ws = _run(lib, args, False)
+        assert torch.equal(d_noalloc, d_ws)
+        assert calc_diff(d_noalloc, ref) < 1e-5
+        assert torch.equal(_run(lib, args, True), d_ws)
