@@ -136,8 +136,9 @@ def _launch_operands(args: _lib.GemmArgs, d: torch.Tensor, a: torch.Tensor, b: t
                      batch_a: bool, batch_b: bool) -> None:
     """Set A and B (strides, batch strides, K) and launch.  e4m3 / bf16 MN-major operands are read in
     place by the 128-byte-stage tile kernels (the reference takes operand majors as kernel parameters,
-    deep_gemm/include/deep_gemm/fp8_gemm.hpp:18-35); a plan with another kernel (DG_ENOKERNEL) and
-    every other operand get a K-major copy."""
+    deep_gemm/include/deep_gemm/fp8_gemm.hpp:18-35), and MN-major B also by the skinny-M decode kernel
+    (with both operands MN-major a decode call copies A only); a plan with another kernel (DG_ENOKERNEL)
+    and every other operand get a K-major copy."""
     if args.kind in (_lib.DG_KIND_FP8_FP8, _lib.DG_KIND_BF16) and not get_dry_run() and not args.jit:
         a_mn, b_mn = _mn_in_place(a, k), _mn_in_place(b, k)
         if args.kind == _lib.DG_KIND_BF16 and not a_mn and args.gemm_type == _lib.DG_GEMM_NORMAL and args.m > 128:
@@ -161,6 +162,15 @@ def _launch_operands(args: _lib.GemmArgs, d: torch.Tensor, a: torch.Tensor, b: t
                 args.a_mn_major, args.b_mn_major = int(a_mn), int(b_mn)
                 if _launch(args, d, allow_no_kernel=True):
                     return
+                if a_mn and b_mn:
+                    # (decode plans read MN-major B, not A, in place: copy only A, the smaller operand)
+                    a_c = _to_kernel_operand(a, k)
+                    if a_c.size(-1) == k:
+                        args.a, args.lda, args.a_mn_major = a_c.data_ptr(), a_c.stride(-2), 0
+                        if batch_a:
+                            args.batch_stride_a = a_c.stride(0)
+                        if _launch(args, d, allow_no_kernel=True):
+                            return
                 args.a_mn_major = args.b_mn_major = 0
     a_k = _to_kernel_operand(a, k)
     b_k = _to_kernel_operand(b, k)

@@ -107,3 +107,31 @@ def test_mn_major_b_decode_fp32_accumulate(no_copy):
     torch.cuda.synchronize()
     no_copy(False)
     assert calc_diff(d.cpu(), ref + c.cpu()) < THRESH
+
+
+@pytest.mark.parametrize('kind', ['fp8', 'bf16'])
+def test_mn_major_tn_decode_copies_only_a(monkeypatch, kind):
+    """tn at a decode shape (A [K, M] and B [K, N] both MN-major): the decode kernels read A K-major, so only
+    A is copied; B is read in place."""
+    m, n, k = 64, 2112, 1024
+    g = gen(94)
+    copied = []
+    orig = dg_gemm_mod._transpose_to_k_major
+    monkeypatch.setattr(dg_gemm_mod, '_transpose_to_k_major',
+                        lambda t, *args, **kw: copied.append(tuple(t.shape)) or orig(t, *args, **kw))
+    d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
+    if kind == 'fp8':
+        a, sfa, a_deq = operand(m, k, 'e4m3', (1, 128), g, 'randn')
+        b, sfb, b_deq = operand(n, k, 'e4m3', (128, 128), g, 'randn')
+        a_km = _mn_major(a.cuda().view(torch.uint8), 16).view(torch.float8_e4m3fn)
+        b_kn = _mn_major(b.cuda().view(torch.uint8), 16).view(torch.float8_e4m3fn)
+        deep_gemm.fp8_gemm_tn((a_km, sfa.cuda().t()), (b_kn, sfb.cuda().t()), d, recipe_a=(1, 128), recipe_b=(128, 128))
+        ref = og.gemm_nt(a_deq, b_deq)
+    else:
+        a = (torch.randn(m, k, generator=g) * 0.1).bfloat16()
+        b = (torch.randn(n, k, generator=g) * 0.1).bfloat16()
+        deep_gemm.bf16_gemm_tn(_mn_major(a.cuda(), 8), _mn_major(b.cuda(), 8), d)
+        ref = og.gemm_nt(a.float(), b.float())
+    torch.cuda.synchronize()
+    assert len(copied) == 1 and sorted(copied[0]) == sorted((m, k)), copied
+    assert calc_diff(d.cpu(), ref) < THRESH
