@@ -78,7 +78,7 @@ def test_mn_major_b_decode_forced(monkeypatch, no_copy, kind, cfg, m, n, k):
 
 
 @pytest.mark.parametrize('kind', ['fp8', 'bf16'])
-@pytest.mark.parametrize('m,n,k', [(1, 2112, 7168), (1, 7168, 2048), (64, 4096, 7168), (100, 2112, 7168),
+@pytest.mark.parametrize('m,n,k', [(1, 2112, 7168), (128, 4096, 7168), (128, 7168, 16384), (96, 3072, 7168), (1, 7168, 2048), (64, 4096, 7168), (100, 2112, 7168),
                                    (128, 7168, 2048), (128, 2112, 7168), (33, 7168, 16384)])
 def test_mn_major_b_decode_default_plan(no_copy, kind, m, n, k):
     """config-2 / config-3 decode shapes in the nn layout on their default plans: B read in place."""
