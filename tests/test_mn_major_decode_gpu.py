@@ -135,3 +135,23 @@ def test_mn_major_tn_decode_copies_only_a(monkeypatch, kind):
     torch.cuda.synchronize()
     assert len(copied) == 1 and sorted(copied[0]) == sorted((m, k)), copied
     assert calc_diff(d.cpu(), ref) < THRESH
+
+
+@pytest.mark.parametrize('kind', ['fp8', 'bf16'])
+@pytest.mark.parametrize('cus,m,n,k', [(100, 64, 2112, 7168), (64, 1, 4096, 4096), (40, 128, 1000, 2048)])
+def test_mn_major_b_decode_under_cu_cap(no_copy, kind, cus, m, n, k):
+    """set_num_sms(n) below the CU count: the MN-major decode launch (padded and remapped so that strips
+    sharing a line of B run on one XCD) goes out in chunks of at most n workgroups; D matches the oracle."""
+    print(f'mn-major B decode {kind} set_num_sms({cus}) m={m} n={n} k={k}', flush=True)
+    full = deep_gemm.get_num_sms()
+    fn, ref = _case(kind, m, n, k, 96)
+    d = torch.empty(m, n, dtype=torch.bfloat16, device='cuda')
+    try:
+        deep_gemm.set_num_sms(cus)
+        no_copy(True)
+        fn(d)
+        torch.cuda.synchronize()
+        no_copy(False)
+    finally:
+        deep_gemm.set_num_sms(full)
+    assert calc_diff(d.cpu(), ref) < THRESH
