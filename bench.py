@@ -95,7 +95,8 @@ def sustained_clock(step, seconds=1.0):
                 # (idle XCDs sit near 100 MHz; a sample taken before the clock ramps is not the
                 # sustained clock)
                 if clks and min(clks) >= 1000:
-                    samples.append((sum(clks) / len(clks), m.get('current_socket_power')))
+                    ts = m.get('system_clock_counter', m.get('firmware_timestamp'))
+                    samples.append((sum(clks) / len(clks), m.get('current_socket_power'), ts))
             except Exception:   # noqa: BLE001
                 pass
             time.sleep(0.005)
@@ -118,14 +119,26 @@ def sustained_clock(step, seconds=1.0):
         amdsmi.amdsmi_shut_down()
     except Exception:   # noqa: BLE001
         pass
-    if not samples:
+    # one sample per refresh of the metrics table (its timestamp), and only those taken under load: the
+    # table can lag the workload, and a refresh from an idle moment reports a low clock at a fraction of
+    # the loaded power
+    seen, uniq = set(), []
+    for c, p, ts in samples:
+        key = ts if ts is not None else (c, p)
+        if key not in seen:
+            seen.add(key)
+            uniq.append((c, p))
+    pmax = max((p for _, p in uniq if isinstance(p, (int, float))), default=None)
+    loaded = [(c, p) for c, p in uniq if pmax is None or (isinstance(p, (int, float)) and p >= 0.6 * pmax)]
+    if not loaded:
         return {'error': 'no samples at a loaded clock (>= 1000 MHz on every XCD)'}
-    clk = sorted(c for c, _ in samples)
-    pw = sorted(p for _, p in samples if isinstance(p, (int, float)))
+    clk = sorted(c for c, _ in loaded)
+    pw = sorted(p for _, p in loaded if isinstance(p, (int, float)))
     return {'clock_mhz_median': round(clk[len(clk) // 2], 1), 'clock_mhz_min': round(clk[0], 1),
             'clock_mhz_max': round(clk[-1], 1), 'socket_power_w_median': pw[len(pw) // 2] if pw else None,
-            'samples': len(samples), 'launches': n,
-            'source': 'amdsmi gpu_metrics current_gfxclks (mean over XCDs), sampled while the step ran back to back'}
+            'samples': len(loaded), 'samples_taken': len(samples), 'launches': n,
+            'source': 'amdsmi gpu_metrics current_gfxclks (mean over XCDs), one sample per metrics refresh, '
+                      'those at >= 60 % of the peak sampled socket power, while the step ran back to back'}
 
 
 def make_inputs(m, n, k):
@@ -581,7 +594,7 @@ def main():
     # reference times its kernels): the roofline's achieved rate
     cold_us = _time_cold(step, iters=max(10, min(args.steps, 40)))
 
-    clock = sustained_clock(step)
+    clock = sustained_clock(step, seconds=4.0)
 
     flops = 2.0 * m * n * k
     tflops = flops / (ms_per_step * 1e-3) / 1e12
