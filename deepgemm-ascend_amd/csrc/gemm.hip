@@ -286,6 +286,16 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
             rows_env.rows = -1;   // (128 x 32 strips measured no gain over the skinny kernel for these kinds)
         }
     }
+    // e4m3 with 32 < M <= 64 and long K over many columns: 64 x 128 tiles, split-K partials summed by the
+    // second launch (cold event us, skinny kernel in brackets, two boxes: 64x7168x16384 35.1 (38.6) and 39.4
+    // (40.7), 64x4096x16384 25.5 (26.8) and 25.5 (27.2); at K = 7168 it measured level or behind: 64x4096x7168
+    // 19.1 (18.6), 64x7168x7168 22.8 (21.8))
+    if (env.rows == -1 && env.mode == -1 && a.kind == kFP8FP8 && !bmn && a.m > 32 && a.m <= 64 && a.k > 8192 &&
+        a.k <= 16384 && a.n >= 4096 && allow_split && (a.gemm_type == kNormal || a.gemm_type == kBatched) &&
+        (int64_t)ceil_div(a.n, 128) * groups0 <= (int64_t)cus) {
+        rows_env.rows = 1;
+        rows_env.rmt = 2; rows_env.rnb = 4; rows_env.rd = 4; rows_env.rsplit = 0; rows_env.rreduce = 1;
+    }
     // (dense and batched launches may hold M in several tiles of 32 mt rows, M <= 128)
     const bool rows_mblocks = (a.gemm_type == kNormal || a.gemm_type == kBatched) && a.m <= 128;
     if (rows_env.rows == 1 && !bmn && (a.m <= 32 * rows_env.rmt || rows_mblocks) &&

@@ -176,6 +176,14 @@ def test_launch_plan_without_device(lib):
     long_args.library_workspace = 1
     assert lib.dg_launch_plan(long_args, ctypes.byref(long_k)) == 0, lib.dg_last_error()
     assert long_k.skinny == 2 and long_k.block_n == 64 and long_k.split_reduce == 1
+    # e4m3 M <= 64 with K > 8192 over many columns: 64 x 128 shared-ring tiles, two launches
+    m64 = _lib.LaunchInfo()
+    m64_args = _plan_args(64, 7168, 16384, 0)
+    m64_args.library_workspace = 1
+    assert lib.dg_launch_plan(m64_args, ctypes.byref(m64)) == 0, lib.dg_last_error()
+    assert m64.skinny == 2 and (m64.block_m, m64.block_n) == (64, 128) and m64.split_reduce == 1 and m64.split_k > 1
+    assert lib.dg_launch_plan(_plan_args(64, 7168, 7168, 0), ctypes.byref(m64)) == 0, lib.dg_last_error()
+    assert m64.skinny == 1
     assert lib.dg_launch_plan(None, None) == -1
 
 
