@@ -290,11 +290,18 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
     // second launch (cold event us, skinny kernel in brackets, two boxes: 64x7168x16384 35.1 (38.6) and 39.4
     // (40.7), 64x4096x16384 25.5 (26.8) and 25.5 (27.2); at K = 7168 it measured level or behind: 64x4096x7168
     // 19.1 (18.6), 64x7168x7168 22.8 (21.8))
-    if (env.rows == -1 && env.mode == -1 && a.kind == kFP8FP8 && !bmn && a.m > 32 && a.m <= 64 && a.k > 8192 &&
-        a.k <= 16384 && a.n >= 4096 && allow_split && (a.gemm_type == kNormal || a.gemm_type == kBatched) &&
-        (int64_t)ceil_div(a.n, 128) * groups0 <= (int64_t)cus) {
+    // bf16 rows (twice the bytes per K) gain from K > 4096: 64 x 128 tiles from N >= 6144, 64 x 64 below
+    // (cold event us, skinny kernel in brackets: 64x7168x16384 51.6 (61.3), 64x7168x7168 30.5 (33.5),
+    // 64x4096x7168 21.9 (23.9), 64x4096x16384 42.6 (43.0); 64x2112x7168 22.1 (19.2) keeps the skinny kernel)
+    const bool m64_rows = env.rows == -1 && env.mode == -1 && !bmn && a.m > 32 && a.m <= 64 && a.k <= 16384 &&
+                          allow_split && (a.gemm_type == kNormal || a.gemm_type == kBatched);
+    if (m64_rows && a.kind == kFP8FP8 && a.k > 8192 && a.n >= 4096 && (int64_t)ceil_div(a.n, 128) * groups0 <= (int64_t)cus) {
         rows_env.rows = 1;
         rows_env.rmt = 2; rows_env.rnb = 4; rows_env.rd = 4; rows_env.rsplit = 0; rows_env.rreduce = 1;
+    } else if (m64_rows && a.kind == kBF16 && a.k > 4096 && a.n >= 3072 &&
+               (int64_t)ceil_div(a.n, 64) * groups0 <= (int64_t)cus) {
+        rows_env.rows = 1;
+        rows_env.rmt = 2; rows_env.rnb = a.n >= 6144 ? 4 : 2; rows_env.rd = 4; rows_env.rsplit = 0; rows_env.rreduce = 1;
     }
     // (dense and batched launches may hold M in several tiles of 32 mt rows, M <= 128)
     const bool rows_mblocks = (a.gemm_type == kNormal || a.gemm_type == kBatched) && a.m <= 128;

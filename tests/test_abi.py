@@ -184,6 +184,14 @@ def test_launch_plan_without_device(lib):
     assert m64.skinny == 2 and (m64.block_m, m64.block_n) == (64, 128) and m64.split_reduce == 1 and m64.split_k > 1
     assert lib.dg_launch_plan(_plan_args(64, 7168, 7168, 0), ctypes.byref(m64)) == 0, lib.dg_last_error()
     assert m64.skinny == 1
+    # bf16 from K > 4096: 64 x 128 tiles from N >= 6144, 64 x 64 below, the skinny kernel under N = 3072
+    for (n, k), want in (((7168, 16384), (2, 64, 128)), ((4096, 7168), (2, 64, 64)), ((2112, 7168), (1, None, None))):
+        bf = _plan_args(64, n, k, 0)
+        bf.kind, bf.library_workspace = _lib.DG_KIND_BF16, 1
+        assert lib.dg_launch_plan(bf, ctypes.byref(m64)) == 0, lib.dg_last_error()
+        assert m64.skinny == want[0], (n, k, m64.skinny)
+        if want[1] is not None:
+            assert (m64.block_m, m64.block_n, m64.split_reduce) == (want[1], want[2], 1), (n, k)
     assert lib.dg_launch_plan(None, None) == -1
 
 
