@@ -234,10 +234,10 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
     const bool bmn = a.b_mn_major != 0;
     if (a.a_mn_major) return false;
     const int groups0 = a.gemm_type == kNormal ? 1 : a.num_groups;
-    // FP8 decode shapes with 64 < M <= 128 and K <= 8192 (dense or batched) take the shared-ring kernel:
-    // its waves own the tile's 32x32 blocks and fetch each group of B and A once per workgroup, four
-    // groups deep.  Measured on MI355X with 128 x 32 strips (fp8, cold L2, event us, skinny kernel in
-    // brackets): 128x2112x7168 21.9 (24.8), 128x4096x7168 26.8 (30.0), 128x7168x2048 15.0 (17.0),
+    // Decode shapes with 64 < M <= 128 (e4m3, bf16, FP8 x FP4; dense or batched; K-major B) take the
+    // shared-ring kernel by the rules below: its waves own the tile's 32x32 blocks and fetch each group of
+    // B and A once per workgroup, four groups deep.  Measured on MI355X when it was introduced, with 128 x 32
+    // strips (fp8, cold L2, event us, skinny kernel in brackets): 128x2112x7168 21.9 (24.8), 128x4096x7168 26.8 (30.0), 128x7168x2048 15.0 (17.0),
     // 96x4096x7168 24.5 (27.6); slower at K = 16384 (87.5 vs 74.5) and for M <= 64 (64x2112x7168
     // 18.6 vs 17.4), which keep the skinny kernel.  The tile shapes below (128 x 64, 64 x 64) replaced
     // the 128 x 32 strips; with them bf16 and FP8 x FP4 (e2m1 B) decode shapes gain too (cold event us,
