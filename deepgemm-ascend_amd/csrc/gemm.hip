@@ -49,9 +49,10 @@ namespace dg {
 
 // csrc/status.hip: m_indices layout check of M-grouped launches (reports through the sticky error
 // words; with may_alloc false it never allocates them)
-int check_m_indices(const int32_t* idx, int m, int alignment, int num_groups, hipStream_t st, bool may_alloc);
+int check_m_indices(const int32_t* idx, int m, int alignment, int num_groups, hipStream_t st, bool may_alloc,
+                    int32_t* blk_end = nullptr);
 // csrc/status.hip: the run table of an m_indices layout (for anchored tiles)
-int m_indices_runs(const int32_t* idx, int m, int alignment, int32_t* runs, hipStream_t st);
+int m_indices_runs(const int32_t* idx, int m, int alignment, int32_t* runs, const int32_t* blk_end, hipStream_t st);
 
 KernelFn lookup_kernel(int kind, int bm, int bn, int epi, bool persistent) {
     switch (kind) {
@@ -893,14 +894,19 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
     if (a.gemm_type == kMGroupedIdx && !compile_only) {
         // m_indices layout check: a device kernel that sets the sticky DG_ERR_M_INDICES word
         // (no host synchronisation; without the words -- a call that may not allocate, before
-        // any other call allocated them -- it is skipped)
-        int rc = check_m_indices(a.grouped_layout, a.m, a.alignment, a.num_groups, st, !noalloc);
-        if (rc != DG_OK) return rc;
-        if (p.anchored) {
-            // the layout's run table: for dg_gemm_noalloc in its scratch past the split-K tile
-            // counters (those must stay zero for the next split-K call; an anchored plan splits no
-            // K, so the partial-tile area is free), else in the library's per-stream buffer
-            const int64_t need = (1 + 3 * (int64_t)ceil_div(a.m, p.alignment)) * 4;
+        // any other call allocated them -- it checks nothing); for anchored plans the same kernel
+        // records each block's valid end for the run table
+        int rc = DG_OK;
+        if (!p.anchored) {
+            rc = check_m_indices(a.grouped_layout, a.m, a.alignment, a.num_groups, st, !noalloc);
+            if (rc != DG_OK) return rc;
+        } else {
+            // the layout's run table, then the per-block valid ends: for dg_gemm_noalloc in its scratch
+            // past the split-K tile counters (those must stay zero for the next split-K call; an
+            // anchored plan splits no K, so the partial-tile area is free), else in the library's
+            // per-stream buffer
+            const int64_t nblk = ceil_div(a.m, p.alignment);
+            const int64_t need = (1 + 4 * nblk) * 4;
             void* runs = nullptr;
             if (noalloc) {
                 if (kCounterBytes + need > a.workspace_bytes)
@@ -910,8 +916,12 @@ int gemm_impl(const dg_gemm_args* args, void* stream, bool compile_only, dg_laun
                 rc = stream_workspace(st, need, &runs, 1);
                 if (rc != DG_OK) return rc;
             }
-            p.runs = reinterpret_cast<const int*>(runs);
-            rc = m_indices_runs(a.grouped_layout, a.m, p.alignment, reinterpret_cast<int32_t*>(runs), st);
+            int32_t* const table = reinterpret_cast<int32_t*>(runs);
+            int32_t* const blk_end = table + 1 + 3 * nblk;
+            p.runs = table;
+            rc = check_m_indices(a.grouped_layout, a.m, p.alignment, a.num_groups, st, !noalloc, blk_end);
+            if (rc != DG_OK) return rc;
+            rc = m_indices_runs(a.grouped_layout, a.m, p.alignment, table, blk_end, st);
             if (rc != DG_OK) return rc;
         }
     }

@@ -262,9 +262,9 @@ __device__ __forceinline__ void expert_major_tile(const int* psum, int num_group
 
 // Segments of anchored tiles: with `runs` null, group e of a psum layout, rows
 // [align(psum[e-1]), align(psum[e])), valid rows up to psum[e]; else run e of an m_indices layout
-// (csrc/status.hip, m_indices_runs: runs[0] = count, then first row and group id per run), rows up
-// to the next run's first row (the last: m_total), every row valid as far as the tile goes (rows
-// of another id are zeroed by the epilogue).
+// (csrc/status.hip, m_indices_runs: runs[0] = count, then first row, group id and valid end per
+// run), rows up to the next run's first row (the last: m_total), valid up to the run's valid end
+// (rows of another id before it are zeroed by the epilogue).
 struct Segment {
     int start, end, valid, group;
 };

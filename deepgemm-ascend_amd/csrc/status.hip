@@ -58,22 +58,29 @@ uint32_t* status_words_if_ready() {
 
 // m_indices of an M-grouped contiguous GEMM: every `alignment`-row block must hold one group id
 // (0 <= id < num_groups) on a prefix of its rows and padding (< 0) on the rest -- the layout the
-// grouped kernel's per-tile group lookup relies on.  Thread r checks row r against row r - 1.
+// grouped kernel's per-tile group lookup relies on.  Thread r checks row r against row r - 1 (with
+// `status`), and (with `blk_end`) a row r that ends its id's rows within its block records r + 1 as
+// the block's valid end (the run table's input; for a checked layout one row per block does).
 __global__ __launch_bounds__(256) void check_m_indices_kernel(const int32_t* idx, int m, int alignment,
-                                                              int num_groups, uint32_t* status) {
+                                                              int num_groups, uint32_t* status, int32_t* blk_end) {
     const int r = blockIdx.x * 256 + threadIdx.x;
     if (r >= m) return;
     const int v = idx[r];
-    bool bad = v >= num_groups;
-    if (v >= 0 && r % alignment != 0) bad = bad || idx[r - 1] != v;
-    if (bad) status[1] = 1u;
+    if (status != nullptr) {
+        bool bad = v >= num_groups;
+        if (v >= 0 && r % alignment != 0) bad = bad || idx[r - 1] != v;
+        if (bad) status[1] = 1u;
+    }
+    if (blk_end != nullptr && v >= 0 && (r + 1 == m || (r + 1) % alignment == 0 || idx[r + 1] != v))
+        blk_end[r / alignment] = r + 1;
 }
 
-int check_m_indices(const int32_t* idx, int m, int alignment, int num_groups, hipStream_t st, bool may_alloc) {
+int check_m_indices(const int32_t* idx, int m, int alignment, int num_groups, hipStream_t st, bool may_alloc,
+                    int32_t* blk_end) {
     uint32_t* status = may_alloc ? status_words() : status_words_if_ready();
-    if (status == nullptr || m <= 0) return DG_OK;
+    if ((status == nullptr && blk_end == nullptr) || m <= 0) return DG_OK;
     hipLaunchKernelGGL(check_m_indices_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, idx, m, alignment,
-                       num_groups, status);
+                       num_groups, status, blk_end);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         dg_set_error(hipGetErrorString(e));
@@ -84,14 +91,14 @@ int check_m_indices(const int32_t* idx, int m, int alignment, int num_groups, hi
 
 // Runs of an m_indices layout: maximal sequences of `alignment`-row blocks whose first rows carry
 // the same group id (-1: padding).  Output: runs[0] = the number of runs, then (first row, group,
-// valid end) per run; a run ends where the next begins (the last at m), and its valid end is one past
-// the last row of its final block that carries the run's group (the padding rows after it are neither
-// loaded nor multiplied by the anchored tiles; rows before it keep their per-row id check).  One
-// workgroup: each thread takes a contiguous span of blocks, counts the runs starting there, and a
+// valid end) per run; a run ends where the next begins (the last at m), and its valid end is where the
+// run's group ends in its final block (`blk_end`, from check_m_indices_kernel; the padding rows after it
+// are neither loaded nor multiplied by the anchored tiles; rows before it keep their per-row id check).
+// One workgroup: each thread takes a contiguous span of blocks, counts the runs starting there, and a
 // workgroup prefix sum places them.
 constexpr int kRunThreads = 1024;
 __global__ __launch_bounds__(kRunThreads) void m_indices_runs_kernel(const int32_t* idx, int m, int alignment,
-                                                                    int32_t* runs) {
+                                                                    int32_t* runs, const int32_t* blk_end) {
     __shared__ int counts[kRunThreads];
     const int tid = threadIdx.x;
     const int nblk = (m + alignment - 1) / alignment;
@@ -118,16 +125,21 @@ __global__ __launch_bounds__(kRunThreads) void m_indices_runs_kernel(const int32
         }
         // the run's final block (the next block starts another run, or there is none): its valid end
         if (b + 1 == nblk || idx[(int64_t)(b + 1) * alignment] != g) {
-            int e = min(m, (b + 1) * alignment);
-            while (e > b * alignment + 1 && idx[e - 1] != g) --e;
+            const int lo = b * alignment + 1, hi = min(m, (b + 1) * alignment);
+            int e = hi;
+            if (g >= 0) {
+                e = min(hi, max(lo, blk_end[b]));   // (clamped: an unchecked layout may leave any value)
+            } else {
+                while (e > lo && idx[e - 1] != g) --e;   // (padding runs: no block end recorded)
+            }
             runs[3 * r] = e;   // (run r - 1, the one this block belongs to)
         }
     }
     if (tid == kRunThreads - 1) runs[0] = counts[tid];
 }
 
-int m_indices_runs(const int32_t* idx, int m, int alignment, int32_t* runs, hipStream_t st) {
-    hipLaunchKernelGGL(m_indices_runs_kernel, dim3(1), dim3(kRunThreads), 0, st, idx, m, alignment, runs);
+int m_indices_runs(const int32_t* idx, int m, int alignment, int32_t* runs, const int32_t* blk_end, hipStream_t st) {
+    hipLaunchKernelGGL(m_indices_runs_kernel, dim3(1), dim3(kRunThreads), 0, st, idx, m, alignment, runs, blk_end);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         dg_set_error(hipGetErrorString(e));
