@@ -266,6 +266,17 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
             rows_env.rnb = 2;
             rows_env.rsplit = (int)std::max<int64_t>(2, std::min<int64_t>(4, cus / strips2));
             rows_env.rreduce = 1;
+            // From K = 8192 over wide N, 128-column strips (half the A traffic again; cold event us, 64-column
+            // plan in brackets): e4m3 128x7168x16384 44.6 (48.4), 96x7168x16384 39.5 (44.2), 128x7168x8192 30.2
+            // (31.7), but 128x6144x12288 40.5 (39.4); bf16 128x7168x16384 63.2 (80.6), 128x6144x12288 47.8
+            // (59.4), 128x3072x16384 38.0 (43.7), 128x7168x8192 43.8 (45.0), 128x4096x16384 level; FP8 x FP4
+            // 128x7168x16384 38.9 (44.0), 96x7168x16384 36.1 (42.5), 128x6144x12288 35.0 (36.2), but
+            // 128x4096x16384 30.2 (29.8)
+            const bool wide128 = a.k >= 8192 && (a.kind == kBF16 || (a.kind == kFP8FP4 ? a.n >= 6144 : a.n >= 7168));
+            if (wide128) {
+                rows_env.rnb = 4;
+                rows_env.rsplit = 0;   // (K split to fill the CUs, as measured)
+            }
         } else if (a.k > 8192) {
             rows_env.rows = -1;   // (longer K otherwise stays on the skinny kernel)
         } else if (a.m > 80) {

@@ -171,11 +171,12 @@ def test_launch_plan_without_device(lib):
     long_k = _lib.LaunchInfo()
     assert lib.dg_launch_plan(_plan_args(128, 7168, 16384, 0), ctypes.byref(long_k)) == 0, lib.dg_last_error()
     assert long_k.skinny == 1
-    # (with a workspace the wide two-launch plan takes it, up to K = 16384)
+    # (with a workspace the wide two-launch plan takes it, up to K = 16384; from K = 8192 over N >= 7168 with
+    # 128-column strips)
     long_args = _plan_args(128, 7168, 16384, 0)
     long_args.library_workspace = 1
     assert lib.dg_launch_plan(long_args, ctypes.byref(long_k)) == 0, lib.dg_last_error()
-    assert long_k.skinny == 2 and long_k.block_n == 64 and long_k.split_reduce == 1
+    assert long_k.skinny == 2 and long_k.block_n == 128 and long_k.split_reduce == 1   # (128-column strips)
     # e4m3 M <= 64 with K > 8192 over many columns: 64 x 128 shared-ring tiles, two launches
     m64 = _lib.LaunchInfo()
     m64_args = _plan_args(64, 7168, 16384, 0)

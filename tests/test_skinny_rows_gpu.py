@@ -154,8 +154,9 @@ def test_rows_default_plan_vs_tile_kernel(monkeypatch, m, n, k):
     if n <= 8192:
         info = deep_gemm.launch_plan(m, n, k)
         wide = k > 4096 and n >= 3072   # 64-column strips, partials summed by the second launch
+        wide128 = wide and k >= 8192 and n >= 7168   # (e4m3: 128-column strips from K = 8192 over N >= 7168)
         # (64 x 64 tiles from M = 81 on, else 128-row strips: 128 x 64 where wide, 128 x 32 otherwise)
-        bm, bn = (128, 64) if wide else (64, 64) if m > 80 else (128, 32)
+        bm, bn = (128, 128) if wide128 else (128, 64) if wide else (64, 64) if m > 80 else (128, 32)
         assert info['skinny'] == 2 and (info['block_m'], info['block_n']) == (bm, bn), info
         assert info['split_reduce'] == int(wide or (m > 80 and info['split_k'] > 2)), info
         assert info['split_k'] > 1 or not wide, info
@@ -261,7 +262,8 @@ def test_rows_split_reduce_launch_bit_exact(monkeypatch, cfg, out):
 
 
 @pytest.mark.parametrize('kind', ['bf16', 'fp4'])
-@pytest.mark.parametrize('m,n,k', [(128, 2112, 7168), (128, 4096, 7168), (128, 7168, 2048), (96, 7168, 4096), (72, 1000, 2048)])
+@pytest.mark.parametrize('m,n,k', [(128, 2112, 7168), (128, 4096, 7168), (128, 7168, 2048), (96, 7168, 4096), (72, 1000, 2048),
+                                   (96, 7168, 12288), (128, 3072, 8192), (128, 7168, 16384)])
 def test_rows_default_plan_bf16_fp4(monkeypatch, kind, m, n, k):
     """bf16 and FP8 x FP4 decode shapes on their default plans (the shared-ring kernel where it measured
     ahead, the skinny kernel elsewhere) agree with the oracle and with the tile kernel."""
@@ -289,7 +291,7 @@ def test_rows_default_plan_bf16_fp4(monkeypatch, kind, m, n, k):
     assert calc_diff(d.cpu(), d0.cpu()) < 1e-6
 
 
-@pytest.mark.parametrize('m,n,k', [(100, 2112, 2048), (128, 4096, 7168), (97, 3000, 5000)])
+@pytest.mark.parametrize('m,n,k', [(100, 2112, 2048), (128, 4096, 7168), (97, 3000, 5000), (128, 7168, 8192)])
 def test_rows_default_plan_bmm(m, n, k):
     """Batched launches on the default decode plans (64 x 64 tiles with M in two row blocks, or the 128 x 64
     two-launch plan): every batch against the oracle."""
