@@ -271,8 +271,10 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
             // (31.7), but 128x6144x12288 40.5 (39.4); bf16 128x7168x16384 63.2 (80.6), 128x6144x12288 47.8
             // (59.4), 128x3072x16384 38.0 (43.7), 128x7168x8192 43.8 (45.0), 128x4096x16384 level; FP8 x FP4
             // 128x7168x16384 38.9 (44.0), 96x7168x16384 36.1 (42.5), 128x6144x12288 35.0 (36.2), but
-            // 128x4096x16384 30.2 (29.8)
-            const bool wide128 = a.k >= 8192 && (a.kind == kBF16 || (a.kind == kFP8FP4 ? a.n >= 6144 : a.n >= 7168));
+            // 128x4096x16384 30.2 (29.8); below K = 8192 only bf16 over N = 7168 gains (128x7168x7168 38.2
+            // (41.4); 128x4096x7168 29.5 (28.6))
+            const bool wide128 = a.k >= 8192 ? (a.kind == kBF16 || (a.kind == kFP8FP4 ? a.n >= 6144 : a.n >= 7168))
+                                             : a.kind == kBF16 && a.n >= 7168;
             if (wide128) {
                 rows_env.rnb = 4;
                 rows_env.rsplit = 0;   // (K split to fill the CUs, as measured)
