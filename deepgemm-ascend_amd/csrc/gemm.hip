@@ -278,7 +278,18 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
             if (wide128) {
                 rows_env.rnb = 4;
                 rows_env.rsplit = 0;   // (K split to fill the CUs, as measured)
+            } else if (a.kind == kFP8FP4 && a.n <= 4096 && a.k <= 8192) {
+                // FP8 x FP4 at mid K: 64 x 128 tiles with M in two row blocks, split 4 (cold event us, 128 x 64
+                // plan in brackets: 128x4096x7168 20.6 (21.4), 128x3072x7168 19.5 (20.1))
+                rows_env.rmt = 2; rows_env.rnb = 4; rows_env.rsplit = 4;
             }
+        } else if (allow_split && a.kind == kBF16 && a.k >= 6144 && a.k <= 8192 && a.n >= 2048 && a.n < 3072 &&
+                   6 * strips2 <= 2 * (int64_t)cus) {
+            // bf16 over about 2112 columns: 128 x 64 tiles split 6 ways, summed by the second launch (cold event
+            // us, 64 x 64 plan in brackets: 128x2112x7168 22.6 (23.7), 96x2112x7168 20.6 (23.0))
+            rows_env.rnb = 2;
+            rows_env.rsplit = 6;
+            rows_env.rreduce = 1;
         } else if (a.k > 8192) {
             rows_env.rows = -1;   // (longer K otherwise stays on the skinny kernel)
         } else if (a.m > 80) {
