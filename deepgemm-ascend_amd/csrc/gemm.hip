@@ -301,6 +301,15 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
             // where the second block holds few rows (65x4096x1024 13.3 vs 12.5: B read twice for one row).
             rows_env.rmt = 2; rows_env.rnb = 2;
             rows_env.rreduce = 2;   // (second launch when the plan splits K three ways or more)
+            // At short K the tiles alone fill the CUs well enough: a two-way split (its last workgroup summing
+            // the partials) measured behind the unsplit plan (cold event us, split plan in brackets): e4m3
+            // 128x4096x2048 13.1 (16.1), 128x3072x2048 13.0 (15.1), 128x2112x2048 12.8 (14.3), 96x4096x3072
+            // 15.9 (16.8); FP8 x FP4 12.2 (15.5), 12.0 (14.6), 12.0 (13.8), 128x4096x4096 17.3 (18.2); bf16
+            // 128x4096x2048 16.4 (17.7), 128x3072x2048 16.3 (16.8), but 128x2112x2048 16.0 (15.0), and
+            // 128x2112x4096 splits better for every kind (e4m3 16.0 vs 18.7)
+            const bool short_k = a.kind == kBF16 ? a.k <= 2048 && a.n >= 3072
+                                                 : (a.k <= 3072 && a.n >= 2048) || (a.kind == kFP8FP4 && a.k <= 4096 && a.n >= 4096);
+            if (short_k) rows_env.rsplit = 1;
             // bf16 rows of 8 KB and more in an unsplit plan stay on the skinny kernel (128x7168x4096
             // 37.1 vs 29.1 us; split or shorter rows gain: 128x4096x4096 23.2 vs 24.2, 128x7168x3072
             // 23.0 vs 24.9, 128x2112x7168 24.0 vs 26.2)
