@@ -378,10 +378,12 @@ bool skinny_kernel_plan(const dg_gemm_args& a, int cus, bool allow_split, const 
     if (allow_split && strips <= kMaxSplitTiles) {
         if (env.mode == 1 && env.split > 0) sp = env.split;
         else sp = (int)std::min<int64_t>(std::max<int64_t>(1, cus / strips), std::max(1, nk64 / (4 * nw)));
-        // (past 16 rows of A, K <= 2048 stays unsplit: cold event us, split 2 in brackets: e4m3 64x4096x2048
-        // 10.9 (12.8), 64x3072x2048 10.8 (12.3), 64x2112x2048 10.6 (11.9), 32x4096x2048 10.2 (10.8); bf16
-        // 64x4096x2048 13.4 (14.2), 64x3072x2048 13.1 (13.5), 64x2112x2048 13.1 (12.8))
-        if (env.mode != 1 && a.m > 16 && nk64 <= 32) sp = 1;
+        // (K <= 2048 stays unsplit, e4m3 up to K = 3072: cold event us, split 2 in brackets: e4m3 64x4096x2048
+        // 10.9 (12.8), 64x3072x2048 10.8 (12.3), 64x2112x2048 10.6 (11.9), 32x4096x2048 10.2 (10.8),
+        // 16x4096x2048 9.0 (10.3), 1x4096x2048 8.6 (10.3), 1x3072x3072 9.7 (10.9), 16x2112x3072 10.0 (10.5);
+        // bf16 64x4096x2048 13.4 (14.2), 16x4096x2048 10.6 (11.3), 1x4096x2048 10.3 (11.2), 64x2112x2048 13.1
+        // (12.8), but 16x2112x3072 12.7 (11.4))
+        if (env.mode != 1 && (nk64 <= 32 || (a.kind == kFP8FP8 && nk64 <= 48))) sp = 1;
         sp = std::max(1, std::min(sp, std::min(16, nk64)));
     }
     const int ss = ceil_div(nk64, sp);

@@ -55,7 +55,7 @@ def test_noalloc_matches_dg_gemm_on_two_calls():
     lib = _lib.load()
     # a split-K decode plan, then a smaller one (the array keeps the first call's contents)
     # (128 x 2112 x 7168 takes the shared-ring decode kernel, the others the skinny kernel)
-    for (m, n, k), seed in (((128, 2112, 7168), 5), ((64, 4096, 7168), 1), ((1, 2112, 2048), 2)):
+    for (m, n, k), seed in (((128, 2112, 7168), 5), ((64, 4096, 7168), 1), ((8, 2112, 4096), 2)):
         args, keep, ref = _args(m, n, k, seed)
         info = _lib.LaunchInfo()
         args.workspace, args.workspace_bytes = 1, 1 << 40   # plan as for a caller with a workspace
